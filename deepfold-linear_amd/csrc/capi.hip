@@ -1,0 +1,215 @@
+// C-ABI entry points (include/dfl_amd.h): argument checking, work split,
+// workspace layout and launches.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/dfl_amd.h"
+#include "sinkhorn_args.h"
+
+namespace dfl {
+size_t sinkhorn_fwd_lds_bytes(int N, int DP, int elem, int G);
+hipError_t launch_sinkhorn_fwd(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
+                               bool coop);
+size_t sinkhorn_bwd_lds_bytes(int N, int DP, int elem, int G);
+hipError_t launch_sinkhorn_bwd(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
+                               bool coop);
+hipError_t launch_sinkhorn_bwd_finalize(const SinkBwdArgs& a, float* dx, float* dpw, float* dw,
+                                        hipStream_t stream);
+}  // namespace dfl
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return -1;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_err = std::string(what) + ": " + hipGetErrorString(e);
+  return (int)e;
+}
+
+std::atomic<uint32_t> g_salt{1};
+uint32_t next_salt() {
+  uint32_t s = g_salt.fetch_add(1) & 0xfffffu;
+  if (s == 0) s = g_salt.fetch_add(1) & 0xfffffu;
+  return s == 0 ? 1u : s;
+}
+
+constexpr size_t WS_HEADER = 256;  // error word + last salt, cache-line padded
+
+struct WsHeader {
+  uint32_t err;
+  uint32_t pad[63];
+};
+
+int cu_count() {
+  static int cached = -1;
+  if (cached < 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cached = c;
+  }
+  return cached;
+}
+
+size_t np32(int N) { return (size_t)((N + 31) / 32) * 32; }
+
+// Exchange words per (b,h): u and v for the forward; four vectors for the backward.
+size_t xch_words(int B, int H, int N) { return (size_t)B * H * 4 * np32(N); }
+
+int head_dim_pad(int d) { return d <= 32 ? 32 : (d <= 64 ? 64 : -1); }
+
+// Workgroups per (b,h): enough to cover the chip, at most one per 16-row tile.
+int group_size(int B, int H, int N) {
+  const int bh = B * H;
+  int G = cu_count() / bh;
+  if (G < 1) G = 1;
+  const int tiles = (N + 15) / 16;
+  if (G > tiles) G = tiles;
+  return G;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dfl_last_error(void) { return g_err.c_str(); }
+
+const char* dfl_version(void) { return "deepfold_amd 0.1.0 (gfx950)"; }
+
+size_t dfl_sinkhorn_workspace_size(int B, int H, int N) {
+  if (B <= 0 || H <= 0 || N <= 0) return 0;
+  const int G = group_size(B, H, N);
+  size_t bytes = WS_HEADER + xch_words(B, H, N) * 8;
+  // backward partials: dx (B,H,N,3), dpw (B*H*G,68), dw (B*H*G)
+  bytes += (size_t)B * H * N * 3 * 4 + (size_t)B * H * G * 69 * 4;
+  return (bytes + 255) / 256 * 256;
+}
+
+int dfl_workspace_error(const void* workspace, void* stream) {
+  if (!workspace) return fail("workspace is NULL");
+  uint32_t words[2] = {0, 0};
+  hipError_t e = hipMemcpyAsync(words, workspace, 8, hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dfl_workspace_error copy");
+  e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dfl_workspace_error sync");
+  // word 0: (salt << 12) | code of the call that raised it; word 1: salt of the
+  // latest call that ran on this workspace (written by its first workgroup).
+  if ((words[0] >> 12) == words[1]) return (int)(words[0] & 0xfffu);
+  return 0;
+}
+
+int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_BF16 && p->dtype != DFL_F32) return fail("dtype must be DFL_BF16 or DFL_F32");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0 || p->d <= 0) return fail("B, H, N, d must be positive");
+  const int DP = head_dim_pad(p->d);
+  if (DP < 0) return fail("head dim d=%d > 64 is not supported", p->d);
+  if (p->K_iter < 0 || p->K_iter > 2000) return fail("K_iter=%d outside [0, 2000]", p->K_iter);
+  if (!p->q || !p->k || !p->v || !p->eps || !p->log_mu || !p->log_nu) return fail("required input is NULL");
+  if (!p->o_flat || !p->x_centroid || !p->log_u || !p->log_v || !p->o_avg || !p->log_z || !p->col_lse)
+    return fail("output pointer is NULL");
+  if (p->stride_n < p->d) return fail("stride_n must be >= d (unit inner stride)");
+  if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
+  const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  const int G = group_size(p->B, p->H, p->N);
+  const int elem = p->dtype == DFL_BF16 ? 2 : 4;
+  const size_t lds = dfl::sinkhorn_fwd_lds_bytes(p->N, DP, elem, G);
+  if (lds > 160 * 1024)
+    return fail("N=%d, d=%d exceeds the LDS-resident limit of this build (needs %zu bytes)", p->N, p->d, lds);
+
+  dfl::SinkFwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = p->q; a.k = p->k; a.v = p->v; a.g = p->g;
+  a.sb = p->stride_b; a.sh = p->stride_h; a.sn = p->stride_n;
+  a.x = p->x_res; a.pos_w = p->pos_weight; a.bins = p->pos_bins;
+  a.eps = p->eps; a.w_dist = p->w_dist; a.log_mu = p->log_mu; a.log_nu = p->log_nu;
+  a.u_init = p->log_u_init; a.v_init = p->log_v_init; a.mask = p->mask;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d;
+  a.K_iter = p->K_iter; a.lam = p->lam; a.r0 = p->r_0;
+  a.o_flat = p->o_flat; a.x_centroid = p->x_centroid; a.log_u = p->log_u; a.log_v = p->log_v;
+  a.o_avg = p->o_avg; a.log_z = p->log_z; a.col_lse = p->col_lse;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
+  a.G = G;
+  a.salt = next_salt();
+  const bool coop = G > 1;
+  hipError_t e = dfl::launch_sinkhorn_fwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  if (e != hipSuccess) return hip_fail(e, "sinkhorn forward launch");
+  return 0;
+}
+
+int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_BF16 && p->dtype != DFL_F32) return fail("dtype must be DFL_BF16 or DFL_F32");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0 || p->d <= 0) return fail("B, H, N, d must be positive");
+  const int DP = head_dim_pad(p->d);
+  if (DP < 0) return fail("head dim d=%d > 64 is not supported", p->d);
+  if (p->solver != DFL_IFT_FIXED_POINT && p->solver != DFL_IFT_CG) return fail("unknown solver %d", p->solver);
+  if (p->mode != DFL_IFT_REFERENCE && p->mode != DFL_IFT_ANALYTIC) return fail("unknown mode %d", p->mode);
+  if (p->iters < 0 || p->iters > 1000) return fail("iters=%d outside [0, 1000]", p->iters);
+  if (!p->q || !p->k || !p->v || !p->eps || !p->log_u || !p->log_v || !p->log_z || !p->col_lse || !p->o_avg ||
+      !p->x_centroid || !p->grad_o)
+    return fail("required input is NULL");
+  if (!p->dq || !p->dk || !p->dv || !p->dg || !p->dlog_mu || !p->dlog_nu || !p->dx_res || !p->dpos_weight ||
+      !p->dw_dist)
+    return fail("output pointer is NULL");
+  if (p->stride_n < p->d) return fail("stride_n must be >= d (unit inner stride)");
+  if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
+  const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  const int G = group_size(p->B, p->H, p->N);
+  const int elem = p->dtype == DFL_BF16 ? 2 : 4;
+  const size_t lds = dfl::sinkhorn_bwd_lds_bytes(p->N, DP, elem, G);
+  if (lds > 160 * 1024)
+    return fail("N=%d, d=%d exceeds the LDS-resident limit of this build (needs %zu bytes)", p->N, p->d, lds);
+
+  dfl::SinkBwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = p->q; a.k = p->k; a.v = p->v; a.g = p->g;
+  a.sb = p->stride_b; a.sh = p->stride_h; a.sn = p->stride_n;
+  a.x = p->x_res; a.pos_w = p->pos_weight; a.bins = p->pos_bins;
+  a.eps = p->eps; a.w_dist = p->w_dist; a.mask = p->mask;
+  a.log_u = p->log_u; a.log_v = p->log_v; a.log_z = p->log_z; a.col_lse = p->col_lse;
+  a.o_avg = p->o_avg; a.x_centroid = p->x_centroid; a.grad_o = p->grad_o; a.grad_xc = p->grad_xc;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d;
+  a.lam = p->lam; a.r0 = p->r_0;
+  a.solver = p->solver; a.iters = p->iters; a.mode = p->mode; a.cg_rtol = p->cg_rtol;
+  a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dg = p->dg;
+  a.dlog_mu = p->dlog_mu; a.dlog_nu = p->dlog_nu;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
+  float* parts = reinterpret_cast<float*>(ws + WS_HEADER + xch_words(p->B, p->H, p->N) * 8);
+  a.dx_part = parts;
+  a.dpw_part = parts + (size_t)p->B * p->H * p->N * 3;
+  a.dw_part = a.dpw_part + (size_t)p->B * p->H * G * 68;
+  a.G = G;
+  a.salt = next_salt();
+  const bool coop = G > 1;
+  hipError_t e = dfl::launch_sinkhorn_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  if (e != hipSuccess) return hip_fail(e, "sinkhorn backward launch");
+  e = dfl::launch_sinkhorn_bwd_finalize(a, p->dx_res, p->dpos_weight, p->dw_dist, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "sinkhorn backward finalize launch");
+  return 0;
+}
+
+}  // extern "C"

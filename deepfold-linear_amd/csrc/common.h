@@ -1,0 +1,200 @@
+// Shared device-side building blocks for the deepfold_amd HIP kernels (gfx950).
+//
+//  * MFMA fragment traits for bf16 (v_mfma_f32_16x16x32_bf16) and fp32
+//    (v_mfma_f32_16x16x4_f32) tiles with one unified LDS fragment layout.
+//  * Tagged device-scope exchange: 64-bit words {tag, float} written and polled
+//    with relaxed agent-scope atomics.  Each word carries its own round tag, so no
+//    fences are needed (agent-scope acquire/release fences cost ~8 us each on
+//    MI355X because they write back / invalidate the whole L2).
+//  * Error flag + bounded spins so every wave of a persistent kernel terminates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dfl {
+
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+constexpr float NEG_BIG = -1.0e30f;  // masked logit (log2 units); exp2 -> 0
+
+constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------------------
+// conversions
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------
+// MFMA traits.
+//
+// A 16x16 output tile D[m][n] lives in 4 fp32 registers per lane:
+//   lane l holds D[4*(l/16) + r][l % 16], r = 0..3.
+// QK-type products D = A * B^T with A rows (m) and B rows (n) taken from LDS
+// arrays stored row-major [row][DP] (DP = padded head dim, multiple of 32 for
+// bf16 and of 4 for fp32).  Both operands use the same k permutation: lane
+// group g = l/16 owns the contiguous column run [g*DP/4, (g+1)*DP/4) of its row
+// (row = l % 16), which is loaded with one vector read.
+//
+// PV-type products O[i][c] += sum_j P[i][j] V[j][c] consume P straight from the
+// QK-type accumulator layout of two consecutive 16-row streamed tiles; V comes
+// from an LDS array stored transposed [c][j].
+template <typename T, int DP> struct Mfma;
+
+template <int DP> struct Mfma<bf16, DP> {
+  static_assert(DP % 32 == 0, "bf16 head dim must be padded to 32");
+  static constexpr int KSTEPS = DP / 32;
+  static constexpr int RUN = DP / 4;  // elements per lane per row
+  struct Frag { bf16x8 v[KSTEPS]; };
+  __device__ static __forceinline__ void load(Frag& f, const bf16* row_base, int lane) {
+    // row_base points at row (l%16) of the tile already
+    const bf16* p = row_base + (lane >> 4) * RUN;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) f.v[s] = *reinterpret_cast<const bf16x8*>(p + 8 * s);
+  }
+  // run: the RUN elements this lane owns, in column order
+  __device__ static __forceinline__ void from_run(Frag& f, const bf16* run) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f.v[s][e] = run[8 * s + e];
+  }
+  __device__ static __forceinline__ f32x4 qk(const Frag& a, const Frag& b, f32x4 c) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v[s], b.v[s], c, 0, 0, 0);
+    return c;
+  }
+  // P: two tiles of accumulator values p0 (streamed rows 0..15), p1 (16..31).
+  // vt_row: LDS pointer to row (c0 + l%16) of the transposed V array, at column j0.
+  __device__ static __forceinline__ f32x4 pv(const f32x4& p0, const f32x4& p1, const bf16* vt_row, int lane,
+                                             f32x4 acc) {
+    const int g = lane >> 4;
+    bf16x8 a, b;
+    a[0] = (bf16)p0[0]; a[1] = (bf16)p0[1]; a[2] = (bf16)p0[2]; a[3] = (bf16)p0[3];
+    a[4] = (bf16)p1[0]; a[5] = (bf16)p1[1]; a[6] = (bf16)p1[2]; a[7] = (bf16)p1[3];
+    bf16x4 lo = *reinterpret_cast<const bf16x4*>(vt_row + 4 * g);
+    bf16x4 hi = *reinterpret_cast<const bf16x4*>(vt_row + 16 + 4 * g);
+    b[0] = lo[0]; b[1] = lo[1]; b[2] = lo[2]; b[3] = lo[3];
+    b[4] = hi[0]; b[5] = hi[1]; b[6] = hi[2]; b[7] = hi[3];
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+};
+
+template <int DP> struct Mfma<float, DP> {
+  static_assert(DP % 4 == 0, "fp32 head dim must be padded to 4");
+  static constexpr int KSTEPS = DP / 4;
+  static constexpr int RUN = DP / 4;
+  struct Frag { float v[KSTEPS]; };
+  __device__ static __forceinline__ void load(Frag& f, const float* row_base, int lane) {
+    const float* p = row_base + (lane >> 4) * RUN;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) f.v[s] = p[s];
+  }
+  __device__ static __forceinline__ void from_run(Frag& f, const float* run) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) f.v[s] = run[s];
+  }
+  __device__ static __forceinline__ f32x4 qk(const Frag& a, const Frag& b, f32x4 c) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[s], b.v[s], c, 0, 0, 0);
+    return c;
+  }
+  __device__ static __forceinline__ f32x4 pv(const f32x4& p0, const f32x4& p1, const float* vt_row, int lane,
+                                             f32x4 acc) {
+    const int g = lane >> 4;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(vt_row + 4 * g);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(vt_row + 16 + 4 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p0[r], lo[r], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[r], hi[r], acc, 0, 0, 0);
+    return acc;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Lane reductions across the 4 lane groups (l/16) of a wave that hold the same
+// accumulator column.
+__device__ __forceinline__ float sum_groups(float x) {
+  x += __shfl_xor(x, 16, WAVE);
+  x += __shfl_xor(x, 32, WAVE);
+  return x;
+}
+__device__ __forceinline__ float max_groups(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, WAVE));
+  x = fmaxf(x, __shfl_xor(x, 32, WAVE));
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// Error flag and tagged exchange.
+constexpr uint32_t SPIN_LIMIT = 1u << 22;  // ~2-4 s of polling
+
+// The error word holds (salt << 12) | code for the call that raised it; a word
+// carrying another call's salt is stale and ignored.
+__device__ __forceinline__ void raise_error(uint32_t* err, uint32_t salt, uint32_t code) {
+  __hip_atomic_store(err, (salt << 12) | (code & 0xfffu), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool error_raised(const uint32_t* err, uint32_t salt) {
+  const uint32_t e = __hip_atomic_load(const_cast<uint32_t*>(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (e >> 12) == salt && (e & 0xfffu) != 0u;
+}
+
+__device__ __forceinline__ void xch_put(uint64_t* word, float v, uint32_t tag) {
+  const uint64_t w = ((uint64_t)__float_as_uint(v) << 32) | (uint64_t)tag;
+  __hip_atomic_store(word, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// All threads of the block cooperatively wait for words [0, n) of `buf` to carry
+// `tag`, writing value * scale into dst[] (LDS).  Returns false (uniformly across
+// the block) if the error flag is raised or the spin limit is hit.
+template <int NT>
+__device__ bool xch_gather(const uint64_t* buf, int n, uint32_t tag, float* dst, float scale,
+                           uint32_t* err, int* s_flag) {
+  const uint32_t salt = tag >> 12;
+  const int t = threadIdx.x;
+  bool ok = true;
+  for (int base = 0; base < n && ok; base += 8 * NT) {
+    uint32_t pending = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (base + t + k * NT < n) pending |= 1u << k;
+    uint32_t spins = 0;
+    while (pending) {
+      uint64_t w[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (pending & (1u << k))
+          w[k] = __hip_atomic_load(const_cast<uint64_t*>(buf + base + t + k * NT), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if ((pending & (1u << k)) && (uint32_t)w[k] == tag) {
+          dst[base + t + k * NT] = __uint_as_float((uint32_t)(w[k] >> 32)) * scale;
+          pending &= ~(1u << k);
+        }
+      }
+      if (pending) {
+        if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); ok = false; break; }
+        if ((spins & 255u) == 0u && error_raised(err, salt)) { ok = false; break; }
+      }
+    }
+  }
+  if (!ok) *s_flag = 1;
+  __syncthreads();
+  const bool all_ok = (*s_flag == 0);
+  return all_ok;
+}
+
+}  // namespace dfl

@@ -1,0 +1,86 @@
+// Argument blocks shared by the Sinkhorn kernels and the C-ABI layer.
+#pragma once
+#include <stdint.h>
+
+namespace dfl {
+
+// Forward (flash_sinkhorn_attn.py:77-244 semantics).
+struct SinkFwdArgs {
+  const void* q;  // (B,H,N,d) bf16 or fp32, element strides sb/sh/sn, unit inner stride
+  const void* k;
+  const void* v;
+  const void* g;  // gate logits, same layout (may be null: gate treated as +inf -> sigma = 1)
+  long long sb, sh, sn;
+  const float* x;       // (B,N,3) contiguous or null (zeros)
+  const float* pos_w;   // (H,68) or null
+  const int* bins;      // (B,N,N) int32 contiguous or null
+  const float* eps;     // (H,)
+  const float* w_dist;  // (H,) or null
+  const float* log_mu;  // (B,H,N)
+  const float* log_nu;  // (B,H,N)
+  const float* u_init;  // (B,H,N) or null
+  const float* v_init;  // (B,H,N) or null
+  const float* mask;    // (B,N) or null
+  int B, H, N, d;
+  int K_iter;
+  float lam, r0;
+  // outputs (caller zero-initialises; padded positions are left untouched)
+  float* o_flat;      // (B,N,H*d)
+  float* x_centroid;  // (B,H,N,3)
+  float* log_u;       // (B,H,N)
+  float* log_v;       // (B,H,N)
+  float* o_avg;       // (B,H,N,d)  saved for the backward
+  float* log_z;       // (B,H,N)    LSE_j(u_i + L_ij + v_j)
+  float* col_lse;     // (B,H,N)    LSE_i(L_ij + u_i) of the last column update
+  // workspace
+  uint64_t* xch;  // B*H*2*Np exchange words
+  uint32_t* err;  // error word
+  int G;          // workgroups per (b,h)
+  uint32_t salt;  // 20-bit call salt for exchange tags
+};
+
+// Backward (flash_sinkhorn_attn.py:246-667 semantics, plus analytic mode / CG).
+struct SinkBwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  long long sb, sh, sn;
+  const float* x;
+  const float* pos_w;
+  const int* bins;
+  const float* eps;
+  const float* w_dist;
+  const float* mask;
+  const float* log_u;     // (B,H,N) forward outputs
+  const float* log_v;
+  const float* log_z;     // (B,H,N)
+  const float* col_lse;   // (B,H,N)
+  const float* o_avg;     // (B,H,N,d)
+  const float* x_centroid;  // (B,H,N,3)
+  const float* grad_o;    // (B,N,H*d) fp32
+  const float* grad_xc;   // (B,H,N,3) fp32 or null
+  int B, H, N, d;
+  float lam, r0;
+  int solver;   // 0 = fixed point (reference Gauss-Seidel), 1 = CG
+  int iters;    // fixed-point sweeps or CG iterations
+  int mode;     // 0 = reference signs, 1 = analytic adjoint
+  float cg_rtol;  // CG early stop on ||r|| <= rtol ||b|| (0 = run all iterations)
+  // outputs (caller zero-initialises)
+  float* dq;        // (B,H,N,d)
+  float* dk;
+  float* dv;
+  float* dg;
+  float* dlog_mu;   // (B,H,N)
+  float* dlog_nu;
+  float* dx_part;   // (B,H,N,3) per-head partials, summed over h by the finaliser
+  float* dpw_part;  // (B*H*G, 68) per-workgroup partials
+  float* dw_part;   // (B*H*G) per-workgroup partials
+  // workspace
+  uint64_t* xch;  // B*H*4*Np exchange words
+  uint32_t* err;
+  int G;
+  uint32_t salt;
+};
+
+}  // namespace dfl

@@ -1,0 +1,154 @@
+"""ctypes binding of libdfl_amd.so (the C ABI declared in include/dfl_amd.h).
+
+The library is built in-tree by ``deepfold-linear_amd/build_lib.py`` (``__graft_entry__.build()``).
+There is no CPU or PyTorch fallback: every public op of this package raises if the
+library is missing or the tensors are not on a ROCm device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdfl_amd.so")
+
+DFL_BF16 = 0
+DFL_F32 = 1
+DFL_IFT_FIXED_POINT = 0
+DFL_IFT_CG = 1
+DFL_IFT_REFERENCE = 0
+DFL_IFT_ANALYTIC = 1
+
+_lock = threading.Lock()
+_lib = None
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int
+I64 = ctypes.c_longlong
+F32 = ctypes.c_float
+
+
+class SinkhornFwdParams(ctypes.Structure):
+    """Mirror of ``dfl_sinkhorn_fwd_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("q", P), ("k", P), ("v", P), ("g", P),
+        ("stride_b", I64), ("stride_h", I64), ("stride_n", I64),
+        ("x_res", P), ("pos_weight", P), ("pos_bins", P),
+        ("eps", P), ("w_dist", P), ("log_mu", P), ("log_nu", P),
+        ("log_u_init", P), ("log_v_init", P), ("mask", P),
+        ("B", I32), ("H", I32), ("N", I32), ("d", I32),
+        ("K_iter", I32), ("lam", F32), ("r_0", F32),
+        ("o_flat", P), ("x_centroid", P), ("log_u", P), ("log_v", P),
+        ("o_avg", P), ("log_z", P), ("col_lse", P),
+    ]
+
+
+class SinkhornBwdParams(ctypes.Structure):
+    """Mirror of ``dfl_sinkhorn_bwd_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("q", P), ("k", P), ("v", P), ("g", P),
+        ("stride_b", I64), ("stride_h", I64), ("stride_n", I64),
+        ("x_res", P), ("pos_weight", P), ("pos_bins", P),
+        ("eps", P), ("w_dist", P), ("mask", P),
+        ("log_u", P), ("log_v", P), ("log_z", P), ("col_lse", P),
+        ("o_avg", P), ("x_centroid", P), ("grad_o", P), ("grad_xc", P),
+        ("B", I32), ("H", I32), ("N", I32), ("d", I32),
+        ("lam", F32), ("r_0", F32),
+        ("solver", I32), ("iters", I32), ("mode", I32), ("cg_rtol", F32),
+        ("dq", P), ("dk", P), ("dv", P), ("dg", P),
+        ("dlog_mu", P), ("dlog_nu", P), ("dx_res", P), ("dpos_weight", P), ("dw_dist", P),
+    ]
+
+
+# (name, restype, argtypes) of every exported symbol; tests check that the .so
+# exports exactly what include/dfl_amd.h declares.
+SIGNATURES = [
+    ("dfl_last_error", ctypes.c_char_p, []),
+    ("dfl_version", ctypes.c_char_p, []),
+    ("dfl_workspace_error", I32, [P, P]),
+    ("dfl_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
+    ("dfl_sinkhorn_fwd", I32, [ctypes.POINTER(SinkhornFwdParams), P, ctypes.c_size_t, P]),
+    ("dfl_sinkhorn_bwd", I32, [ctypes.POINTER(SinkhornBwdParams), P, ctypes.c_size_t, P]),
+]
+
+
+def load(path: str = LIB_PATH):
+    """Load (once) and return the ctypes handle; raise if the library is absent."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise RuntimeError(
+                    f"deepfold_amd: HIP library not built ({path} missing). "
+                    "Run `python -c 'import __graft_entry__ as g; g.build()'` from the repo root.")
+            lib = ctypes.CDLL(path)
+            for name, res, args in SIGNATURES:
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+        return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().dfl_last_error().decode(errors="replace")
+        raise RuntimeError(f"deepfold_amd {what} failed (code {rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(*tensors) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("deepfold_amd ops run only on ROCm GPU tensors (no CPU fallback)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError("deepfold_amd: all tensors must be on the same device")
+    if dev is None:
+        raise RuntimeError("deepfold_amd: no tensor inputs")
+    return dev
+
+
+_ws_cache: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled device workspace, cached per (device, stream) and grown on demand."""
+    key = (device.index, stream_handle(device))
+    ws = _ws_cache.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _ws_cache[key] = ws
+    return ws
+
+
+def debug_checks() -> bool:
+    return os.environ.get("DFL_AMD_CHECK", "0") not in ("", "0")
+
+
+def check_workspace(ws: torch.Tensor, what: str) -> None:
+    """Synchronising check of the kernel-side error word (used when DFL_AMD_CHECK=1)."""
+    code = load().dfl_workspace_error(ctypes.c_void_p(ws.data_ptr()),
+                                      ctypes.c_void_p(stream_handle(ws.device)))
+    if code != 0:
+        raise RuntimeError(f"deepfold_amd {what}: kernel reported error code {code} "
+                           "(a cross-workgroup wait expired)")

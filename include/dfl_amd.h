@@ -1,0 +1,152 @@
+/*
+ * deepfold_amd C ABI: MI355X (gfx950) kernels for DeepFold-Linear's flash-Sinkhorn
+ * optimal-transport attention, its implicit-function-theorem backward, and the
+ * neighbouring flash diffusion / atom-window / atom<->token cross attention.
+ *
+ * Conventions (every entry point):
+ *  - Plain device pointers, explicit shapes and element strides, a dtype enum;
+ *    no torch types.  Potentials, accumulators and every output are fp32.
+ *  - The caller allocates every output (zero-initialised: padded positions are
+ *    left untouched) and a workspace of dfl_*_workspace_size() bytes.  A workspace
+ *    must be zero-filled once when it is first allocated; after that it may be
+ *    reused by any number of calls without clearing.  Calls that share a
+ *    workspace must not overlap in time.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).  The
+ *    library never allocates device memory and never synchronises.
+ *  - Return value: 0 = success, < 0 = argument error (see dfl_last_error()),
+ *    > 0 = hipError_t of a failed launch.
+ *  - Kernels that wait on other workgroups have bounded spins; if a wait ever
+ *    expires the kernel exits and records an error in the workspace, which
+ *    dfl_workspace_error() reports (it synchronises `stream`).
+ */
+#ifndef DFL_AMD_H
+#define DFL_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dfl_dtype { DFL_BF16 = 0, DFL_F32 = 1 };
+
+/* Thread-local message for the last failed call on this thread. */
+const char* dfl_last_error(void);
+
+/* Library version string. */
+const char* dfl_version(void);
+
+/* Reports (and clears nothing) the error recorded by the most recent call that
+ * used `workspace`: 0 = none, else the kernel's error code.  Synchronises `stream`. */
+int dfl_workspace_error(const void* workspace, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Flash-Sinkhorn forward.
+ * Replaces FlashSinkhornAttn.forward (src/deepfold/model/kernels/flash_sinkhorn_attn.py:77-244)
+ * and the Triton forward FlashSinkhornFunction.forward (sinkhorn_kernel.py:1921-2083):
+ * K_iter log-domain UOT Sinkhorn iterations, then O_avg = T_norm V, x_c = T_norm x,
+ * o = sigmoid(G) * O_avg permuted to (B, N, H*d).
+ * q, k, v, g: (B,H,N,d) elements of `dtype` at q + b*stride_b + h*stride_h + n*stride_n + c.
+ * g may be NULL (no gate: o = O_avg).  x_res (B,N,3), pos_weight (H,68), pos_bins (B,N,N)
+ * int32, w_dist (H,), log_u_init/log_v_init (B,H,N) and mask (B,N) may be NULL.
+ * Outputs o_flat (B,N,H*d), x_centroid (B,H,N,3), log_u, log_v (B,H,N); saved for the
+ * backward: o_avg (B,H,N,d), log_z (B,H,N) = LSE_j(u_i + L_ij + v_j) and
+ * col_lse (B,H,N) = LSE_i(L_ij + u_i) of the last column update.
+ */
+typedef struct dfl_sinkhorn_fwd_params {
+  int dtype;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  long long stride_b, stride_h, stride_n;
+  const float* x_res;
+  const float* pos_weight;
+  const int* pos_bins;
+  const float* eps;
+  const float* w_dist;
+  const float* log_mu;
+  const float* log_nu;
+  const float* log_u_init;
+  const float* log_v_init;
+  const float* mask;
+  int B, H, N, d;
+  int K_iter;
+  float lam;
+  float r_0;
+  float* o_flat;
+  float* x_centroid;
+  float* log_u;
+  float* log_v;
+  float* o_avg;
+  float* log_z;
+  float* col_lse;
+} dfl_sinkhorn_fwd_params;
+
+size_t dfl_sinkhorn_workspace_size(int B, int H, int N);
+int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Flash-Sinkhorn IFT backward.
+ * Replaces FlashSinkhornAttn.backward (flash_sinkhorn_attn.py:246-667).  The linear
+ * system (I - kappa^2 S_row^T S_col) z_v = g_v is solved either by the reference's
+ * Gauss-Seidel fixed point (solver = DFL_IFT_FIXED_POINT, `iters` sweeps; the
+ * reference uses iters = K_iter) or by conjugate gradient on its symmetric form
+ * (solver = DFL_IFT_CG, `iters` CG steps).  mode = DFL_IFT_REFERENCE reproduces the
+ * reference's signs; DFL_IFT_ANALYTIC gives the true implicit adjoint (the z_v*S_col
+ * term of dC and d log_mu change sign).  Padded tokens (mask == 0) are excluded,
+ * which equals evaluating each sample on its unpadded slice.
+ * Inputs are the forward's inputs and saved outputs plus grad_o (B,N,H*d) fp32 and
+ * grad_xc (B,H,N,3) fp32 (may be NULL).  Outputs (fp32, zero-initialised by the caller):
+ * dq, dk, dv, dg (B,H,N,d), dlog_mu, dlog_nu (B,H,N), dx_res (B,N,3),
+ * dpos_weight (H,68), dw_dist (H,).
+ */
+enum dfl_ift_solver { DFL_IFT_FIXED_POINT = 0, DFL_IFT_CG = 1 };
+enum dfl_ift_mode { DFL_IFT_REFERENCE = 0, DFL_IFT_ANALYTIC = 1 };
+
+typedef struct dfl_sinkhorn_bwd_params {
+  int dtype;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  long long stride_b, stride_h, stride_n;
+  const float* x_res;
+  const float* pos_weight;
+  const int* pos_bins;
+  const float* eps;
+  const float* w_dist;
+  const float* mask;
+  const float* log_u;
+  const float* log_v;
+  const float* log_z;
+  const float* col_lse;
+  const float* o_avg;
+  const float* x_centroid;
+  const float* grad_o;
+  const float* grad_xc;
+  int B, H, N, d;
+  float lam;
+  float r_0;
+  int solver;
+  int iters;
+  int mode;
+  float cg_rtol;
+  float* dq;
+  float* dk;
+  float* dv;
+  float* dg;
+  float* dlog_mu;
+  float* dlog_nu;
+  float* dx_res;
+  float* dpos_weight;
+  float* dw_dist;
+} dfl_sinkhorn_bwd_params;
+
+int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFL_AMD_H */

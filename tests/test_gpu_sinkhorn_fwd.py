@@ -1,0 +1,146 @@
+"""GPU parity of the flash-Sinkhorn forward against the CPU oracle.
+
+Relative error = max |gpu - oracle| / max |oracle| per tensor.  Bars (north star):
+1e-4 for fp32 inputs, 2e-2 for bf16 inputs (the oracle consumes the bf16-rounded
+inputs upcast to float64).  Padded batches are compared with each sample
+evaluated on its unpadded slice (oracle.sinkhorn.backward_masked).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_rel
+from oracle import sinkhorn as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def make_inputs(B, H, N, d, *, seed, eps, pos_geo=False, with_bins=None, dirichlet=False):
+    g = torch.Generator().manual_seed(seed)
+    Q = torch.randn(B, H, N, d, generator=g) / d ** 0.5
+    K = torch.randn(B, H, N, d, generator=g) / d ** 0.5
+    V = torch.randn(B, H, N, d, generator=g)
+    G = torch.randn(B, H, N, d, generator=g)
+    if pos_geo:
+        x = torch.randn(B, N, 3, generator=g) * 3.0
+        pw = torch.randn(H, 68, generator=g) * 0.5
+        bins = torch.randint(0, 68, (B, N, N), generator=g, dtype=torch.int32)
+        wd = torch.rand(H, generator=g)
+    else:
+        x = torch.randn(B, N, 3, generator=g)
+        pw = torch.zeros(H, 68)
+        bins = None
+        wd = torch.zeros(H)
+    if with_bins is False:
+        bins = None
+    lmu = torch.log_softmax(torch.randn(B, H, N, generator=g), -1)
+    lnu = torch.log_softmax(torch.randn(B, H, N, generator=g), -1)
+    return dict(Q=Q, K=K, V=V, G=G, x_res=x, pos_weight=pw, pos_bins=bins,
+                eps=torch.tensor(eps, dtype=torch.float32), w_dist=wd, log_mu=lmu, log_nu=lnu)
+
+
+def run_gpu(inp, K_iter, dtype, mask=None, **kw):
+    from deepfold_amd import flash_sinkhorn_attn
+
+    dev = torch.device("cuda:0")
+    t = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
+    for k in ("Q", "K", "V", "G"):
+        t[k] = t[k].to(dtype)
+    out = flash_sinkhorn_attn(t["Q"], t["K"], t["V"], t["G"], t["x_res"], t["pos_weight"], t["pos_bins"],
+                              t["eps"], t["w_dist"], t["log_mu"], t["log_nu"], K_iter=K_iter,
+                              mask=None if mask is None else mask.to(dev), **kw)
+    torch.cuda.synchronize()
+    return [o.float().cpu().numpy() for o in out]
+
+
+def oracle_inputs(inp, dtype):
+    o = {}
+    for k, v in inp.items():
+        if v is None:
+            o[k] = None
+        elif k in ("Q", "K", "V", "G"):
+            o[k] = v.to(dtype).to(torch.float64).numpy()
+        else:
+            o[k] = v.numpy()
+    return o
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("B,H,N,d,eps,K", [
+    (1, 4, 256, 32, [1.0] * 4, 20),      # BASELINE config 1 shape
+    (2, 2, 70, 16, [0.5, 2.0], 7),       # ragged tile, small d
+    (1, 2, 100, 64, [0.25, 1.0], 5),     # d = 64
+    (1, 1, 16, 8, [1.0], 3),             # single tile
+])
+def test_forward_matches_oracle(dtype, tol, B, H, N, d, eps, K):
+    inp = make_inputs(B, H, N, d, seed=100 + N + d, eps=eps)
+    got = run_gpu(inp, K, dtype)
+    want = ref.forward(**oracle_inputs(inp, dtype), K_iter=K)
+    for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+        assert_close_rel(gv, want[name], tol, name)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_forward_general_cost(dtype, tol):
+    """Position bins + geometry terms (the reference's full cost, flash_sinkhorn_attn.py:155-159)."""
+    inp = make_inputs(2, 4, 40, 32, seed=5, eps=[0.5, 1.0, 2.0, 4.0], pos_geo=True)
+    got = run_gpu(inp, 6, dtype)
+    want = ref.forward(**oracle_inputs(inp, dtype), K_iter=6)
+    for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+        assert_close_rel(gv, want[name], tol, name)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_forward_masked_equals_unpadded(dtype, tol):
+    B, H, N, d = 3, 2, 96, 32
+    inp = make_inputs(B, H, N, d, seed=9, eps=[0.5, 1.0])
+    lengths = [96, 61, 17]
+    mask = torch.zeros(B, N)
+    for b, n in enumerate(lengths):
+        mask[b, :n] = 1
+    got = run_gpu(inp, 8, dtype, mask=mask)
+    oi = oracle_inputs(inp, dtype)
+    oi["mask"] = mask.numpy()
+    fo, _ = ref.backward_masked(dict(oi, K_iter=8, lam=1.0, r_0=10.0), None)
+    for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+        assert_close_rel(gv, fo[name], tol, name)
+        # padded positions are exactly zero
+        for b, n in enumerate(lengths):
+            if name == "o_flat":
+                assert np.all(gv[b, n:] == 0)
+            else:
+                assert np.all(gv[b, :, n:] == 0)
+
+
+def test_forward_golden_vectors():
+    """The reference's own outputs (tests/golden/make_golden.py) at fp32."""
+    import glob
+    import os
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    files = sorted(glob.glob(os.path.join(here, "golden", "flash_sinkhorn_*.npz")))
+    assert files
+    for f in files:
+        z = np.load(f)
+        inp = {k: torch.from_numpy(z[k]) for k in ("Q", "K", "V", "G", "x_res", "pos_weight", "pos_bins",
+                                                   "eps", "w_dist", "log_mu", "log_nu")}
+        got = run_gpu(inp, int(z["K_iter"]), torch.float32)
+        # torch.cdist's matmul path (N > 25) rounds the reference's distances; 3e-4 covers it
+        for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+            assert_close_rel(gv, z[name], 3e-4, f"{os.path.basename(f)}:{name}")
+
+
+def test_unbatched_matches_batched():
+    inp = make_inputs(1, 2, 40, 32, seed=3, eps=[0.5, 1.0])
+    from deepfold_amd import flash_sinkhorn_attn
+
+    dev = torch.device("cuda:0")
+    t = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
+    ob = flash_sinkhorn_attn(t["Q"], t["K"], t["V"], t["G"], t["x_res"], t["pos_weight"], None, t["eps"],
+                             t["w_dist"], t["log_mu"], t["log_nu"], K_iter=4)
+    ou = flash_sinkhorn_attn(t["Q"][0], t["K"][0], t["V"][0], t["G"][0], t["x_res"][0], t["pos_weight"], None,
+                             t["eps"], t["w_dist"], t["log_mu"][0], t["log_nu"][0], K_iter=4)
+    for a, b in zip(ob, ou):
+        assert a.shape[1:] == b.shape
+        assert torch.equal(a[0], b)
