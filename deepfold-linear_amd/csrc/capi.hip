@@ -169,9 +169,7 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   if (!p->q || !p->k || !p->v || !p->eps || !p->log_u || !p->log_v || !p->log_z || !p->col_lse || !p->o_avg ||
       !p->x_centroid || !p->grad_o)
     return fail("required input is NULL");
-  if (!p->dq || !p->dk || !p->dv || !p->dg || !p->dlog_mu || !p->dlog_nu || !p->dx_res || !p->dpos_weight ||
-      !p->dw_dist)
-    return fail("output pointer is NULL");
+  if (!p->dq || !p->dk || !p->dv || !p->dg || !p->dlog_mu || !p->dlog_nu) return fail("output pointer is NULL");
   if (p->stride_n < p->d) return fail("stride_n must be >= d (unit inner stride)");
   if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
   const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
@@ -193,6 +191,7 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d;
   a.lam = p->lam; a.r0 = p->r_0;
   a.solver = p->solver; a.iters = p->iters; a.mode = p->mode; a.cg_rtol = p->cg_rtol;
+  a.geo_grad = (p->x_res && (p->dx_res || p->dw_dist)) ? 1 : 0;
   a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dg = p->dg;
   a.dlog_mu = p->dlog_mu; a.dlog_nu = p->dlog_nu;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -89,6 +89,26 @@ template <int DP> struct Mfma<bf16, DP> {
     b[4] = hi[0]; b[5] = hi[1]; b[6] = hi[2]; b[7] = hi[3];
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
   }
+  // Same product with P carried as a hi + lo pair of bf16 values (~16-bit
+  // mantissa): two MFMAs against the same V operand.
+  __device__ static __forceinline__ f32x4 pv_split(const f32x4& p0, const f32x4& p1, const bf16* vt_row, int lane,
+                                                   f32x4 acc) {
+    const int g = lane >> 4;
+    bf16x8 ah, al, b;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bf16 h0 = (bf16)p0[r], h1 = (bf16)p1[r];
+      ah[r] = h0; ah[4 + r] = h1;
+      al[r] = (bf16)(p0[r] - (float)h0); al[4 + r] = (bf16)(p1[r] - (float)h1);
+    }
+    bf16x4 lo = *reinterpret_cast<const bf16x4*>(vt_row + 4 * g);
+    bf16x4 hi = *reinterpret_cast<const bf16x4*>(vt_row + 16 + 4 * g);
+    b[0] = lo[0]; b[1] = lo[1]; b[2] = lo[2]; b[3] = lo[3];
+    b[4] = hi[0]; b[5] = hi[1]; b[6] = hi[2]; b[7] = hi[3];
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, acc, 0, 0, 0);
+  }
+  static constexpr bool SPLIT = true;
 };
 
 template <int DP> struct Mfma<float, DP> {
@@ -121,6 +141,11 @@ template <int DP> struct Mfma<float, DP> {
     for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[r], hi[r], acc, 0, 0, 0);
     return acc;
   }
+  __device__ static __forceinline__ f32x4 pv_split(const f32x4& p0, const f32x4& p1, const float* vt_row, int lane,
+                                                   f32x4 acc) {
+    return pv(p0, p1, vt_row, lane, acc);
+  }
+  static constexpr bool SPLIT = false;  // fp32 operands are exact already
 };
 
 // ---------------------------------------------------------------------------

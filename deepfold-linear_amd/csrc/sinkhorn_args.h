@@ -66,6 +66,7 @@ struct SinkBwdArgs {
   int iters;    // fixed-point sweeps or CG iterations
   int mode;     // 0 = reference signs, 1 = analytic adjoint
   float cg_rtol;  // CG early stop on ||r|| <= rtol ||b|| (0 = run all iterations)
+  int geo_grad;   // compute d x_res / d w_dist cost terms (x given and requested)
   // outputs (caller zero-initialises)
   float* dq;        // (B,H,N,d)
   float* dk;

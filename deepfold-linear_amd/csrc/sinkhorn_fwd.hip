@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c)
-        oacc[c] = M::pv(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
+        oacc[c] = M::pv_split(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
     }
     xc0 = sum_groups(xc0);
     xc1 = sum_groups(xc1);

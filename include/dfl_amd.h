@@ -98,8 +98,8 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
  * which equals evaluating each sample on its unpadded slice.
  * Inputs are the forward's inputs and saved outputs plus grad_o (B,N,H*d) fp32 and
  * grad_xc (B,H,N,3) fp32 (may be NULL).  Outputs (fp32, zero-initialised by the caller):
- * dq, dk, dv, dg (B,H,N,d), dlog_mu, dlog_nu (B,H,N), dx_res (B,N,3),
- * dpos_weight (H,68), dw_dist (H,).
+ * dq, dk, dv, dg (B,H,N,d), dlog_mu, dlog_nu (B,H,N); optional (NULL = not requested,
+ * which also skips their per-element work): dx_res (B,N,3), dpos_weight (H,68), dw_dist (H,).
  */
 enum dfl_ift_solver { DFL_IFT_FIXED_POINT = 0, DFL_IFT_CG = 1 };
 enum dfl_ift_mode { DFL_IFT_REFERENCE = 0, DFL_IFT_ANALYTIC = 1 };

@@ -220,7 +220,10 @@ def backward_reference(fwd_inputs: dict, fwd_out: dict, grad_o_flat, grad_xc=Non
                     z_u = k_h * (S_col @ z_v)
                     z_v = g_v + k_h * (S_row.T @ z_u)
             elif solver == "cg":
-                z_v = cg_system(T, k_h, g_v, n_cg if n_cg is not None else 50)
+                # unnormalised plan exp(u + L + v) up to the scalar exp(-max logZ)
+                lz = pc["logZ"]
+                T_un = T * np.exp(lz - lz.max())[:, None]
+                z_v = cg_system(T_un, k_h, g_v, n_cg if n_cg is not None else 50)
                 z_u = k_h * (S_col @ z_v)
             else:
                 raise ValueError(f"unknown solver {solver!r}")
@@ -241,16 +244,17 @@ def backward_reference(fwd_inputs: dict, fwd_out: dict, grad_o_flat, grad_xc=Non
     return out
 
 
-def cg_system(T_unnorm_or_norm, kappa, g_v, n_iter, *, tol=0.0):
+def cg_system(T, kappa, g_v, n_iter, *, tol=0.0):
     """Solve (I - kappa^2 S_row^T S_col) z_v = g_v by CG on its symmetric form.
 
-    With T_ij = exp(u_i + L_ij + v_j) (any positive row scaling of it gives the
-    same S_row and S_col), r = T 1, c = T^T 1, W = D_r^{-1/2} T D_c^{-1/2}:
-    S_row^T S_col = D_c^{1/2} W^T W D_c^{-1/2}, so with y = D_c^{-1/2} z_v the
-    system is (I - kappa^2 W^T W) y = D_c^{-1/2} g_v, whose spectrum lies in
-    [1 - kappa^2, 1].  CG steps follow utils/cg.py:56-97 (x0 = 0).
+    ``T`` is the transport plan T_ij = exp(u_i + L_ij + v_j) up to one positive
+    scalar factor (a scalar leaves S_row = D_r^{-1} T and S_col = T D_c^{-1}
+    unchanged; a row rescaling would change S_col).  With r = T 1, c = T^T 1 and
+    W = D_r^{-1/2} T D_c^{-1/2}:  S_row^T S_col = D_c^{1/2} W^T W D_c^{-1/2}, so with
+    y = D_c^{-1/2} z_v the system is (I - kappa^2 W^T W) y = D_c^{-1/2} g_v, whose
+    spectrum lies in [1 - kappa^2, 1].  CG steps follow utils/cg.py:56-97 (x0 = 0).
     """
-    T = np.asarray(T_unnorm_or_norm)
+    T = np.asarray(T)
     r = T.sum(1)
     c = T.sum(0)
     W = T / np.sqrt(r)[:, None] / np.sqrt(c)[None, :]
