@@ -1,0 +1,220 @@
+"""Benchmark: flash-Sinkhorn forward + IFT backward per layer on one MI355X.
+
+Workload: B=2, H=8, N=768 padded, d=32, bf16 inputs
+with fp32 accumulation, ragged valid lengths n_b ~ U[384, 768] with a padding
+mask, eps=0.5, 50 Sinkhorn iterations, 20 CG iterations in the IFT solve,
+upstream gradient dO ~ N(0,1).  Synthetic data, seed 1002 (= 1000 + config#).
+Unspecified terms are neutral: no position bins, w_dist = 0, x_res = 0, G = 0.
+
+One "step" = one forward (flash_sinkhorn_attn) + one backward (autograd) of the
+layer, inputs resident in HBM.  Prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "deepfold-linear_amd"))
+
+# MI355X published peaks (dense): bf16 MFMA 2.5 PFLOP/s, HBM 8 TB/s.
+PEAK_MFMA_BF16 = 2.5e15
+PEAK_HBM = 8.0e12
+# v_exp_f32 rate used by BASELINE.md's exp roof (quarter-rate estimate).
+PEAK_EXP_NOMINAL = 9.8e12
+
+CFG = dict(B=2, H=8, N=768, d=32, eps=0.5, K_iter=50, n_cg=20, seed=1002)
+
+
+def make_workload(device, dtype=None):
+    import torch
+
+    dtype = dtype or torch.bfloat16
+    B, H, N, d = CFG["B"], CFG["H"], CFG["N"], CFG["d"]
+    g = torch.Generator().manual_seed(CFG["seed"])
+    lengths = torch.randint(384, 769, (B,), generator=g).tolist()
+    Q = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(dtype)
+    K = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(dtype)
+    V = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(dtype)
+    G = torch.zeros(B, H, N, d, dtype=dtype)
+    mask = torch.zeros(B, N)
+    log_m = torch.zeros(B, H, N)
+    for b, n in enumerate(lengths):
+        mask[b, :n] = 1.0
+        log_m[b, :, :n] = -math.log(n)
+    dO = torch.randn(B, N, H * d, generator=g).to(dtype).float()
+    dO = dO * mask[:, :, None]
+    x = torch.zeros(B, N, 3)
+    pw = torch.zeros(H, 68)
+    eps = torch.full((H,), CFG["eps"])
+    wd = torch.zeros(H)
+    cpu = dict(Q=Q, K=K, V=V, G=G, x_res=x, pos_weight=pw, eps=eps, w_dist=wd, log_mu=log_m,
+               log_nu=log_m.clone(), mask=mask, dO=dO, lengths=lengths)
+    dev = {k: (v.to(device) if hasattr(v, "to") else v) for k, v in cpu.items()}
+    return cpu, dev
+
+
+def step(t):
+    from deepfold_amd import flash_sinkhorn_attn
+
+    q, k, v, g = (t[n].detach().requires_grad_(True) for n in ("Q", "K", "V", "G"))
+    o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], t["w_dist"],
+                                        t["log_mu"], t["log_nu"], K_iter=CFG["K_iter"], mask=t["mask"],
+                                        ift_solver="cg", ift_iters=CFG["n_cg"])
+    o.backward(t["dO"])
+    return q.grad
+
+
+def algorithmic_counts(lengths):
+    """Per-layer algorithmic work (BASELINE.md section 2 / SURVEY.md section 8d):
+    E = sum_b H n_b^2 valid plan elements; forward 2K LSE sweeps at 2d flops +
+    one output sweep at 4d; backward n_CG matvec sweeps at 2d + g_v sweep 6d +
+    gradient sweep 8d; one exp per element per sweep."""
+    H, d, K, ncg = CFG["H"], CFG["d"], CFG["K_iter"], CFG["n_cg"]
+    E = sum(H * n * n for n in lengths)
+    f_fwd = E * d * (4 * K + 4)
+    f_bwd = E * d * (14 + 2 * ncg)
+    x_fwd = E * (2 * K + 1)
+    x_bwd = E * (ncg + 2)
+    return E, f_fwd, f_bwd, x_fwd, x_bwd
+
+
+def cpu_baseline(cpu, budget_s=20.0):
+    """Time the numpy oracle (float32, one thread) on a bounded sample of the
+    layer: full forward (K=50) + reference fixed-point IFT backward (50 sweeps)
+    of whole (b, h) heads, stopping once ~budget_s of CPU time is spent, then
+    scaled to the B*H heads of the layer."""
+    import numpy as np
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except Exception:  # pragma: no cover
+        threadpool_limits = None
+    sys.path.insert(0, ROOT)
+    from oracle import sinkhorn as ref
+
+    B, H, d = CFG["B"], CFG["H"], CFG["d"]
+    lengths = cpu["lengths"]
+    spent, sampled, heads = 0.0, 0, []
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    try:
+        order = [(b, h) for h in range(H) for b in range(B)]  # alternate samples
+        for b, h in order:
+            n = lengths[b]
+            sl = lambda a: a[b:b + 1, h:h + 1, :n].float().numpy()
+            inp = dict(Q=sl(cpu["Q"]), K=sl(cpu["K"]), V=sl(cpu["V"]), G=sl(cpu["G"]),
+                       x_res=cpu["x_res"][b:b + 1, :n].numpy(), pos_weight=cpu["pos_weight"][h:h + 1].numpy(),
+                       pos_bins=None, eps=cpu["eps"][h:h + 1].numpy(), w_dist=cpu["w_dist"][h:h + 1].numpy(),
+                       log_mu=cpu["log_mu"][b:b + 1, h:h + 1, :n].numpy(),
+                       log_nu=cpu["log_nu"][b:b + 1, h:h + 1, :n].numpy(),
+                       K_iter=CFG["K_iter"], lam=1.0, r_0=10.0)
+            go = cpu["dO"].reshape(B, -1, H, d)[b:b + 1, :n, h, :].numpy()
+            t0 = time.perf_counter()
+            fo = ref.forward(**inp, dtype=np.float32)
+            ref.backward_reference(inp, fo, go, None, K_back=CFG["K_iter"], dtype=np.float32)
+            spent += time.perf_counter() - t0
+            sampled += 1
+            heads.append((b, h))
+            if spent > budget_s:
+                break
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
+    # per-head cost scales with n_b^2: extrapolate by the sampled share of plan elements
+    e_all = sum(H * n * n for n in lengths)
+    e_smp = sum(lengths[b] ** 2 for b, _ in heads)
+    return dict(value=round(spent * e_all / e_smp * 1e3, 1), unit="ms/layer", cores=1, kind="port",
+                sample=f"numpy oracle (float32, 1 thread): dense forward K={CFG['K_iter']} + reference "
+                       f"fixed-point IFT backward ({CFG['K_iter']} sweeps) on {sampled} of {B * H} (b,h) heads "
+                       f"({spent:.1f} s), extrapolated by valid plan elements")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the flash-Sinkhorn "
+              "path shards by (b, h) with no communication, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import deepfold_amd
+    from deepfold_amd import _lib
+
+    os.environ["DFL_AMD_CHECK"] = "0"
+    dev = torch.device("cuda:0")
+    cpu, t = make_workload(dev)
+    for _ in range(args.warmup):
+        step(t)
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` steps, kernel launches bracketed by events
+    _lib.launch_timings = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(t)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    timings = _lib.launch_timings
+    _lib.launch_timings = None
+    per = {}
+    for name, s, e in timings:
+        per.setdefault(name, []).append(s.elapsed_time(e))
+    avg = {k: sum(v) / len(v) for k, v in per.items()}
+    ms_per_step = wall * 1e3 / args.steps
+
+    E, f_fwd, f_bwd, x_fwd, x_bwd = algorithmic_counts(cpu["lengths"])
+    dom = max(avg, key=avg.get)
+    f_dom = f_fwd if dom == "sinkhorn_fwd" else f_bwd
+    x_dom = x_fwd if dom == "sinkhorn_fwd" else x_bwd
+    achieved = f_dom / (avg[dom] * 1e-3)
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"{dom}_cfg2_traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            traffic = json.load(fh).get("hbm_bytes_per_launch")
+    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
+
+    out = {
+        "metric": "flash-Sinkhorn fwd+IFT-bwd ms/layer @B2,H8,N768,d32 bf16; % of MFMA/HBM roof",
+        "value": round(ms_per_step, 4),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed 1002): Q,K,V ~ N(0,1)/sqrt(d), ragged n_b ~ U[384,768], dO ~ N(0,1)",
+        "config": {"workload": "BASELINE configs[1]: flash-Sinkhorn fwd + IFT(CG) bwd", "B": CFG["B"],
+                   "H": CFG["H"], "N": CFG["N"], "d": CFG["d"], "n_b": cpu["lengths"], "eps": CFG["eps"],
+                   "K_iter": CFG["K_iter"], "n_cg": CFG["n_cg"], "valid_plan_elements": E},
+        "kernel_ms": {k: round(v, 4) for k, v in avg.items()},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
+                     "peak": PEAK_MFMA_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_BF16, 5),
+                     "traffic": traffic},
+        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_NOMINAL,
+                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
+                         "layer_t_roof_ms": t_roof * 1e3, "layer_frac": t_roof * 1e3 / ms_per_step},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cpu)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -75,10 +75,11 @@ size_t xch_words(int B, int H, int N) { return (size_t)B * H * 4 * np32(N); }
 
 int head_dim_pad(int d) { return d <= 32 ? 32 : (d <= 64 ? 64 : -1); }
 
-// Workgroups per (b,h): enough to cover the chip, at most one per 16-row tile.
+// Workgroups per (b,h): as many as fit one per CU in the XCD-aligned grid
+// (dfl::grid_blocks), at most one per 16-row tile.
 int group_size(int B, int H, int N) {
   const int bh = B * H;
-  int G = cu_count() / bh;
+  int G = cu_count() / (8 * ((bh + 7) / 8));
   if (G < 1) G = 1;
   const int tiles = (N + 15) / 16;
   if (G > tiles) G = tiles;
@@ -151,7 +152,7 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
   a.salt = next_salt();
-  const bool coop = G > 1;
+  const bool coop = G > 1;  // members wait on each other: all must be co-resident
   hipError_t e = dfl::launch_sinkhorn_fwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn forward launch");
   return 0;

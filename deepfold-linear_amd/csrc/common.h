@@ -185,7 +185,7 @@ __device__ __forceinline__ void xch_put(uint64_t* word, float v, uint32_t tag) {
 // `tag`, writing value * scale into dst[] (LDS).  Returns false (uniformly across
 // the block) if the error flag is raised or the spin limit is hit.
 template <int NT>
-__device__ bool xch_gather(const uint64_t* buf, int n, uint32_t tag, float* dst, float scale,
+__device__ __forceinline__ bool xch_gather(const uint64_t* buf, int n, uint32_t tag, float* dst, float scale,
                            uint32_t* err, int* s_flag) {
   const uint32_t salt = tag >> 12;
   const int t = threadIdx.x;
@@ -211,6 +211,7 @@ __device__ bool xch_gather(const uint64_t* buf, int n, uint32_t tag, float* dst,
         }
       }
       if (pending) {
+        __builtin_amdgcn_s_sleep(1);  // back off: tight polling slows the publishers' stores
         if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); ok = false; break; }
         if ((spins & 255u) == 0u && error_raised(err, salt)) { ok = false; break; }
       }

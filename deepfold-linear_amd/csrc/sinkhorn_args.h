@@ -4,6 +4,9 @@
 
 namespace dfl {
 
+// Workgroups launched for n_groups groups of G members: whole 8-XCD slots.
+inline int grid_blocks(int n_groups, int G) { return 8 * ((n_groups + 7) / 8) * G; }
+
 // Forward (flash_sinkhorn_attn.py:77-244 semantics).
 struct SinkFwdArgs {
   const void* q;  // (B,H,N,d) bf16 or fp32, element strides sb/sh/sn, unit inner stride

@@ -120,7 +120,7 @@ __device__ float block_sum(int n, F f, float* red) {
 // Gather a published vector into dst (scale 1), zeroing invalid entries and the tail.
 __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
                                               const unsigned char* valid, uint32_t* err, int* s_flag) {
-  if (!xch_gather<SK_NT>(buf, n, tag, dst, 1.f, err, s_flag)) return false;
+  if (!xch_gather<SK_NT>(buf, n, tag, dst, 1.f, err, s_flag)) return false;  // values as published
   for (int i = threadIdx.x; i < Np; i += SK_NT)
     if (i >= n || !valid[i]) dst[i] = 0.f;
   __syncthreads();
@@ -176,7 +176,8 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   using M = Mfma<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ BwdShared sh;
-  const int grp = blockIdx.x / a.G, member = blockIdx.x % a.G;
+  int grp, member;
+  if (!group_of(a.B * a.H, a.G, grp, member)) return;  // surplus workgroup of the XCD-aligned grid
   const int b = grp / a.H, h = grp % a.H;
   const int N = a.N, d = a.d;
   const int Np = ((N + 31) / 32) * 32;
@@ -910,7 +911,7 @@ static hipError_t launch_bwd_t(const SinkBwdArgs& a, size_t lds, hipStream_t str
   auto kern = sinkhorn_bwd_kernel<T, DP>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  dim3 grid(a.B * a.H * a.G), block(SK_NT);
+  dim3 grid(grid_blocks(a.B * a.H, a.G)), block(SK_NT);
   SinkBwdArgs copy = a;
   if (coop) {
     void* args[] = {&copy};

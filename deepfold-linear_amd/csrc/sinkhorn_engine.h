@@ -4,15 +4,19 @@
 // streamed 16-row tiles of the same (b,h): the cost tile QK^T is recomputed on
 // MFMA from LDS-resident operands and reduced on the fly.  In a row sweep the
 // resident rows are Q (plan rows i) and the streamed rows are K (plan columns
-// j); in a column sweep the roles swap.
+// j); in a column sweep the roles swap.  NT = threads per workgroup.
 #pragma once
 #include "common.h"
 
 namespace dfl {
 
-constexpr int SK_NT = 256;
+constexpr int SK_NT = 256;  // backward workgroup size
 constexpr int SK_NW = SK_NT / WAVE;
-constexpr int SK_RT = 4;  // resident tiles per register chunk
+constexpr int SK_RT = 4;    // resident tiles per register chunk
+
+// Scratch floats needed by the sweeps of an NT-thread workgroup.
+template <int NT> constexpr int sweep_scratch() { return 2 * (NT / WAVE) * SK_RT * 16; }
+constexpr int LSE_SCRATCH = 2 * SK_NW * SK_RT * 16;
 
 // Position-bin / geometry bias of the cost, in log2 units of the logit:
 //   bias(i, j) = -(log2 e / eps) * (pw[bins_ij] + w * d_ij / (r0 + d_ij)).
@@ -36,9 +40,22 @@ struct Bias {
 };
 
 // Stage rows [0, n) of a row-strided slice into LDS row-major [Np][DP]
-// (zero-filling columns >= d and rows >= n).
+// (zero-filling columns >= d and rows >= n).  16-byte loads when the layout allows.
 template <typename T, int DP>
-__device__ void stage_rows(T* dst, const T* __restrict__ src, long long sn, int n, int d, int Np) {
+__device__ __forceinline__ void stage_rows(T* dst, const T* __restrict__ src, long long sn, int n, int d, int Np) {
+  constexpr int VE = 16 / sizeof(T);  // elements per 16-byte vector
+  const bool vec = (d == DP) && (sn % VE == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
+  if (vec) {
+    typedef __attribute__((__vector_size__(16))) int i32x4;
+    constexpr int CPR = DP / VE;  // vectors per row
+    for (int c = threadIdx.x; c < Np * CPR; c += blockDim.x) {
+      const int row = c / CPR, k = c - row * CPR;
+      i32x4 v = {0, 0, 0, 0};
+      if (row < n) v = *reinterpret_cast<const i32x4*>(src + (size_t)row * sn + k * VE);
+      *reinterpret_cast<i32x4*>(dst + (size_t)row * DP + k * VE) = v;
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < Np * DP; e += blockDim.x) {
     const int row = e / DP, col = e - row * DP;
     T v = from_f32<T>(0.f);
@@ -48,7 +65,27 @@ __device__ void stage_rows(T* dst, const T* __restrict__ src, long long sn, int 
 }
 // Transposed: dst[col][row], row stride Np.
 template <typename T, int DP>
-__device__ void stage_rows_t(T* dst, const T* __restrict__ src, long long sn, int n, int d, int Np) {
+__device__ __forceinline__ void stage_rows_t(T* dst, const T* __restrict__ src, long long sn, int n, int d, int Np) {
+  constexpr int VE = 16 / sizeof(T);
+  const bool vec = (d == DP) && (sn % VE == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
+  if (vec) {
+    constexpr int CPR = DP / VE;
+    for (int c = threadIdx.x; c < Np * CPR; c += blockDim.x) {
+      const int row = c % Np, k = c / Np;  // consecutive threads -> consecutive rows (LDS-friendly)
+      T v[VE];
+      if (row < n) {
+        const T* p = src + (size_t)row * sn + k * VE;
+#pragma unroll
+        for (int e = 0; e < VE; ++e) v[e] = p[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) v[e] = from_f32<T>(0.f);
+      }
+#pragma unroll
+      for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * Np + row] = v[e];
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < Np * DP; e += blockDim.x) {
     const int col = e / Np, row = e - col * Np;
     T v = from_f32<T>(0.f);
@@ -90,48 +127,108 @@ __device__ __forceinline__ int mask_setup(const float* mask, int N, unsigned cha
   return n;
 }
 
-// Gather a published vector and convert it into log2-unit LDS form, pinning
-// invalid entries (and the tail [n, Np)) to NEG_BIG.
-__device__ __forceinline__ bool gather_potential(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
-                                                 const unsigned char* valid, uint32_t* err, int* s_flag) {
-  if (!xch_gather<SK_NT>(buf, n, tag, dst, LOG2E, err, s_flag)) return false;
-  for (int i = threadIdx.x; i < Np; i += SK_NT)
-    if (i >= n || !valid[i]) dst[i] = NEG_BIG;
+// Gather a published potential vector [0, n) into dst (log2 units), writing
+// NEG_BIG for masked entries, and fold max |new - old| over valid entries into
+// *s_delta (float bits, >= 0; reset by the caller before a barrier that
+// precedes this call).  Entries [n, Np) are pinned once by the caller.
+// Returns false (uniformly) if the error flag is raised or a wait expires.
+template <int NT>
+__device__ __forceinline__ bool gather_potential(const uint64_t* buf, int n, uint32_t tag, float* dst,
+                                                 const unsigned char* valid, uint32_t* err, int* s_flag,
+                                                 unsigned* s_delta) {
+  const int t = threadIdx.x;
+  const uint32_t salt = tag >> 12;
+  bool ok = true;
+  float dmax = 0.f;
+  for (int base = 0; base < n && ok; base += 4 * NT) {
+    // words base + t + k*NT, k < cnt, owned by this thread
+    const int rem = n - base - t;
+    const int cnt = rem <= 0 ? 0 : min(4, (rem + NT - 1) / NT);
+    bool done[4] = {cnt <= 0, cnt <= 1, cnt <= 2, cnt <= 3};
+    uint32_t spins = 0;
+    while (!(done[0] && done[1] && done[2] && done[3])) {
+      uint64_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (!done[k])
+          w[k] = __hip_atomic_load(const_cast<uint64_t*>(buf + base + t + k * NT), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (!done[k] && (uint32_t)w[k] == tag) {
+          const int i = base + t + k * NT;
+          if (valid[i]) {
+            const float nv = __uint_as_float((uint32_t)(w[k] >> 32)) * LOG2E;
+            dmax = fmaxf(dmax, fabsf(nv - dst[i]));
+            dst[i] = nv;
+          } else {
+            dst[i] = NEG_BIG;
+          }
+          done[k] = true;
+        }
+      }
+      if (!(done[0] && done[1] && done[2] && done[3])) {
+        __builtin_amdgcn_s_sleep(1);  // back off: tight polling slows the publishers' stores
+        if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); ok = false; break; }
+        if ((spins & 255u) == 0u && error_raised(err, salt)) { ok = false; break; }
+      }
+    }
+  }
+  if (!ok) *s_flag = 1;
+  // NaN-safe: a NaN delta forces the online path
+  atomicMax(s_delta, dmax == dmax ? __float_as_uint(dmax) : 0x7f800000u);
   __syncthreads();
-  return true;
+  return *s_flag == 0;
 }
 
-// Online log2-sum-exp of x_ij = sc * <res_i, str_j> + w2_j (+ bias) over all
-// streamed rows j, for each resident row of tiles [rt0, rt0 + nr).  TRANS: the
-// streamed index is the plan's row index (column sweep), which matters only
-// for the bias.  lse2[q] (and mx2[q] if non-null) receive the result for local
-// resident row q in [0, nr*16).  Called by the whole block.
-template <typename T, int DP, bool GENERAL, bool TRANS>
-__device__ void lse_sweep(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
+// Log2-sum-exp of x_ij = sc * <res_i, str_j> + w2_j (+ bias) over all streamed
+// rows j, for each resident row of tiles [rt0, rt0 + nr).  TRANS: the streamed
+// index is the plan's row index (column sweep), which matters only for the bias.
+//   ONLINE = true : running max per lane (robust for any range); mx2 (if non-null)
+//                   receives the row maximum.
+//   ONLINE = false: fixed shift shift2[q] per resident row (caller guarantees
+//                   every exponent x - shift stays within fp32 range).
+// lse2[q] receives the result for local resident row q in [0, nr*16).
+// If publish != null, the threads that finish row q also call publish(q, lse2_q)
+// before the closing barrier.  *s_reset (if non-null) is zeroed between the two
+// barriers of each chunk.  Called by the whole block.
+template <int NT, typename T, int DP, bool GENERAL, bool TRANS, bool ONLINE, typename Pub>
+__device__ __forceinline__ void lse_sweep(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
                           const float* __restrict__ w2, int n_str_tiles, int rt0, int nr, float sc,
-                          const Bias& bias, float* lse2, float* mx2, float* scratch) {
+                          const Bias& bias, const float* __restrict__ shift2, float* lse2, float* mx2,
+                          float* scratch, unsigned* s_reset, Pub publish) {
   using M = Mfma<T, DP>;
+  constexpr int NW = NT / WAVE;
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int g = lane >> 4;
+  const float isc = 1.f / sc;
   for (int c0 = 0; c0 < nr; c0 += SK_RT) {
     const int nc = min(SK_RT, nr - c0);
     typename M::Frag bf[SK_RT];
-#pragma unroll
-    for (int r = 0; r < SK_RT; ++r)
-      if (r < nc) M::load(bf[r], res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
+    f32x4 cinit[SK_RT];
     float m[SK_RT], s[SK_RT];
 #pragma unroll
-    for (int r = 0; r < SK_RT; ++r) { m[r] = NEG_BIG; s[r] = 0.f; }
-    for (int st = wave; st < n_str_tiles; st += SK_NW) {
+    for (int r = 0; r < SK_RT; ++r) {
+      m[r] = NEG_BIG;
+      s[r] = 0.f;
+      cinit[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (r < nc) {
+        M::load(bf[r], res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
+        if (!ONLINE) {
+          const float ci = -shift2[(c0 + r) * 16 + (lane & 15)] * isc;
+          cinit[r] = f32x4{ci, ci, ci, ci};
+        }
+      }
+    }
+    for (int st = wave; st < n_str_tiles; st += NW) {
       typename M::Frag af;
       M::load(af, str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
       const f32x4 w = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
 #pragma unroll
       for (int r = 0; r < SK_RT; ++r) {
         if (r < nc) {
-          const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-          const f32x4 acc = M::qk(af, bf[r], zero);
+          const f32x4 acc = M::qk(af, bf[r], cinit[r]);
           float x[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
@@ -142,47 +239,81 @@ __device__ void lse_sweep(const T* __restrict__ res_lds, const T* __restrict__ s
               if (w[k] > 0.5f * NEG_BIG) x[k] += TRANS ? bias(jstr, ires) : bias(ires, jstr);
             }
           }
-          const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-          const float mn = fmaxf(m[r], tm);
-          float acc_s = s[r] * fast_exp2(m[r] - mn);
+          if (ONLINE) {
+            const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+            const float mn = fmaxf(m[r], tm);
+            float acc_s = s[r] * fast_exp2(m[r] - mn);
 #pragma unroll
-          for (int k = 0; k < 4; ++k) acc_s += fast_exp2(x[k] - mn);
-          s[r] = acc_s;
-          m[r] = mn;
+            for (int k = 0; k < 4; ++k) acc_s += fast_exp2(x[k] - mn);
+            s[r] = acc_s;
+            m[r] = mn;
+          } else {
+            s[r] += (fast_exp2(x[0]) + fast_exp2(x[1])) + (fast_exp2(x[2]) + fast_exp2(x[3]));
+          }
         }
       }
     }
 #pragma unroll
     for (int r = 0; r < SK_RT; ++r) {
       if (r < nc) {
-        const float mm = max_groups(m[r]);
-        const float ss = sum_groups(s[r] * fast_exp2(m[r] - mm));
+        float mm = 0.f, ss;
+        if (ONLINE) {
+          mm = max_groups(m[r]);
+          ss = sum_groups(s[r] * fast_exp2(m[r] - mm));
+        } else {
+          ss = sum_groups(s[r]);
+        }
         if (lane < 16) {
           scratch[(wave * SK_RT + r) * 16 + lane] = mm;
-          scratch[SK_NW * SK_RT * 16 + (wave * SK_RT + r) * 16 + lane] = ss;
+          scratch[NW * SK_RT * 16 + (wave * SK_RT + r) * 16 + lane] = ss;
         }
       }
     }
     __syncthreads();
+    if (s_reset && threadIdx.x == 0) *s_reset = 0u;
     if ((int)threadIdx.x < nc * 16) {
       const int q = threadIdx.x;
       const int r = q >> 4, l = q & 15;
-      float mm = NEG_BIG;
+      float res;
+      if (ONLINE) {
+        float mm = NEG_BIG;
 #pragma unroll
-      for (int w = 0; w < SK_NW; ++w) mm = fmaxf(mm, scratch[(w * SK_RT + r) * 16 + l]);
-      float ss = 0.f;
+        for (int w = 0; w < NW; ++w) mm = fmaxf(mm, scratch[(w * SK_RT + r) * 16 + l]);
+        float ss = 0.f;
 #pragma unroll
-      for (int w = 0; w < SK_NW; ++w)
-        ss += scratch[SK_NW * SK_RT * 16 + (w * SK_RT + r) * 16 + l] * fast_exp2(scratch[(w * SK_RT + r) * 16 + l] - mm);
-      lse2[c0 * 16 + q] = mm + fast_log2(ss);
-      if (mx2) mx2[c0 * 16 + q] = mm;
+        for (int w = 0; w < NW; ++w)
+          ss += scratch[NW * SK_RT * 16 + (w * SK_RT + r) * 16 + l] * fast_exp2(scratch[(w * SK_RT + r) * 16 + l] - mm);
+        res = mm + fast_log2(ss);
+        if (mx2) mx2[c0 * 16 + q] = mm;
+      } else {
+        float ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) ss += scratch[NW * SK_RT * 16 + (w * SK_RT + r) * 16 + l];
+        res = shift2[c0 * 16 + q] + fast_log2(ss);
+      }
+      lse2[c0 * 16 + q] = res;
+      publish(c0 * 16 + q, res);
     }
     __syncthreads();
   }
 }
 
-// Scratch floats needed by lse_sweep.
-constexpr int LSE_SCRATCH = 2 * SK_NW * SK_RT * 16;
+struct NoPublish {
+  __device__ __forceinline__ void operator()(int, float) const {}
+};
+
+// Workgroup -> (group, member).  Workgroups are dispatched round-robin over the
+// 8 XCDs (id % 8), so the members of one group are taken from a single XCD:
+// local index l = id / 8 on XCD x = id % 8, slot s = l / G, member = l % G,
+// group = 8 s + x.  Exchanges between workgroups of one XCD measured ~2.5x
+// faster than across XCDs; the mapping affects speed only, never correctness.
+// Returns false for surplus workgroups (group >= n_groups), which own nothing.
+__device__ __forceinline__ bool group_of(int n_groups, int G, int& group, int& member) {
+  const int id = blockIdx.x, x = id & 7, l = id >> 3;
+  member = l % G;
+  group = 8 * (l / G) + x;
+  return group < n_groups;
+}
 
 // Stripe of 16-row tiles owned by `member` out of G.
 __device__ __forceinline__ void stripe(int n_tiles, int member, int G, int& t0, int& t1) {

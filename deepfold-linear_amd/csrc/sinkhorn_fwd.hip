@@ -22,18 +22,39 @@
 
 namespace dfl {
 
+constexpr int FWD_NT = 512;  // 8 waves: two per SIMD for latency hiding
+constexpr int FWD_NW = FWD_NT / WAVE;
+// Largest |change| of a potential between two sweeps (log2 units) for which the
+// previous LSE is used as the exponent shift: every term is then <= 2^delta and
+// the sum >= 2^-delta, far inside fp32 range.
+constexpr float FIXED_SHIFT_MAX_DELTA = 64.f;
+
 __host__ __device__ inline int fwd_local_rows(int N, int G) { return 16 * (((N + 15) / 16 + G - 1) / G); }
 
+template <typename T, int DP, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void fwd_sweep(bool online, const T* res, const T* str, const float* w2, int n_tiles,
+                                          int t0, int nr, float sc, const Bias& bias, float* lse, float* mx,
+                                          float* scratch, unsigned* s_reset, Pub pub) {
+  if (online)
+    lse_sweep<FWD_NT, T, DP, GENERAL, TRANS, true>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, lse, mx, scratch,
+                                                   s_reset, pub);
+  else
+    lse_sweep<FWD_NT, T, DP, GENERAL, TRANS, false>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, lse, mx, scratch,
+                                                    s_reset, pub);
+}
+
 template <typename T, int DP>
-__global__ void __launch_bounds__(SK_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
+__global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_flag, s_tmp;
+  __shared__ unsigned s_du, s_dv;
   __shared__ float s_posw[68];
-  const int grp = blockIdx.x / a.G, member = blockIdx.x % a.G;
+  int grp, member;
+  if (!group_of(a.B * a.H, a.G, grp, member)) return;  // surplus workgroup of the XCD-aligned grid
   const int b = grp / a.H, h = grp % a.H;
   const int N = a.N, d = a.d;
   const int Np = ((N + 31) / 32) * 32;
-  if (threadIdx.x == 0) s_flag = 0;
+  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; }
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
@@ -45,9 +66,12 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   float* vecV = vecU + Np;                                         // v of all columns (log2)
   float* xs = vecV + Np;                                           // [Np][3]
   const int loc = fwd_local_rows(N, a.G);
-  float* lse2 = xs + 3 * Np;
-  float* mx2 = lse2 + loc;
-  float* scratch = mx2 + loc;
+  float* lse_r = xs + 3 * Np;   // row LSE of my rows (log2); shift of the next row sweep
+  float* lse_c = lse_r + loc;   // column LSE of my columns (log2)
+  float* mx2 = lse_c + loc;     // row maxima of the final sweep
+  float* lmu_l = mx2 + loc;     // log mu of my rows
+  float* lnu_l = lmu_l + loc;   // log nu of my columns
+  float* scratch = lnu_l + loc;
 
   const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &s_tmp);
   const int n_tiles = (n + 15) / 16;
@@ -68,9 +92,13 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const float kappa = a.lam / (a.lam + eps);
   const float sc = LOG2E / (sqrtf((float)d) * eps);
   const size_t bh = (size_t)b * a.H + h;
-  const float* lmu = a.log_mu + bh * N;
-  const float* lnu = a.log_nu + bh * N;
-  for (int i = threadIdx.x; i < Np; i += SK_NT) {
+  const int r_lo = t0 * 16;
+  for (int q = threadIdx.x; q < nr * 16; q += FWD_NT) {
+    const int i = r_lo + q;
+    lmu_l[q] = i < n ? a.log_mu[bh * N + i] : 0.f;
+    lnu_l[q] = i < n ? a.log_nu[bh * N + i] : 0.f;
+  }
+  for (int i = threadIdx.x; i < Np; i += FWD_NT) {
     const bool ok = i < n && valid[i];
     vecU[i] = ok ? (a.u_init ? a.u_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
     vecV[i] = ok ? (a.v_init ? a.v_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
@@ -79,8 +107,8 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const bool use_geo = (a.x != nullptr) && (w_h != 0.f);
   const bool use_pos = (a.bins != nullptr) && (a.pos_w != nullptr);
   if (use_pos)
-    for (int k = threadIdx.x; k < 68; k += SK_NT) s_posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
-  for (int e = threadIdx.x; e < 3 * Np; e += SK_NT) xs[e] = (a.x && e < 3 * n) ? a.x[(size_t)b * N * 3 + e] : 0.f;
+    for (int k = threadIdx.x; k < 68; k += FWD_NT) s_posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
+  for (int e = threadIdx.x; e < 3 * Np; e += FWD_NT) xs[e] = (a.x && e < 3 * n) ? a.x[(size_t)b * N * 3 + e] : 0.f;
   __syncthreads();
   Bias bias;
   bias.bins = use_pos ? a.bins + (size_t)b * N * N : nullptr;
@@ -95,36 +123,52 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   uint64_t* xv = xu + Np;                       // v words
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
-  const int r_lo = t0 * 16, r_hi = min(t1 * 16, n);
 
   for (int it = 0; it < a.K_iter; ++it) {
-    // ---- row update: u_i for rows of my stripe
-    if (general) lse_sweep<T, DP, true, false>(QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse2, nullptr, scratch);
-    else lse_sweep<T, DP, false, false>(QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse2, nullptr, scratch);
+    // ---- row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j)) for my rows
     ++phase;
-    for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += SK_NT)
-      xch_put(xu + i, kappa * (lmu[i] - lse2[i - r_lo] * LN2), salt | phase);
-    if (!gather_potential(xu, n, Np, salt | phase, vecU, valid, a.err, &s_flag)) return;
-    // ---- column update: v_j for columns of my stripe
-    if (general) lse_sweep<T, DP, true, true>(KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse2, nullptr, scratch);
-    else lse_sweep<T, DP, false, true>(KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse2, nullptr, scratch);
-    ++phase;
-    for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += SK_NT) {
-      xch_put(xv + j, kappa * (lnu[j] - lse2[j - r_lo] * LN2), salt | phase);
-      if (it == a.K_iter - 1 && valid[j]) a.col_lse[bh * N + j] = lse2[j - r_lo] * LN2;
+    {
+      const uint32_t tag = salt | phase;
+      const bool online = it == 0 || __uint_as_float(s_dv) > FIXED_SHIFT_MAX_DELTA;
+      auto pub = [&](int q, float l2) {
+        const int i = r_lo + q;
+        if (i < n) xch_put(xu + i, kappa * (lmu_l[q] - l2 * LN2), tag);
+      };
+      if (general) fwd_sweep<T, DP, true, false>(online, QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse_r, nullptr, scratch, &s_du, pub);
+      else fwd_sweep<T, DP, false, false>(online, QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse_r, nullptr, scratch, &s_du, pub);
+      if (!gather_potential<FWD_NT>(xu, n, tag, vecU, valid, a.err, &s_flag, &s_du)) return;
     }
-    if (!gather_potential(xv, n, Np, salt | phase, vecV, valid, a.err, &s_flag)) return;
+    // ---- column update: v_j = kappa (log nu_j - LSE_i(L_ij + u_i)) for my columns
+    ++phase;
+    {
+      const uint32_t tag = salt | phase;
+      const bool online = it == 0 || __uint_as_float(s_du) > FIXED_SHIFT_MAX_DELTA;
+      const bool last = it == a.K_iter - 1;
+      auto pub = [&](int q, float l2) {
+        const int j = r_lo + q;
+        if (j < n) {
+          xch_put(xv + j, kappa * (lnu_l[q] - l2 * LN2), tag);
+          if (last && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
+        }
+      };
+      if (general) fwd_sweep<T, DP, true, true>(online, KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse_c, nullptr, scratch, &s_dv, pub);
+      else fwd_sweep<T, DP, false, true>(online, KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse_c, nullptr, scratch, &s_dv, pub);
+      if (!gather_potential<FWD_NT>(xv, n, tag, vecV, valid, a.err, &s_flag, &s_dv)) return;
+    }
   }
   if (a.K_iter == 0) {
-    if (general) lse_sweep<T, DP, true, true>(KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse2, nullptr, scratch);
-    else lse_sweep<T, DP, false, true>(KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse2, nullptr, scratch);
-    for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += SK_NT)
-      if (valid[j]) a.col_lse[bh * N + j] = lse2[j - r_lo] * LN2;
+    auto pub = [&](int q, float l2) {
+      const int j = r_lo + q;
+      if (j < n && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
+    };
+    if (general) fwd_sweep<T, DP, true, true>(true, KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse_c, nullptr, scratch, nullptr, pub);
+    else fwd_sweep<T, DP, false, true>(true, KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse_c, nullptr, scratch, nullptr, pub);
   }
 
   // ---- final row LSE with the last v: exact log Z and the row maximum
-  if (general) lse_sweep<T, DP, true, false>(QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse2, mx2, scratch);
-  else lse_sweep<T, DP, false, false>(QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse2, mx2, scratch);
+  if (general) fwd_sweep<T, DP, true, false>(true, QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse_r, mx2, scratch, nullptr, NoPublish());
+  else fwd_sweep<T, DP, false, false>(true, QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse_r, mx2, scratch, nullptr, NoPublish());
+  float* lse2 = lse_r;
 
   // ---- transport output for my rows: O_avg = T_norm V, x_c = T_norm x.
   // V^T replaces Q in LDS; resident Q fragments are read from global memory.
@@ -137,7 +181,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   __syncthreads();
   const int n_pairs = (n_tiles + 1) / 2;
   constexpr int NC = DP / 16;
-  for (int rt = wave; rt < nr; rt += SK_NW) {
+  for (int rt = wave; rt < nr; rt += FWD_NW) {
     const int tile = t0 + rt;
     const int qloc = rt * 16;
     const int irow = tile * 16 + (lane & 15);  // this lane's row in the P layout
@@ -219,8 +263,8 @@ size_t sinkhorn_fwd_lds_bytes(int N, int DP, int elem, int G) {
   size_t bytes = ((Np + 15) / 16) * 16;               // valid
   bytes += 2 * Np * DP * elem;                        // QS, KS
   bytes += (2 * Np + 3 * Np) * 4;                     // vecU, vecV, xs
-  bytes += (size_t)2 * fwd_local_rows(N, G) * 4;      // lse2, mx2
-  bytes += (size_t)LSE_SCRATCH * 4;                   // scratch
+  bytes += (size_t)5 * fwd_local_rows(N, G) * 4;      // lse_r, lse_c, mx2, lmu_l, lnu_l
+  bytes += (size_t)sweep_scratch<FWD_NT>() * 4;       // scratch
   return bytes;
 }
 
@@ -229,7 +273,7 @@ static hipError_t launch_fwd_t(const SinkFwdArgs& a, size_t lds, hipStream_t str
   auto kern = sinkhorn_fwd_kernel<T, DP>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  dim3 grid(a.B * a.H * a.G), block(SK_NT);
+  dim3 grid(grid_blocks(a.B * a.H, a.G)), block(FWD_NT);
   SinkFwdArgs copy = a;
   if (coop) {
     void* args[] = {&copy};

@@ -141,6 +141,25 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+# Optional per-launch timing: when a list is installed here, every C-ABI launch
+# appends (name, start_event, end_event) recorded on the launch stream.
+launch_timings: list | None = None
+
+
+def timed_launch(name: str, device: torch.device, fn):
+    """Run ``fn()`` (one C-ABI call), bracketing it with events if timing is on."""
+    if launch_timings is None:
+        return fn()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream(device)
+    s.record(stream)
+    rc = fn()
+    e.record(stream)
+    launch_timings.append((name, s, e))
+    return rc
+
+
 def debug_checks() -> bool:
     return os.environ.get("DFL_AMD_CHECK", "0") not in ("", "0")
 

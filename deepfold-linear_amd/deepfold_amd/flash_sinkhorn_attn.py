@@ -100,8 +100,8 @@ class FlashSinkhornAttn(torch.autograd.Function):
             B, H, N, d, int(K_iter), float(lam), float(r_0),
             o_flat.data_ptr(), x_c.data_ptr(), log_u.data_ptr(), log_v.data_ptr(),
             o_avg.data_ptr(), log_z.data_ptr(), col_lse.data_ptr())
-        rc = lib.dfl_sinkhorn_fwd(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
-                                  ctypes.c_void_p(_lib.stream_handle(dev)))
+        rc = _lib.timed_launch("sinkhorn_fwd", dev, lambda: lib.dfl_sinkhorn_fwd(
+            ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
         _lib.check(rc, "dfl_sinkhorn_fwd")
         if _lib.debug_checks():
             _lib.check_workspace(ws, "dfl_sinkhorn_fwd")
@@ -135,9 +135,13 @@ class FlashSinkhornAttn(torch.autograd.Function):
         dg = torch.zeros(B, H, N, d, **f32)
         dlmu = torch.zeros(B, H, N, **f32)
         dlnu = torch.zeros(B, H, N, **f32)
-        dx = torch.zeros(B, N, 3, **f32)
-        dpw = torch.zeros(H, 68, **f32)
-        dw = torch.zeros(H, **f32)
+        # optional outputs: NULL skips their per-element work in the kernel
+        need_dx = x is not None and ctx.needs_input_grad[4]
+        need_dpw = pw is not None and ctx.needs_input_grad[5]
+        need_dw = wd is not None and ctx.needs_input_grad[8]
+        dx = torch.zeros(B, N, 3, **f32) if need_dx else None
+        dpw = torch.zeros(H, 68, **f32) if need_dpw else None
+        dw = torch.zeros(H, **f32) if need_dw else None
         lib = _lib.load()
         ws = _lib.workspace(dev, lib.dfl_sinkhorn_workspace_size(B, H, N))
         sb, sh, sn, _ = q.stride()
@@ -152,14 +156,15 @@ class FlashSinkhornAttn(torch.autograd.Function):
             B, H, N, d, lam, r_0,
             _SOLVERS[solver], iters, _MODES[mode], rtol,
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
-            dlmu.data_ptr(), dlnu.data_ptr(), dx.data_ptr(), dpw.data_ptr(), dw.data_ptr())
-        rc = lib.dfl_sinkhorn_bwd(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
-                                  ctypes.c_void_p(_lib.stream_handle(dev)))
+            dlmu.data_ptr(), dlnu.data_ptr(),
+            _lib.ptr(dx) if need_dx else None, _lib.ptr(dpw) if need_dpw else None,
+            _lib.ptr(dw) if need_dw else None)
+        rc = _lib.timed_launch("sinkhorn_bwd", dev, lambda: lib.dfl_sinkhorn_bwd(
+            ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
         _lib.check(rc, "dfl_sinkhorn_bwd")
         if _lib.debug_checks():
             _lib.check_workspace(ws, "dfl_sinkhorn_bwd")
-        return ((dq, dk, dv, dg if has_g else None, dx if x is not None else None,
-                 dpw if pw is not None else None, None, None, dw if wd is not None else None,
+        return ((dq, dk, dv, dg if has_g else None, dx, dpw, None, None, dw,
                  dlmu, dlnu, None, None, None, None, None, None) + (None,) * n_opts)
 
 
