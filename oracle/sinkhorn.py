@@ -405,7 +405,7 @@ def backward_masked(fwd_inputs: dict, grad_o_flat, grad_xc=None, mode="reference
                 sl[k] = np.asarray(v)[b:b + 1, :, :n]
             else:
                 sl[k] = np.asarray(v)[b:b + 1, :, :n]
-        f1 = forward(**{kk: sl[kk] for kk in ("K_iter", "lam", "r_0")},
+        f1 = forward(**{kk: sl[kk] for kk in ("K_iter", "lam", "r_0") if kk in sl},
                      Q=sl["Q"], K=sl["K"], V=sl["V"], G=sl["G"], x_res=sl["x_res"],
                      pos_weight=sl["pos_weight"], pos_bins=sl.get("pos_bins"), eps=sl["eps"],
                      w_dist=sl["w_dist"], log_mu=sl["log_mu"], log_nu=sl["log_nu"],

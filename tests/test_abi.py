@@ -1,0 +1,134 @@
+"""CPU checks of the C ABI and the host side (no GPU, no kernel launches).
+
+* libdfl_amd.so loads and exports every function include/dfl_amd.h declares, and
+  the ctypes binding lists exactly those functions;
+* the ctypes mirrors of the parameter structs have the C layout (offsets and
+  sizes printed by a probe compiled with gcc against the header);
+* the public op refuses CPU tensors (there is no CPU fallback);
+* bench.py refuses more than one GPU.
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+import tempfile
+
+import pytest
+
+from conftest import PKG_ROOT, ROOT
+
+HEADER = os.path.join(ROOT, "include", "dfl_amd.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dfl_\w+)\s*\(", text)))
+
+
+def header_structs():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for body, name in re.findall(r"typedef struct \w+ \{(.*?)\} (\w+);", text, flags=re.S):
+        fields = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            head, names = re.match(r"(.*?[\s*])(\w+(?:\s*,\s*\w+)*)$", decl).groups()
+            fields += [n.strip() for n in names.split(",")]
+        out[name] = fields
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib_path():
+    from deepfold_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):  # build it (hipcc cross-compiles without a GPU)
+        sys.path.insert(0, PKG_ROOT)
+        import build_lib
+
+        build_lib.build(verbose=False)
+    return _lib.LIB_PATH
+
+
+def test_library_exports_every_header_function(lib_path):
+    lib = ctypes.CDLL(lib_path)
+    names = header_functions()
+    assert "dfl_sinkhorn_fwd" in names and "dfl_sinkhorn_bwd" in names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    nm = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True, text=True)
+    exported = set(re.findall(r"\bT (dfl_\w+)$", nm.stdout, flags=re.M))
+    assert exported == set(names), f"extra exports: {exported - set(names)}"
+
+
+def test_binding_matches_header(lib_path):
+    from deepfold_amd import _lib
+
+    assert sorted(n for n, _, _ in _lib.SIGNATURES) == header_functions()
+    lib = _lib.load(lib_path)
+    assert lib.dfl_version().decode().startswith("deepfold_amd")
+
+
+def test_struct_layout_matches_c(lib_path):
+    from deepfold_amd import _lib
+
+    structs = header_structs()
+    mirrors = {"dfl_sinkhorn_fwd_params": _lib.SinkhornFwdParams,
+               "dfl_sinkhorn_bwd_params": _lib.SinkhornBwdParams}
+    assert set(mirrors) == set(structs)
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for sname, fields in structs.items():
+        lines.append(f'  printf("{sname} size %zu\\n", sizeof({sname}));')
+        for f in fields:
+            lines.append(f'  printf("{sname} {f} %zu\\n", offsetof({sname}, {f}));')
+    lines += ["  return 0;", "}"]
+    with tempfile.TemporaryDirectory() as td:
+        src, exe = os.path.join(td, "probe.c"), os.path.join(td, "probe")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-std=c99", "-o", exe, src], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    c_layout = {}
+    for line in out.splitlines():
+        s, f, v = line.split()
+        c_layout[(s, f)] = int(v)
+    for sname, cls in mirrors.items():
+        py_fields = [f for f, _ in cls._fields_]
+        assert py_fields == structs[sname], sname
+        assert ctypes.sizeof(cls) == c_layout[(sname, "size")], sname
+        for f in py_fields:
+            assert getattr(cls, f).offset == c_layout[(sname, f)], (sname, f)
+
+
+def test_op_refuses_cpu_tensors():
+    import torch
+    from deepfold_amd import flash_sinkhorn_attn
+
+    B, H, N, d = 1, 2, 8, 4
+    q = torch.randn(B, H, N, d)
+    with pytest.raises(RuntimeError, match="GPU"):
+        flash_sinkhorn_attn(q, q, q, q, torch.zeros(B, N, 3), torch.zeros(H, 68), None, torch.ones(H),
+                            torch.zeros(H), torch.zeros(B, H, N), torch.zeros(B, H, N))
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    from deepfold_amd import _lib
+
+    saved = _lib._lib
+    _lib._lib = None
+    try:
+        with pytest.raises(RuntimeError, match="not built"):
+            _lib.load(str(tmp_path / "absent.so"))
+    finally:
+        _lib._lib = saved
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
