@@ -86,11 +86,23 @@ def algorithmic_counts(lengths):
     return E, f_fwd, f_bwd, x_fwd, x_bwd
 
 
-def cpu_baseline(cpu, budget_s=20.0):
+def profiled_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a copy kernel), or None."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", "sinkhorn_cfg2_bench.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(rf"^\s*{kernel} hbm_bytes_per_launch = (\d+)", open(path).read(), flags=re.M)
+    return int(m.group(1)) if m else None
+
+
+def cpu_baseline(cpu, budget_s=12.0):
     """Time the numpy oracle (float32, one thread) on a bounded sample of the
     layer: full forward (K=50) + reference fixed-point IFT backward (50 sweeps)
-    of whole (b, h) heads, stopping once ~budget_s of CPU time is spent, then
-    scaled to the B*H heads of the layer."""
+    of whole (b, h) heads, cycling over the heads until ~budget_s of CPU time is
+    spent, then scaled by plan elements to one layer (B*H heads)."""
     import numpy as np
 
     try:
@@ -105,7 +117,7 @@ def cpu_baseline(cpu, budget_s=20.0):
     spent, sampled, heads = 0.0, 0, []
     ctx = threadpool_limits(limits=1) if threadpool_limits else None
     try:
-        order = [(b, h) for h in range(H) for b in range(B)]  # alternate samples
+        order = [(b, h) for h in range(H) for b in range(B)] * 64  # alternate samples
         for b, h in order:
             n = lengths[b]
             sl = lambda a: a[b:b + 1, h:h + 1, :n].float().numpy()
@@ -132,8 +144,8 @@ def cpu_baseline(cpu, budget_s=20.0):
     e_smp = sum(lengths[b] ** 2 for b, _ in heads)
     return dict(value=round(spent * e_all / e_smp * 1e3, 1), unit="ms/layer", cores=1, kind="port",
                 sample=f"numpy oracle (float32, 1 thread): dense forward K={CFG['K_iter']} + reference "
-                       f"fixed-point IFT backward ({CFG['K_iter']} sweeps) on {sampled} of {B * H} (b,h) heads "
-                       f"({spent:.1f} s), extrapolated by valid plan elements")
+                       f"fixed-point IFT backward ({CFG['K_iter']} sweeps), {sampled} (b,h) head solves cycling "
+                       f"over the layer's {B * H} heads ({spent:.1f} s), scaled to one layer by valid plan elements")
 
 
 def main():
@@ -142,6 +154,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB -> 256 MiB elementwise copy (torch.neg), used to "
+                         "calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the flash-Sinkhorn "
@@ -154,6 +169,16 @@ def main():
 
     os.environ["DFL_AMD_CHECK"] = "0"
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        n = 64 << 20  # float32 elements: 256 MiB read + 256 MiB written per launch
+        a = torch.ones(n, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy": {"kernel": "torch.neg", "launches": 5, "read_bytes": 4 * n,
+                                             "write_bytes": 4 * n}}), flush=True)
+        return
     cpu, t = make_workload(dev)
     for _ in range(args.warmup):
         step(t)
@@ -180,11 +205,7 @@ def main():
     f_dom = f_fwd if dom == "sinkhorn_fwd" else f_bwd
     x_dom = x_fwd if dom == "sinkhorn_fwd" else x_bwd
     achieved = f_dom / (avg[dom] * 1e-3)
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"{dom}_cfg2_traffic.json")
-    if os.path.exists(tfile):
-        with open(tfile) as fh:
-            traffic = json.load(fh).get("hbm_bytes_per_launch")
+    traffic = profiled_traffic(dom)
     t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
 
     out = {

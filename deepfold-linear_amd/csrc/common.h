@@ -162,6 +162,27 @@ __device__ __forceinline__ float max_groups(float x) {
   return x;
 }
 
+// Unsigned maximum over the 64 lanes of a wave; every lane must be active.
+// Four DPP steps reduce each 16-lane row, four readlanes combine the rows.  (An
+// atomicMax on one LDS word from every lane compiles to a 64-step readlane loop
+// per wave, which measured ~2 us for a 512-thread block.)
+__device__ __forceinline__ unsigned wave_max_u32(unsigned x) {
+  x = max(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  x = max(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  x = max(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  x = max(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xf, 0xf, false));  // row_mirror
+  const unsigned r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
+  const unsigned r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+// *s = max(*s, x) over the whole block (LDS word); one atomic per wave.
+// Called by every thread of the block (full waves).
+__device__ __forceinline__ void block_atomic_max_u32(unsigned* s, unsigned x) {
+  const unsigned w = wave_max_u32(x);
+  if ((threadIdx.x & (WAVE - 1)) == 0) atomicMax(s, w);
+}
+
 // ---------------------------------------------------------------------------
 // Error flag and tagged exchange.
 constexpr uint32_t SPIN_LIMIT = 1u << 22;  // ~2-4 s of polling

@@ -114,13 +114,13 @@ __device__ __forceinline__ void load_frag_global(typename Mfma<T, DP>::Frag& f, 
 __device__ __forceinline__ int mask_setup(const float* mask, int N, unsigned char* valid, int* s_tmp) {
   if (threadIdx.x == 0) *s_tmp = 0;
   __syncthreads();
-  int hi = 0;
+  unsigned hi = 0;
   for (int i = threadIdx.x; i < N; i += blockDim.x) {
     const bool ok = mask ? (mask[i] > 0.5f) : true;
     valid[i] = ok ? 1 : 0;
     if (ok) hi = i + 1;
   }
-  atomicMax(s_tmp, hi);
+  block_atomic_max_u32(reinterpret_cast<unsigned*>(s_tmp), hi);
   __syncthreads();
   const int n = *s_tmp;
   __syncthreads();
@@ -176,7 +176,7 @@ __device__ __forceinline__ bool gather_potential(const uint64_t* buf, int n, uin
   }
   if (!ok) *s_flag = 1;
   // NaN-safe: a NaN delta forces the online path
-  atomicMax(s_delta, dmax == dmax ? __float_as_uint(dmax) : 0x7f800000u);
+  block_atomic_max_u32(s_delta, dmax == dmax ? __float_as_uint(dmax) : 0x7f800000u);
   __syncthreads();
   return *s_flag == 0;
 }
