@@ -18,6 +18,7 @@ hipError_t launch_sinkhorn_fwd(const SinkFwdArgs& a, bool bf16_in, int DP, size_
 size_t sinkhorn_bwd_lds_bytes(int N, int DP, int elem, int G);
 hipError_t launch_sinkhorn_bwd(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                bool coop);
+hipError_t launch_sinkhorn_bwd_prep(const SinkBwdArgs& a, bool bf16_in, int DP, hipStream_t stream);
 hipError_t launch_sinkhorn_bwd_finalize(const SinkBwdArgs& a, float* dx, float* dpw, float* dw,
                                         hipStream_t stream);
 }  // namespace dfl
@@ -86,6 +87,16 @@ int group_size(int B, int H, int N) {
   return G;
 }
 
+// Backward partials: dx (B,H,N,3), dpw (B*H*G,68), dw (B*H*G), rounded to 256 bytes.
+size_t partials_bytes(int B, int H, int N, int G) {
+  const size_t b = (size_t)B * H * N * 3 * 4 + (size_t)B * H * G * 69 * 4;
+  return (b + 255) / 256 * 256;
+}
+
+// Prepared backward operands, sized for the widest case (d <= 64, fp32):
+// go_hi, go_lo, go_t of B*H*Np*64 elements each, then D (B*H*Np floats).
+size_t prep_operand_bytes(int B, int H, int N) { return (size_t)B * H * np32(N) * 64 * 4; }
+
 }  // namespace
 
 extern "C" {
@@ -98,8 +109,8 @@ size_t dfl_sinkhorn_workspace_size(int B, int H, int N) {
   if (B <= 0 || H <= 0 || N <= 0) return 0;
   const int G = group_size(B, H, N);
   size_t bytes = WS_HEADER + xch_words(B, H, N) * 8;
-  // backward partials: dx (B,H,N,3), dpw (B*H*G,68), dw (B*H*G)
-  bytes += (size_t)B * H * N * 3 * 4 + (size_t)B * H * G * 69 * 4;
+  bytes += partials_bytes(B, H, N, G);
+  bytes += 3 * prep_operand_bytes(B, H, N) + (size_t)B * H * np32(N) * 4;
   return (bytes + 255) / 256 * 256;
 }
 
@@ -198,14 +209,23 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   a.err = reinterpret_cast<uint32_t*>(ws);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
-  float* parts = reinterpret_cast<float*>(ws + WS_HEADER + xch_words(p->B, p->H, p->N) * 8);
+  unsigned char* cur = ws + WS_HEADER + xch_words(p->B, p->H, p->N) * 8;
+  float* parts = reinterpret_cast<float*>(cur);
   a.dx_part = parts;
   a.dpw_part = parts + (size_t)p->B * p->H * p->N * 3;
   a.dw_part = a.dpw_part + (size_t)p->B * p->H * G * 68;
+  cur += partials_bytes(p->B, p->H, p->N, G);
+  const size_t opb = prep_operand_bytes(p->B, p->H, p->N);
+  a.go_hi = cur;
+  a.go_lo = cur + opb;
+  a.go_t = cur + 2 * opb;
+  a.dcoef = reinterpret_cast<float*>(cur + 3 * opb);
   a.G = G;
   a.salt = next_salt();
   const bool coop = G > 1;
-  hipError_t e = dfl::launch_sinkhorn_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  hipError_t e = dfl::launch_sinkhorn_bwd_prep(a, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "sinkhorn backward prep launch");
+  e = dfl::launch_sinkhorn_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward launch");
   e = dfl::launch_sinkhorn_bwd_finalize(a, p->dx_res, p->dpos_weight, p->dw_dist, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward finalize launch");

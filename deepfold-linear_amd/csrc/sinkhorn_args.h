@@ -83,6 +83,11 @@ struct SinkBwdArgs {
   // workspace
   uint64_t* xch;  // B*H*4*Np exchange words
   uint32_t* err;
+  // prepared by the prep kernel (per (b,h), Np rows, zero on invalid rows / padded columns):
+  void* go_hi;    // [B*H][Np][DP]  T(gO), gO = sigma(G) * dO
+  void* go_lo;    // [B*H][Np][DP]  T(gO - T(gO)) (bf16 inputs only)
+  void* go_t;     // [B*H][DP][Np]  T(gO) transposed
+  float* dcoef;   // [B*H][Np]      D_i = gO_i.O_avg_i + dxc_i.xc_i
   int G;
   uint32_t salt;
 };

@@ -36,7 +36,7 @@ namespace dfl {
 // light sweep: out[q] = sum_j exp2(sc*<res_q, str_j> + cres[q] + w2_j (+bias)) * z_j
 // Every exponent is <= 0 here (S_col, T and W are bounded by 1), so no shift.
 template <typename T, int DP, bool GENERAL, bool TRANS>
-__device__ void light_sweep(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
+__device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
                             const float* __restrict__ w2, const float* __restrict__ zv, int n_str_tiles, int rt0,
                             int nr, float sc, const float* __restrict__ cres, const Bias& bias, float* out,
                             float* scratch) {
@@ -101,7 +101,7 @@ __device__ void light_sweep(const T* __restrict__ res_lds, const T* __restrict__
 
 // Deterministic block-wide sum of f(i) over i in [0, n) (same order in every block).
 template <typename F>
-__device__ float block_sum(int n, F f, float* red) {
+__device__ __forceinline__ float block_sum(int n, F f, float* red) {
   float acc = 0.f;
   for (int i = threadIdx.x; i < n; i += SK_NT) acc += f(i);
 #pragma unroll
@@ -129,33 +129,80 @@ __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np
 
 __device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// Stage chunk rows [r0, r0 + CH) of gO = sigma(G) * dO into LDS (row-major
-// [CH][DP] if !TRANSP, else transposed [DP][CH]).  LO: store the rounding
-// residual gO - T(gO) instead (the low half of a hi + lo pair).
-template <typename T, int DP, bool TRANSP, bool LO = false>
-__device__ void stage_gO(T* dst, const T* __restrict__ Gg, long long sn, const float* __restrict__ go,
-                         long long go_row, int r0, int CH, int n, int d) {
-  for (int e = threadIdx.x; e < CH * DP; e += SK_NT) {
-    int row, col;
-    if (TRANSP) { col = e / CH; row = e - col * CH; }
-    else { row = e / DP; col = e - row * DP; }
-    const int i = r0 + row;
-    float v = 0.f;
-    if (i < n && col < d) v = (Gg ? sigm(to_f32(Gg[(size_t)i * sn + col])) : 1.f) * go[(size_t)i * go_row + col];
-    if (LO) v -= to_f32(from_f32<T>(v));
-    dst[e] = from_f32<T>(v);
+// Rows [r0, r0 + CH) of a row-major [.][DP] operand into LDS dst[CH][DP]
+// (zero outside rows [0, n) and columns [0, d)).  `src` rows are `sn` elements
+// apart; 16-byte vector copies when d == DP and the rows are 16-byte aligned.
+template <typename T, int DP>
+__device__ __forceinline__ void stage_chunk(T* dst, const T* __restrict__ src, long long sn, int r0, int CH, int n,
+                                            int d) {
+  constexpr int VE = 16 / sizeof(T);
+  typedef __attribute__((__vector_size__(16))) int i32x4;
+  if (d == DP && sn % VE == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    constexpr int CPR = DP / VE;
+    for (int c = threadIdx.x; c < CH * CPR; c += SK_NT) {
+      const int row = c / CPR, k = c - row * CPR;
+      const int i = r0 + row;
+      i32x4 v = {0, 0, 0, 0};
+      if (i < n) v = *reinterpret_cast<const i32x4*>(src + (size_t)i * sn + k * VE);
+      *reinterpret_cast<i32x4*>(dst + (size_t)row * DP + k * VE) = v;
+    }
+    return;
   }
-}
-template <typename T, int DP, bool TRANSP>
-__device__ void stage_chunk(T* dst, const T* __restrict__ src, long long sn, int r0, int CH, int n, int d) {
   for (int e = threadIdx.x; e < CH * DP; e += SK_NT) {
-    int row, col;
-    if (TRANSP) { col = e / CH; row = e - col * CH; }
-    else { row = e / DP; col = e - row * DP; }
+    const int row = e / DP, col = e - row * DP;
     const int i = r0 + row;
     T v = from_f32<T>(0.f);
     if (i < n && col < d) v = src[(size_t)i * sn + col];
     dst[e] = v;
+  }
+}
+
+// Transposed: dst[DP][CH] with dst[c][row] = src[r0 + row][c].
+template <typename T, int DP>
+__device__ __forceinline__ void stage_chunk_t(T* dst, const T* __restrict__ src, long long sn, int r0, int CH, int n,
+                                              int d) {
+  constexpr int VE = 16 / sizeof(T);
+  if (d == DP && sn % VE == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    constexpr int CPR = DP / VE;
+    for (int c = threadIdx.x; c < CH * CPR; c += SK_NT) {
+      const int row = c % CH, k = c / CH;  // consecutive threads -> consecutive rows
+      const int i = r0 + row;
+      T v[VE];
+      if (i < n) {
+        typedef __attribute__((__vector_size__(16))) int i32x4;
+        const i32x4 w = *reinterpret_cast<const i32x4*>(src + (size_t)i * sn + k * VE);
+        __builtin_memcpy(v, &w, 16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) v[e] = from_f32<T>(0.f);
+      }
+#pragma unroll
+      for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * CH + row] = v[e];
+    }
+    return;
+  }
+  for (int e = threadIdx.x; e < CH * DP; e += SK_NT) {
+    const int col = e / CH, row = e - col * CH;
+    const int i = r0 + row;
+    T v = from_f32<T>(0.f);
+    if (i < n && col < d) v = src[(size_t)i * sn + col];
+    dst[e] = v;
+  }
+}
+
+// Columns [r0, r0 + CH) of a prepared transposed operand src[DP][Np] into dst[DP][CH]
+// (Np and r0 are multiples of 32 and CH of 32, so rows are 16-byte aligned).
+template <typename T, int DP>
+__device__ __forceinline__ void stage_chunk_tt(T* dst, const T* __restrict__ src, int Np, int r0, int CH) {
+  constexpr int VE = 16 / sizeof(T);
+  typedef __attribute__((__vector_size__(16))) int i32x4;
+  const int per = CH / VE;
+  for (int c = threadIdx.x; c < DP * per; c += SK_NT) {
+    const int k = c / per, e = c - k * per;
+    const int i = r0 + e * VE;
+    i32x4 v = {0, 0, 0, 0};
+    if (i < Np) v = *reinterpret_cast<const i32x4*>(src + (size_t)k * Np + i);
+    *reinterpret_cast<i32x4*>(dst + (size_t)k * CH + e * VE) = v;
   }
 }
 
@@ -235,9 +282,9 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const T* Qg = reinterpret_cast<const T*>(a.q) + qoff;
   const T* Kg = reinterpret_cast<const T*>(a.k) + qoff;
   const T* Vg = reinterpret_cast<const T*>(a.v) + qoff;
-  const T* Gg = a.g ? reinterpret_cast<const T*>(a.g) + qoff : nullptr;
-  const long long go_row = (long long)a.H * d;
-  const float* go = a.grad_o + (size_t)b * N * go_row + (size_t)h * d;  // row i at go + i*go_row
+  const T* gOh = reinterpret_cast<const T*>(a.go_hi) + bh * Np * DP;  // [Np][DP]
+  const T* gOlo = reinterpret_cast<const T*>(a.go_lo) + bh * Np * DP;  // [Np][DP]
+  const T* gOt = reinterpret_cast<const T*>(a.go_t) + bh * DP * Np;    // [DP][Np]
   const float eps = a.eps[h];
   const float kappa = a.lam / (a.lam + eps);
   const float sc = LOG2E / (sqrtf((float)d) * eps);
@@ -277,30 +324,9 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const bool general = use_pos || use_geo;
   const bool geo_grad = a.geo_grad != 0 && a.x != nullptr;
 
-  // ---- P0: D_i for all valid rows; dG for my rows
-  for (int i = threadIdx.x; i < Np; i += SK_NT) {
-    float Dsum = 0.f;
-    if (i < n && valid[i]) {
-      const float* oa = a.o_avg + (bh * N + i) * d;
-      for (int c = 0; c < d; ++c) {
-        const float s = Gg ? sigm(to_f32(Gg[(size_t)i * a.sn + c])) : 1.f;
-        Dsum += s * go[(size_t)i * go_row + c] * oa[c];
-      }
-      if (has_dxc) {
-        const float* xc = a.x_centroid + (bh * N + i) * 3;
-        Dsum += dxc[3 * i] * xc[0] + dxc[3 * i + 1] * xc[1] + dxc[3 * i + 2] * xc[2];
-      }
-    }
-    Dv[i] = Dsum;
-  }
-  if (Gg) {
-    for (int e = threadIdx.x; e < (r_hi - r_lo) * d; e += SK_NT) {
-      const int i = r_lo + e / d, c = e % d;
-      if (!valid[i]) continue;
-      const float s = sigm(to_f32(Gg[(size_t)i * a.sn + c]));
-      a.dg[(bh * N + i) * d + c] = s * (1.f - s) * a.o_avg[(bh * N + i) * d + c] * go[(size_t)i * go_row + c];
-    }
-  }
+  // ---- D_i (prep kernel) for all rows
+  const float* Dg = a.dcoef + bh * Np;
+  for (int i = threadIdx.x; i < Np; i += SK_NT) Dv[i] = Dg[i];
   __syncthreads();
 
   uint64_t* xbase = a.xch + bh * 4 * (size_t)Np;
@@ -346,10 +372,10 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       }
       for (int c0 = 0; c0 < n; c0 += CH) {
         __syncthreads();
-        stage_chunk<T, DP, false>(Qc, Qg, a.sn, c0, CH, n, d);
-        stage_gO<T, DP, false>(gOc, Gg, a.sn, go, go_row, c0, CH, n, d);
-        if (M::SPLIT) stage_gO<T, DP, false, true>(gOl, Gg, a.sn, go, go_row, c0, CH, n, d);
-        stage_gO<T, DP, true>(gOT, Gg, a.sn, go, go_row, c0, CH, n, d);
+        stage_chunk<T, DP>(Qc, Qg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(gOc, gOh, DP, c0, CH, Np, DP);
+        if (M::SPLIT) stage_chunk<T, DP>(gOl, gOlo, DP, c0, CH, Np, DP);
+        stage_chunk_tt<T, DP>(gOT, gOt, Np, c0, CH);
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
         for (int pr = 0; pr < npair; ++pr) {
@@ -480,7 +506,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     // CG on (I - kappa^2 W^T W) y = D_c^{-1/2} g_v, W_ij = exp2(sc qk + alpha_i + beta_j)
     float* al = zu;   // alpha_i = u - logZ/2 (rows); zu is rebuilt after the solve
     float* be = zvv;  // beta_j = (v - col_lse)/2 (cols)
-    float* cs = Dv;   // s = W^T t; D is rebuilt before R2
+    float* cs = gv;   // s = W^T t; g_v is not read again once r and p are set
     for (int i = threadIdx.x; i < Np; i += SK_NT) {
       const bool ok = i < n && valid[i];
       al[i] = ok ? uu[i] - 0.5f * lz[i] : NEG_BIG;
@@ -536,23 +562,6 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       zu[i] = ok ? kappa * ctw[i] * fast_exp2(0.5f * lz[i]) : 0.f;
     }
     __syncthreads();
-    // rebuild D (its storage held s)
-    for (int i = threadIdx.x; i < Np; i += SK_NT) {
-      float Dsum = 0.f;
-      if (i < n && valid[i]) {
-        const float* oa = a.o_avg + (bh * N + i) * d;
-        for (int c = 0; c < d; ++c) {
-          const float s = Gg ? sigm(to_f32(Gg[(size_t)i * a.sn + c])) : 1.f;
-          Dsum += s * go[(size_t)i * go_row + c] * oa[c];
-        }
-        if (has_dxc) {
-          const float* xc = a.x_centroid + (bh * N + i) * 3;
-          Dsum += dxc[3 * i] * xc[0] + dxc[3 * i + 1] * xc[1] + dxc[3 * i + 2] * xc[2];
-        }
-      }
-      Dv[i] = Dsum;
-    }
-    __syncthreads();
   }
   // marginal gradients (flash_sinkhorn_attn.py:645-646; analytic: d log_mu = kappa lambda_u = -kappa z_u)
   for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += SK_NT) {
@@ -595,22 +604,8 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
           ++ntile;
           const int i = (t0 + rt) * 16 + (lane & 15);
           load_frag_global<T, DP>(qf[k], Qg, a.sn, i, n, d, lane);
-          {
-            constexpr int RUN = M::RUN;
-            T tmp[RUN], tml[RUN];
-            const int cb = (lane >> 4) * RUN;
-#pragma unroll
-            for (int e = 0; e < RUN; ++e) {
-              const int col = cb + e;
-              float v = 0.f;
-              if (i < n && col < d)
-                v = (Gg ? sigm(to_f32(Gg[(size_t)i * a.sn + col])) : 1.f) * go[(size_t)i * go_row + col];
-              tmp[e] = from_f32<T>(v);
-              tml[e] = from_f32<T>(v - to_f32(tmp[e]));
-            }
-            M::from_run(gf[k], tmp);
-            if (M::SPLIT) M::from_run(gfl[k], tml);
-          }
+          load_frag_global<T, DP>(gf[k], gOh, DP, i, Np, DP, lane);
+          if (M::SPLIT) load_frag_global<T, DP>(gfl[k], gOlo, DP, i, Np, DP, lane);
           const float ci = a2[i] / sc;
           cinit[k] = f32x4{ci, ci, ci, ci};
           lzi[k] = lz[i];
@@ -622,9 +617,9 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       }
       for (int c0 = 0; c0 < n; c0 += CH) {
         __syncthreads();
-        stage_chunk<T, DP, false>(Kc, Kg, a.sn, c0, CH, n, d);
-        stage_chunk<T, DP, false>(Vc, Vg, a.sn, c0, CH, n, d);
-        stage_chunk<T, DP, true>(KT, Kg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(Kc, Kg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(Vc, Vg, a.sn, c0, CH, n, d);
+        stage_chunk_t<T, DP>(KT, Kg, a.sn, c0, CH, n, d);
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
         for (int pr = 0; pr < npair; ++pr) {
@@ -751,10 +746,10 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       }
       for (int c0 = 0; c0 < n; c0 += CH) {
         __syncthreads();
-        stage_chunk<T, DP, false>(Qc, Qg, a.sn, c0, CH, n, d);
-        stage_gO<T, DP, false>(gOc, Gg, a.sn, go, go_row, c0, CH, n, d);
-        if (M::SPLIT) stage_gO<T, DP, false, true>(gOl, Gg, a.sn, go, go_row, c0, CH, n, d);
-        stage_chunk<T, DP, true>(QT, Qg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(Qc, Qg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(gOc, gOh, DP, c0, CH, Np, DP);
+        if (M::SPLIT) stage_chunk<T, DP>(gOl, gOlo, DP, c0, CH, Np, DP);
+        stage_chunk_t<T, DP>(QT, Qg, a.sn, c0, CH, n, d);
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
         for (int pr = 0; pr < npair; ++pr) {
@@ -863,6 +858,48 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   for (int k = threadIdx.x; k < 68; k += SK_NT) a.dpw_part[wg_id * 68 + k] = dpw[k];
 }
 
+// Prep: per (b,h) and row i < Np, with gO = sigma(G) dO on valid rows (0 elsewhere):
+//   go_hi = T(gO), go_lo = T(gO - T(gO)), go_t = go_hi transposed, dG = sigma(1-sigma) O_avg dO,
+//   D_i = sum_c gO_ic O_avg_ic + dxc_i . xc_i   (flash_sinkhorn_attn.py:278-292).
+// One thread per (b, h, i, c), c < DP; the DP lanes of a row are contiguous in a wave.
+template <typename T, int DP>
+__global__ void __launch_bounds__(256) sinkhorn_bwd_prep_kernel(SinkBwdArgs a) {
+  const int N = a.N, d = a.d;
+  const int Np = ((N + 31) / 32) * 32;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;  // grid covers B*H*Np*DP exactly
+  const size_t row = e / DP;
+  const int c = (int)(e % DP);
+  const int bh = (int)(row / Np), i = (int)(row % Np);
+  const int b = bh / a.H, h = bh % a.H;
+  const bool ok = i < N && (a.mask ? a.mask[(size_t)b * N + i] > 0.5f : true);
+  float go = 0.f, oa = 0.f, s = 1.f;
+  if (ok && c < d) {
+    go = a.grad_o[((size_t)b * N + i) * a.H * d + (size_t)h * d + c];
+    oa = a.o_avg[((size_t)bh * N + i) * d + c];
+    if (a.g) {
+      const T* Gg = reinterpret_cast<const T*>(a.g) + (size_t)b * a.sb + (size_t)h * a.sh;
+      s = sigm(to_f32(Gg[(size_t)i * a.sn + c]));
+      a.dg[((size_t)bh * N + i) * d + c] = s * (1.f - s) * oa * go;
+    }
+  }
+  const float g = s * go;
+  const T hi = from_f32<T>(g);
+  reinterpret_cast<T*>(a.go_hi)[row * DP + c] = hi;
+  reinterpret_cast<T*>(a.go_lo)[row * DP + c] = from_f32<T>(g - to_f32(hi));
+  reinterpret_cast<T*>(a.go_t)[((size_t)bh * DP + c) * Np + i] = hi;
+  float part = g * oa;
+#pragma unroll
+  for (int o = DP / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, WAVE);
+  if (c == 0) {
+    if (ok && a.grad_xc) {
+      const float* dxc = a.grad_xc + ((size_t)bh * N + i) * 3;
+      const float* xc = a.x_centroid + ((size_t)bh * N + i) * 3;
+      part += dxc[0] * xc[0] + dxc[1] * xc[1] + dxc[2] * xc[2];
+    }
+    a.dcoef[row] = ok ? part : 0.f;
+  }
+}
+
 // dx_res[b,i,:] = sum_h dx_part[b,h,i,:] on valid rows; dpw / dw summed over
 // (b, member) partials in a fixed order.
 __global__ void sinkhorn_bwd_finalize_kernel(SinkBwdArgs a, float* dx, float* dpw, float* dw) {
@@ -929,6 +966,25 @@ hipError_t launch_sinkhorn_bwd(const SinkBwdArgs& a, bool bf16_in, int DP, size_
   } else {
     if (DP == 32) return launch_bwd_t<float, 32>(a, lds, stream, coop);
     if (DP == 64) return launch_bwd_t<float, 64>(a, lds, stream, coop);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename T, int DP>
+static hipError_t launch_prep_t(const SinkBwdArgs& a, hipStream_t stream) {
+  const size_t Np = ((a.N + 31) / 32) * 32;
+  const size_t threads = (size_t)a.B * a.H * Np * DP;  // multiple of 1024
+  hipLaunchKernelGGL((sinkhorn_bwd_prep_kernel<T, DP>), dim3((unsigned)(threads / 256)), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sinkhorn_bwd_prep(const SinkBwdArgs& a, bool bf16_in, int DP, hipStream_t stream) {
+  if (bf16_in) {
+    if (DP == 32) return launch_prep_t<bf16, 32>(a, stream);
+    if (DP == 64) return launch_prep_t<bf16, 64>(a, stream);
+  } else {
+    if (DP == 32) return launch_prep_t<float, 32>(a, stream);
+    if (DP == 64) return launch_prep_t<float, 64>(a, stream);
   }
   return hipErrorInvalidValue;
 }
