@@ -32,6 +32,11 @@
 
 namespace dfl {
 
+constexpr int BWD_NT = 512;             // 8 waves: two per SIMD
+constexpr int BWD_NW = BWD_NT / WAVE;
+constexpr int BWD_MAXT = 2;             // resident tiles per wave in the heavy passes
+constexpr int BWD_SCRATCH = sweep_scratch<BWD_NT>();
+
 // ---------------------------------------------------------------------------
 // light sweep: out[q] = sum_j exp2(sc*<res_q, str_j> + cres[q] + w2_j (+bias)) * z_j
 // Every exponent is <= 0 here (S_col, T and W are bounded by 1), so no shift.
@@ -59,7 +64,7 @@ __device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const
         cinit[r] = f32x4{ci, ci, ci, ci};
       }
     }
-    for (int st = wave; st < n_str_tiles; st += SK_NW) {
+    for (int st = wave; st < n_str_tiles; st += BWD_NW) {
       typename M::Frag af;
       M::load(af, str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
       const f32x4 w = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
@@ -92,7 +97,7 @@ __device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const
       const int q = threadIdx.x, r = q >> 4, l = q & 15;
       float ss = 0.f;
 #pragma unroll
-      for (int w = 0; w < SK_NW; ++w) ss += scratch[(w * SK_RT + r) * 16 + l];
+      for (int w = 0; w < BWD_NW; ++w) ss += scratch[(w * SK_RT + r) * 16 + l];
       out[c0 * 16 + q] = ss;
     }
     __syncthreads();
@@ -103,7 +108,7 @@ __device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const
 template <typename F>
 __device__ __forceinline__ float block_sum(int n, F f, float* red) {
   float acc = 0.f;
-  for (int i = threadIdx.x; i < n; i += SK_NT) acc += f(i);
+  for (int i = threadIdx.x; i < n; i += BWD_NT) acc += f(i);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
   const int wave = threadIdx.x / WAVE;
@@ -112,7 +117,7 @@ __device__ __forceinline__ float block_sum(int n, F f, float* red) {
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
-  for (int w = 0; w < SK_NW; ++w) tot += red[w];
+  for (int w = 0; w < BWD_NW; ++w) tot += red[w];
   __syncthreads();
   return tot;
 }
@@ -120,14 +125,16 @@ __device__ __forceinline__ float block_sum(int n, F f, float* red) {
 // Gather a published vector into dst (scale 1), zeroing invalid entries and the tail.
 __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
                                               const unsigned char* valid, uint32_t* err, int* s_flag) {
-  if (!xch_gather<SK_NT>(buf, n, tag, dst, 1.f, err, s_flag)) return false;  // values as published
-  for (int i = threadIdx.x; i < Np; i += SK_NT)
+  if (!xch_gather<BWD_NT>(buf, n, tag, dst, 1.f, err, s_flag)) return false;  // values as published
+  for (int i = threadIdx.x; i < Np; i += BWD_NT)
     if (i >= n || !valid[i]) dst[i] = 0.f;
   __syncthreads();
   return true;
 }
 
 __device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
+
+constexpr int STAGE_BATCH = 4;  // 16-byte loads each thread keeps in flight while staging
 
 // Rows [r0, r0 + CH) of a row-major [.][DP] operand into LDS dst[CH][DP]
 // (zero outside rows [0, n) and columns [0, d)).  `src` rows are `sn` elements
@@ -139,16 +146,27 @@ __device__ __forceinline__ void stage_chunk(T* dst, const T* __restrict__ src, l
   typedef __attribute__((__vector_size__(16))) int i32x4;
   if (d == DP && sn % VE == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
     constexpr int CPR = DP / VE;
-    for (int c = threadIdx.x; c < CH * CPR; c += SK_NT) {
-      const int row = c / CPR, k = c - row * CPR;
-      const int i = r0 + row;
-      i32x4 v = {0, 0, 0, 0};
-      if (i < n) v = *reinterpret_cast<const i32x4*>(src + (size_t)i * sn + k * VE);
-      *reinterpret_cast<i32x4*>(dst + (size_t)row * DP + k * VE) = v;
+    const int total = CH * CPR;
+    // STAGE_BATCH loads in flight per thread before the first store
+    for (int c0 = threadIdx.x; c0 < total; c0 += STAGE_BATCH * BWD_NT) {
+      i32x4 v[STAGE_BATCH];
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c / CPR, k = c - row * CPR;
+        v[u] = i32x4{0, 0, 0, 0};
+        if (c < total && r0 + row < n) v[u] = *reinterpret_cast<const i32x4*>(src + (size_t)(r0 + row) * sn + k * VE);
+      }
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c / CPR, k = c - row * CPR;
+        if (c < total) *reinterpret_cast<i32x4*>(dst + (size_t)row * DP + k * VE) = v[u];
+      }
     }
     return;
   }
-  for (int e = threadIdx.x; e < CH * DP; e += SK_NT) {
+  for (int e = threadIdx.x; e < CH * DP; e += BWD_NT) {
     const int row = e / DP, col = e - row * DP;
     const int i = r0 + row;
     T v = from_f32<T>(0.f);
@@ -163,25 +181,33 @@ __device__ __forceinline__ void stage_chunk_t(T* dst, const T* __restrict__ src,
                                               int d) {
   constexpr int VE = 16 / sizeof(T);
   if (d == DP && sn % VE == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    typedef __attribute__((__vector_size__(16))) int i32x4;
     constexpr int CPR = DP / VE;
-    for (int c = threadIdx.x; c < CH * CPR; c += SK_NT) {
-      const int row = c % CH, k = c / CH;  // consecutive threads -> consecutive rows
-      const int i = r0 + row;
-      T v[VE];
-      if (i < n) {
-        typedef __attribute__((__vector_size__(16))) int i32x4;
-        const i32x4 w = *reinterpret_cast<const i32x4*>(src + (size_t)i * sn + k * VE);
-        __builtin_memcpy(v, &w, 16);
-      } else {
+    const int total = CH * CPR;
+    for (int c0 = threadIdx.x; c0 < total; c0 += STAGE_BATCH * BWD_NT) {
+      i32x4 w[STAGE_BATCH];
 #pragma unroll
-        for (int e = 0; e < VE; ++e) v[e] = from_f32<T>(0.f);
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c % CH, k = c / CH;  // consecutive threads -> consecutive rows
+        w[u] = i32x4{0, 0, 0, 0};
+        if (c < total && r0 + row < n) w[u] = *reinterpret_cast<const i32x4*>(src + (size_t)(r0 + row) * sn + k * VE);
       }
 #pragma unroll
-      for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * CH + row] = v[e];
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c % CH, k = c / CH;
+        if (c < total) {
+          T v[VE];
+          __builtin_memcpy(v, &w[u], 16);
+#pragma unroll
+          for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * CH + row] = v[e];
+        }
+      }
     }
     return;
   }
-  for (int e = threadIdx.x; e < CH * DP; e += SK_NT) {
+  for (int e = threadIdx.x; e < CH * DP; e += BWD_NT) {
     const int col = e / CH, row = e - col * CH;
     const int i = r0 + row;
     T v = from_f32<T>(0.f);
@@ -197,19 +223,29 @@ __device__ __forceinline__ void stage_chunk_tt(T* dst, const T* __restrict__ src
   constexpr int VE = 16 / sizeof(T);
   typedef __attribute__((__vector_size__(16))) int i32x4;
   const int per = CH / VE;
-  for (int c = threadIdx.x; c < DP * per; c += SK_NT) {
-    const int k = c / per, e = c - k * per;
-    const int i = r0 + e * VE;
-    i32x4 v = {0, 0, 0, 0};
-    if (i < Np) v = *reinterpret_cast<const i32x4*>(src + (size_t)k * Np + i);
-    *reinterpret_cast<i32x4*>(dst + (size_t)k * CH + e * VE) = v;
+  const int total = DP * per;
+  for (int c0 = threadIdx.x; c0 < total; c0 += STAGE_BATCH * BWD_NT) {
+    i32x4 v[STAGE_BATCH];
+#pragma unroll
+    for (int u = 0; u < STAGE_BATCH; ++u) {
+      const int c = c0 + u * BWD_NT;
+      const int k = c / per, e = c - k * per;
+      v[u] = i32x4{0, 0, 0, 0};
+      if (c < total && r0 + e * VE < Np) v[u] = *reinterpret_cast<const i32x4*>(src + (size_t)k * Np + r0 + e * VE);
+    }
+#pragma unroll
+    for (int u = 0; u < STAGE_BATCH; ++u) {
+      const int c = c0 + u * BWD_NT;
+      const int k = c / per, e = c - k * per;
+      if (c < total) *reinterpret_cast<i32x4*>(dst + (size_t)k * CH + e * VE) = v[u];
+    }
   }
 }
 
 struct BwdShared {
   int flag, tmp;
   float posw[68];
-  float red[SK_NW];
+  float red[BWD_NW];
 };
 
 __host__ __device__ inline int bwd_chunk(int N) {
@@ -219,7 +255,7 @@ __host__ __device__ inline int bwd_chunk(int N) {
 __host__ __device__ inline int bwd_local_rows(int N, int G) { return 16 * (((N + 15) / 16 + G - 1) / G); }
 
 template <typename T, int DP>
-__global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
+__global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   using M = Mfma<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ BwdShared sh;
@@ -261,7 +297,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   float* lout = lres + loc;      // per-local-row results [loc]
   float* dxs = lout + loc;       // dx accumulator for my stripe [loc][3]
   float* dpw = dxs + 3 * loc;    // d pos_weight histogram [68]
-  float* scratch = dpw + 68;     // LSE_SCRATCH floats
+  float* scratch = dpw + 68;     // BWD_SCRATCH floats
 
   const size_t bh = (size_t)b * a.H + h;
   const size_t wg_id = bh * a.G + member;
@@ -272,7 +308,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const int nr = t1 - t0;
   if (n == 0 || nr <= 0) {
     // owns nothing: publish empty partials so the finaliser can sum every slot
-    for (int k = threadIdx.x; k < 68; k += SK_NT) a.dpw_part[wg_id * 68 + k] = 0.f;
+    for (int k = threadIdx.x; k < 68; k += BWD_NT) a.dpw_part[wg_id * 68 + k] = 0.f;
     if (threadIdx.x == 0) a.dw_part[wg_id] = 0.f;
     return;
   }
@@ -295,7 +331,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const bool has_dxc = a.grad_xc != nullptr;
 
   // ---- per-(b,h) vectors (log2 units; invalid -> NEG_BIG / 0)
-  for (int i = threadIdx.x; i < Np; i += SK_NT) {
+  for (int i = threadIdx.x; i < Np; i += BWD_NT) {
     const bool ok = i < n && valid[i];
     uu[i] = ok ? a.log_u[bh * N + i] * LOG2E : NEG_BIG;
     vv[i] = ok ? a.log_v[bh * N + i] * LOG2E : NEG_BIG;
@@ -306,13 +342,13 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       dxc[3 * i + c] = (has_dxc && ok) ? a.grad_xc[(bh * N + i) * 3 + c] : 0.f;
     }
   }
-  for (int q = threadIdx.x; q < 3 * loc; q += SK_NT) dxs[q] = 0.f;
-  for (int k = threadIdx.x; k < 68; k += SK_NT) dpw[k] = 0.f;
+  for (int q = threadIdx.x; q < 3 * loc; q += BWD_NT) dxs[q] = 0.f;
+  for (int k = threadIdx.x; k < 68; k += BWD_NT) dpw[k] = 0.f;
   const float w_h = a.w_dist ? a.w_dist[h] : 0.f;
   const bool use_geo = (a.x != nullptr) && (w_h != 0.f);
   const bool use_pos = (a.bins != nullptr) && (a.pos_w != nullptr);
   if (use_pos)
-    for (int k = threadIdx.x; k < 68; k += SK_NT) sh.posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
+    for (int k = threadIdx.x; k < 68; k += BWD_NT) sh.posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
   __syncthreads();
   Bias bias;
   bias.bins = use_pos ? a.bins + (size_t)b * N * N : nullptr;
@@ -326,7 +362,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 
   // ---- D_i (prep kernel) for all rows
   const float* Dg = a.dcoef + bh * Np;
-  for (int i = threadIdx.x; i < Np; i += SK_NT) Dv[i] = Dg[i];
+  for (int i = threadIdx.x; i < Np; i += BWD_NT) Dv[i] = Dg[i];
   __syncthreads();
 
   uint64_t* xbase = a.xch + bh * 4 * (size_t)Np;
@@ -344,18 +380,18 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* gOl = gOc + (size_t)CH * DP;  // low halves of gO (bf16 only)
     T* gOT = gOl + (size_t)CH * DP;  // [DP][CH]
     float* a2 = ct;                  // (u - logZ) in log2, rows (ct is free until the solve)
-    for (int i = threadIdx.x; i < Np; i += SK_NT) a2[i] = (i < n && valid[i]) ? uu[i] - lz[i] : NEG_BIG;
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) a2[i] = (i < n && valid[i]) ? uu[i] - lz[i] : NEG_BIG;
     __syncthreads();
-    for (int rt0 = 0; rt0 < nr; rt0 += 4 * SK_NW) {
+    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
       // wave w owns resident tiles rt0 + w + 4*k, k < 4 (up to 16 tiles per batch)
-      constexpr int MAXT = 4;
+      constexpr int MAXT = BWD_MAXT;
       typename M::Frag kf[MAXT], vf[MAXT];
       f32x4 cinit[MAXT], dvacc[MAXT][NC];
       float gva[MAXT], dxa[MAXT][3], xj[MAXT][3];
       int ntile = 0;
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
-        const int rt = rt0 + wave + SK_NW * k;
+        const int rt = rt0 + wave + BWD_NW * k;
         gva[k] = 0.f;
         dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
 #pragma unroll
@@ -393,7 +429,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int k = 0; k < MAXT; ++k) {
             if (k < ntile) {
-              const int j = (t0 + rt0 + wave + SK_NW * k) * 16 + (lane & 15);
+              const int j = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
               f32x4 tv[2];
 #pragma unroll
               for (int hf = 0; hf < 2; ++hf) {
@@ -431,7 +467,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
         if (k < ntile) {
-          const int tile = t0 + rt0 + wave + SK_NW * k;
+          const int tile = t0 + rt0 + wave + BWD_NW * k;
           const int jl = tile * 16 + (lane & 15);
           const float gsum = sum_groups(gva[k]);
           const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
@@ -458,7 +494,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     __syncthreads();
     ++phase;
     uint64_t* xg = xbase;  // slot 0: g_v
-    for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += SK_NT) xch_put(xg + j, lout[j - r_lo], salt | phase);
+    for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xg + j, lout[j - r_lo], salt | phase);
     if (!gather_vector(xg, n, Np, salt | phase, gv, valid, a.err, &sh.flag)) return;
   }
 
@@ -474,10 +510,10 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   uint64_t* xB = xbase + 2 * Np;  // slot 2
   if (a.solver == 0) {
     // reference Gauss-Seidel (flash_sinkhorn_attn.py:471-542): z_u = 0, z_v = g_v
-    for (int i = threadIdx.x; i < Np; i += SK_NT) { zu[i] = 0.f; zvv[i] = gv[i]; }
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) { zu[i] = 0.f; zvv[i] = gv[i]; }
     float* mcl = cy;  // -col_lse (log2) on valid columns
     float* a2 = cr;   // u - logZ (log2) on valid rows
-    for (int i = threadIdx.x; i < Np; i += SK_NT) {
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) {
       const bool ok = i < n && valid[i];
       mcl[i] = ok ? -cl[i] : NEG_BIG;
       a2[i] = ok ? uu[i] - lz[i] : NEG_BIG;
@@ -485,20 +521,20 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     __syncthreads();
     for (int it = 0; it < a.iters; ++it) {
       // z_u_i = kappa sum_j S_col_ij z_v_j   (resident rows: cres = u_i)
-      for (int q = threadIdx.x; q < nr * 16; q += SK_NT) lres[q] = uu[r_lo + q];
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = uu[r_lo + q];
       __syncthreads();
       if (general) light_sweep<T, DP, true, false>(QS, KS, mcl, zvv, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       else light_sweep<T, DP, false, false>(QS, KS, mcl, zvv, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       ++phase;
-      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += SK_NT) xch_put(xA + i, kappa * lout[i - r_lo], salt | phase);
+      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, kappa * lout[i - r_lo], salt | phase);
       if (!gather_vector(xA, n, Np, salt | phase, zu, valid, a.err, &sh.flag)) return;
       // z_v_j = g_v_j + kappa sum_i T_ij z_u_i   (resident cols: cres = v_j)
-      for (int q = threadIdx.x; q < nr * 16; q += SK_NT) lres[q] = vv[r_lo + q];
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = vv[r_lo + q];
       __syncthreads();
       if (general) light_sweep<T, DP, true, true>(KS, QS, a2, zu, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       else light_sweep<T, DP, false, true>(KS, QS, a2, zu, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       ++phase;
-      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += SK_NT)
+      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT)
         xch_put(xB + j, gv[j] + kappa * lout[j - r_lo], salt | phase);
       if (!gather_vector(xB, n, Np, salt | phase, zvv, valid, a.err, &sh.flag)) return;
     }
@@ -507,7 +543,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     float* al = zu;   // alpha_i = u - logZ/2 (rows); zu is rebuilt after the solve
     float* be = zvv;  // beta_j = (v - col_lse)/2 (cols)
     float* cs = gv;   // s = W^T t; g_v is not read again once r and p are set
-    for (int i = threadIdx.x; i < Np; i += SK_NT) {
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) {
       const bool ok = i < n && valid[i];
       al[i] = ok ? uu[i] - 0.5f * lz[i] : NEG_BIG;
       be[i] = ok ? 0.5f * (vv[i] - cl[i]) : NEG_BIG;
@@ -519,44 +555,48 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     }
     __syncthreads();
     float rr = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red);
+    // cg_rtol > 0: stop once ||r|| <= rtol ||b|| (utils/cg.py:63-80).  cg_rtol == 0:
+    // exactly `iters` iterations; a residual that reaches zero stays zero (alpha = beta = 0).
+    // rr, pAp and rr_new are bit-identical in every member, so the exit is uniform.
+    const bool early_exit = a.cg_rtol > 0.f;
     const float stop2 = a.cg_rtol * a.cg_rtol * rr;
     const float k2 = kappa * kappa;
     for (int it = 0; it < a.iters; ++it) {
-      if (rr <= stop2 || rr == 0.f) break;
+      if (early_exit && (rr <= stop2 || rr == 0.f)) break;
       // t_i = sum_j W_ij p_j (my rows)
-      for (int q = threadIdx.x; q < nr * 16; q += SK_NT) lres[q] = al[r_lo + q];
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = al[r_lo + q];
       __syncthreads();
       if (general) light_sweep<T, DP, true, false>(QS, KS, be, cp, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       else light_sweep<T, DP, false, false>(QS, KS, be, cp, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       ++phase;
-      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += SK_NT) xch_put(xA + i, lout[i - r_lo], salt | phase);
+      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, lout[i - r_lo], salt | phase);
       if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) return;
       // s_j = sum_i W_ij t_i (my cols)
-      for (int q = threadIdx.x; q < nr * 16; q += SK_NT) lres[q] = be[r_lo + q];
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = be[r_lo + q];
       __syncthreads();
       if (general) light_sweep<T, DP, true, true>(KS, QS, al, ct, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       else light_sweep<T, DP, false, true>(KS, QS, al, ct, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
       ++phase;
-      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += SK_NT) xch_put(xB + j, lout[j - r_lo], salt | phase);
+      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase);
       if (!gather_vector(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag)) return;
       // CG update, identical in every member (utils/cg.py:70-92 with x0 = 0)
       const float pAp = block_sum(Np, [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red);
-      if (pAp == 0.f) break;
-      const float alpha = rr / pAp;
-      for (int i = threadIdx.x; i < Np; i += SK_NT) {
+      if (early_exit && pAp == 0.f) break;
+      const float alpha = (pAp != 0.f && rr != 0.f) ? rr / pAp : 0.f;
+      for (int i = threadIdx.x; i < Np; i += BWD_NT) {
         cy[i] += alpha * cp[i];
         cr[i] -= alpha * (cp[i] - k2 * cs[i]);
         ctw[i] += alpha * ct[i];
       }
       __syncthreads();
       const float rr_new = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red);
-      const float beta = rr_new / rr;
-      for (int i = threadIdx.x; i < Np; i += SK_NT) cp[i] = cr[i] + beta * cp[i];
+      const float beta = rr != 0.f ? rr_new / rr : 0.f;
+      for (int i = threadIdx.x; i < Np; i += BWD_NT) cp[i] = cr[i] + beta * cp[i];
       rr = rr_new;
       __syncthreads();
     }
     // z_v = D_c^{1/2} y, z_u = kappa D_r^{1/2} (W y)
-    for (int i = threadIdx.x; i < Np; i += SK_NT) {
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) {
       const bool ok = i < n && valid[i];
       zvv[i] = ok ? cy[i] * fast_exp2(0.5f * (vv[i] + cl[i])) : 0.f;
       zu[i] = ok ? kappa * ctw[i] * fast_exp2(0.5f * lz[i]) : 0.f;
@@ -564,7 +604,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     __syncthreads();
   }
   // marginal gradients (flash_sinkhorn_attn.py:645-646; analytic: d log_mu = kappa lambda_u = -kappa z_u)
-  for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += SK_NT) {
+  for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) {
     if (!valid[i]) continue;
     a.dlog_mu[bh * N + i] = (a.mode == 1 ? -kappa : kappa) * zu[i];
     a.dlog_nu[bh * N + i] = kappa * zvv[i];
@@ -573,7 +613,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   // per-row helper vectors for R2 / C2
   float* a2 = cy;   // u - logZ (log2), rows
   float* lc = cr;   // v + col_lse (log2) = log c_j, cols
-  for (int i = threadIdx.x; i < Np; i += SK_NT) {
+  for (int i = threadIdx.x; i < Np; i += BWD_NT) {
     const bool ok = i < n && valid[i];
     a2[i] = ok ? uu[i] - lz[i] : NEG_BIG;
     lc[i] = ok ? vv[i] + cl[i] : 0.f;
@@ -588,15 +628,15 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* Kc = R0;
     T* Vc = Kc + (size_t)CH * DP;
     T* KT = Vc + (size_t)CH * DP;  // [DP][CH]
-    for (int rt0 = 0; rt0 < nr; rt0 += 4 * SK_NW) {
-      constexpr int MAXT = 4;
+    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
+      constexpr int MAXT = BWD_MAXT;
       typename M::Frag qf[MAXT], gf[MAXT], gfl[MAXT];
       f32x4 cinit[MAXT], dqacc[MAXT][NC];
       float lzi[MAXT], zui[MAXT], Di[MAXT], xi[MAXT][3], dci[MAXT][3], dxa[MAXT][3];
       int ntile = 0;
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
-        const int rt = rt0 + wave + SK_NW * k;
+        const int rt = rt0 + wave + BWD_NW * k;
         dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) dqacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -637,7 +677,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int k = 0; k < MAXT; ++k) {
             if (k < ntile) {
-              const int i = (t0 + rt0 + wave + SK_NW * k) * 16 + (lane & 15);
+              const int i = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
               f32x4 dcv[2];
 #pragma unroll
               for (int hf = 0; hf < 2; ++hf) {
@@ -687,7 +727,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
         if (k < ntile) {
-          const int tile = t0 + rt0 + wave + SK_NW * k;
+          const int tile = t0 + rt0 + wave + BWD_NW * k;
           const int il = tile * 16 + (lane & 15);
           const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
           if (lane < 16 && il < n) {
@@ -720,15 +760,15 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* QT = gOl + (size_t)CH * DP;   // [DP][CH]
     float* a2s = a2;
     float* zus = zu;
-    for (int rt0 = 0; rt0 < nr; rt0 += 4 * SK_NW) {
-      constexpr int MAXT = 4;
+    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
+      constexpr int MAXT = BWD_MAXT;
       typename M::Frag kf[MAXT], vf[MAXT];
       f32x4 cinit[MAXT], dkacc[MAXT][NC];
       float lcj[MAXT], zvj[MAXT], xj[MAXT][3], dxa[MAXT][3];
       int ntile = 0;
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
-        const int rt = rt0 + wave + SK_NW * k;
+        const int rt = rt0 + wave + BWD_NW * k;
         dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) dkacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -769,7 +809,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int k = 0; k < MAXT; ++k) {
             if (k < ntile) {
-              const int j = (t0 + rt0 + wave + SK_NW * k) * 16 + (lane & 15);
+              const int j = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
               const bool jok = j < n && valid[j];
               f32x4 dcv[2];
 #pragma unroll
@@ -814,7 +854,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
         if (k < ntile) {
-          const int tile = t0 + rt0 + wave + SK_NW * k;
+          const int tile = t0 + rt0 + wave + BWD_NW * k;
           const int jl = tile * 16 + (lane & 15);
           const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
           if (lane < 16 && jl < n) {
@@ -840,7 +880,7 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   __syncthreads();
 
   // ---- partials: dx for my stripe, dpw / dw of this workgroup
-  for (int q = threadIdx.x; q < 3 * (r_hi - r_lo); q += SK_NT)
+  for (int q = threadIdx.x; q < 3 * (r_hi - r_lo); q += BWD_NT)
     a.dx_part[(bh * N + r_lo) * 3 + q] = dxs[q];
   // d w_dist: per-thread partials summed in a fixed order
   {
@@ -851,11 +891,11 @@ __global__ void __launch_bounds__(SK_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     __syncthreads();
     if (threadIdx.x == 0) {
       float tot = 0.f;
-      for (int w = 0; w < SK_NW; ++w) tot += sh.red[w];
+      for (int w = 0; w < BWD_NW; ++w) tot += sh.red[w];
       a.dw_part[wg_id] = tot;
     }
   }
-  for (int k = threadIdx.x; k < 68; k += SK_NT) a.dpw_part[wg_id * 68 + k] = dpw[k];
+  for (int k = threadIdx.x; k < 68; k += BWD_NT) a.dpw_part[wg_id * 68 + k] = dpw[k];
 }
 
 // Prep: per (b,h) and row i < Np, with gO = sigma(G) dO on valid rows (0 elsewhere):
@@ -939,7 +979,7 @@ size_t sinkhorn_bwd_lds_bytes(int N, int DP, int elem, int G) {
   bytes += std::max(2 * Np * DP * elem, 4 * CH * DP * elem);     // operand region
   bytes += 13 * Np * 4 + 6 * Np * 4;                              // vectors, xs, dxc
   bytes += (2 * loc + 3 * loc + 68) * 4;                          // lres, lout, dxs, dpw
-  bytes += (size_t)LSE_SCRATCH * 4;
+  bytes += (size_t)BWD_SCRATCH * 4;
   return bytes;
 }
 
@@ -948,7 +988,7 @@ static hipError_t launch_bwd_t(const SinkBwdArgs& a, size_t lds, hipStream_t str
   auto kern = sinkhorn_bwd_kernel<T, DP>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  dim3 grid(grid_blocks(a.B * a.H, a.G)), block(SK_NT);
+  dim3 grid(grid_blocks(a.B * a.H, a.G)), block(BWD_NT);
   SinkBwdArgs copy = a;
   if (coop) {
     void* args[] = {&copy};
