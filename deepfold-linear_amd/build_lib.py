@@ -12,7 +12,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "deepfold_amd", "libdfl_amd.so")
-SOURCES = ["capi.hip", "sinkhorn_fwd.hip", "sinkhorn_bwd.hip"]
+SOURCES = ["capi.hip", "sinkhorn_fwd.hip", "sinkhorn_bwd.hip", "attention.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

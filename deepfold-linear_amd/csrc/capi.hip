@@ -9,6 +9,7 @@
 #include <string>
 
 #include "../../include/dfl_amd.h"
+#include "attn_args.h"
 #include "sinkhorn_args.h"
 
 namespace dfl {
@@ -21,6 +22,10 @@ hipError_t launch_sinkhorn_bwd(const SinkBwdArgs& a, bool bf16_in, int DP, size_
 hipError_t launch_sinkhorn_bwd_prep(const SinkBwdArgs& a, bool bf16_in, int DP, hipStream_t stream);
 hipError_t launch_sinkhorn_bwd_finalize(const SinkBwdArgs& a, float* dx, float* dpw, float* dw,
                                         hipStream_t stream);
+hipError_t launch_attn_fwd(const AttnArgs& a, bool bf16_in, int DP, hipStream_t s);
+hipError_t launch_attn_bwd(const AttnArgs& a, bool bf16_in, int DP, hipStream_t s);
+hipError_t launch_a2t_fwd(const A2TArgs& a, bool bf16_in, hipStream_t s);
+hipError_t launch_a2t_bwd(const A2TArgs& a, bool bf16_in, hipStream_t s);
 }  // namespace dfl
 
 namespace {
@@ -96,6 +101,85 @@ size_t partials_bytes(int B, int H, int N, int G) {
 // Prepared backward operands, sized for the widest case (d <= 64, fp32):
 // go_hi, go_lo, go_t of B*H*Np*64 elements each, then D (B*H*Np floats).
 size_t prep_operand_bytes(int B, int H, int N) { return (size_t)B * H * np32(N) * 64 * 4; }
+
+// Query-range splits of the attention dK/dV pass: enough workgroups to cover the
+// chip when keys are few (token-to-atom: 341 keys, 8192 queries).
+int attn_qsplit(int B, int H, int Mq, int Nk) {
+  const int kv_blocks = ((Nk + 63) / 64) * B * H;
+  int s = kv_blocks >= 256 ? 1 : (256 + kv_blocks - 1) / kv_blocks;
+  const int max_s = (Mq + 63) / 64;
+  return s < 1 ? 1 : (s > max_s ? max_s : s);
+}
+
+// Attention backward workspace: do_w, D, dK/dV partials, d pos_weight partials.
+struct AttnWs {
+  size_t do_w, dcoef, kv_part, dpw_part, total;
+};
+AttnWs attn_ws_layout(int B, int H, int Mq, int Nk) {
+  auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+  AttnWs w;
+  const size_t rows = (size_t)B * H * Mq;
+  const int qs = attn_qsplit(B, H, Mq, Nk);
+  w.do_w = 0;
+  w.dcoef = w.do_w + r256(rows * 64 * 4);
+  w.kv_part = w.dcoef + r256(rows * 4);
+  w.dpw_part = w.kv_part + (qs > 1 ? r256((size_t)qs * B * H * Nk * 2 * 64 * 4) : 0);
+  w.total = w.dpw_part + r256((size_t)B * H * ((Mq + 63) / 64) * 68 * 4);
+  return w;
+}
+
+int check_attn(const dfl_attn_params* p, bool bwd) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_BF16 && p->dtype != DFL_F32) return fail("dtype must be DFL_BF16 or DFL_F32");
+  if (p->B <= 0 || p->H <= 0 || p->Mq <= 0 || p->Nk <= 0 || p->d <= 0) return fail("B, H, Mq, Nk, d must be positive");
+  if (head_dim_pad(p->d) < 0) return fail("head dim d=%d > 64 is not supported", p->d);
+  if (!p->q || !p->k || !p->v || !p->o || !p->lse) return fail("q, k, v, o and lse are required");
+  if (p->q_stride_n < p->d || p->k_stride_n < p->d) return fail("row strides must be >= d (unit inner stride)");
+  if (p->bias_mode < DFL_ATTN_BIAS_NONE || p->bias_mode > DFL_ATTN_BIAS_WINDOW) return fail("unknown bias_mode");
+  if (p->bias_mode == DFL_ATTN_BIAS_BINS && (!p->pos_weight || !p->pos_bins)) return fail("BINS needs pos_weight and pos_bins");
+  if ((p->bias_mode == DFL_ATTN_BIAS_DENSE || p->bias_mode == DFL_ATTN_BIAS_WINDOW) && !p->bias) return fail("bias is NULL");
+  if (p->window && p->Mq != p->Nk) return fail("windowed attention needs Mq == Nk");
+  if (p->bias_mode == DFL_ATTN_BIAS_WINDOW && !p->window) return fail("a window bias needs window = 1");
+  if (bwd && (!p->grad_o || !p->dq || !p->dk || !p->dv)) return fail("grad_o, dq, dk and dv are required");
+  return 0;
+}
+
+dfl::AttnArgs attn_args(const dfl_attn_params* p) {
+  dfl::AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = p->q; a.k = p->k; a.v = p->v; a.g = p->g;
+  a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.qsn = p->q_stride_n;
+  a.ksb = p->k_stride_b; a.ksh = p->k_stride_h; a.ksn = p->k_stride_n;
+  a.qmask = p->q_mask; a.kmask = p->k_mask;
+  a.bias_mode = p->bias_mode; a.pos_w = p->pos_weight; a.bins = p->pos_bins; a.bias = p->bias;
+  a.window = p->window ? 1 : 0;
+  a.B = p->B; a.H = p->H; a.Mq = p->Mq; a.Nk = p->Nk; a.d = p->d;
+  a.scale = p->scale;
+  a.o = p->o; a.lse = p->lse;
+  a.dout = p->grad_o; a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dg = p->dg;
+  a.dbias = p->dbias; a.dpos_w = p->dpos_weight;
+  a.qsplit = 1;
+  return a;
+}
+
+int check_a2t(const dfl_a2t_params* p, bool bwd) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_BF16 && p->dtype != DFL_F32) return fail("dtype must be DFL_BF16 or DFL_F32");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0 || p->M <= 0 || p->d <= 0) return fail("B, H, N, M, d must be positive");
+  if (p->d > 64) return fail("head dim d=%d > 64 is not supported", p->d);
+  if (!p->q || !p->k || !p->v || !p->starts || !p->counts || !p->o || !p->lse) return fail("required input is NULL");
+  if (bwd && (!p->grad_o || !p->dq || !p->dk || !p->dv)) return fail("grad_o, dq, dk and dv are required");
+  return 0;
+}
+
+dfl::A2TArgs a2t_args(const dfl_a2t_params* p) {
+  dfl::A2TArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = p->q; a.k = p->k; a.v = p->v; a.starts = p->starts; a.counts = p->counts; a.tmask = p->token_mask;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.M = p->M; a.d = p->d; a.scale = p->scale;
+  a.o = p->o; a.lse = p->lse; a.dout = p->grad_o; a.dq = p->dq; a.dk = p->dk; a.dv = p->dv;
+  return a;
+}
 
 }  // namespace
 
@@ -229,6 +313,61 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward launch");
   e = dfl::launch_sinkhorn_bwd_finalize(a, p->dx_res, p->dpos_weight, p->dw_dist, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward finalize launch");
+  return 0;
+}
+
+size_t dfl_attn_workspace_size(int B, int H, int Mq, int Nk, int d) {
+  (void)d;
+  if (B <= 0 || H <= 0 || Mq <= 0 || Nk <= 0) return 0;
+  return attn_ws_layout(B, H, Mq, Nk).total;
+}
+
+int dfl_attn_fwd(const dfl_attn_params* p, void* stream) {
+  if (int rc = check_attn(p, false)) return rc;
+  const dfl::AttnArgs a = attn_args(p);
+  hipError_t e = dfl::launch_attn_fwd(a, p->dtype == DFL_BF16, head_dim_pad(p->d), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "attention forward launch");
+  return 0;
+}
+
+int dfl_attn_bwd(const dfl_attn_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_attn(p, true)) return rc;
+  const AttnWs w = attn_ws_layout(p->B, p->H, p->Mq, p->Nk);
+  if (!workspace || workspace_bytes < w.total) return fail("workspace too small: need %zu bytes", w.total);
+  dfl::AttnArgs a = attn_args(p);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  a.do_w = ws + w.do_w;
+  a.dcoef = reinterpret_cast<float*>(ws + w.dcoef);
+  a.kv_part = reinterpret_cast<float*>(ws + w.kv_part);
+  a.dpw_part = reinterpret_cast<float*>(ws + w.dpw_part);
+  a.qsplit = attn_qsplit(p->B, p->H, p->Mq, p->Nk);
+  if (a.bias_mode != dfl::ATTN_BIAS_DENSE && a.bias_mode != dfl::ATTN_BIAS_WINDOW) a.dbias = nullptr;
+  if (!a.g) a.dg = nullptr;
+  hipError_t e = dfl::launch_attn_bwd(a, p->dtype == DFL_BF16, head_dim_pad(p->d), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "attention backward launch");
+  return 0;
+}
+
+size_t dfl_a2t_workspace_size(int B, int H, int M, int d) {
+  if (B <= 0 || H <= 0 || M <= 0 || d <= 0) return 0;
+  return ((size_t)B * H * M * 2 * d * 4 + 255) / 256 * 256;
+}
+
+int dfl_a2t_fwd(const dfl_a2t_params* p, void* stream) {
+  if (int rc = check_a2t(p, false)) return rc;
+  hipError_t e = dfl::launch_a2t_fwd(a2t_args(p), p->dtype == DFL_BF16, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "atom-to-token forward launch");
+  return 0;
+}
+
+int dfl_a2t_bwd(const dfl_a2t_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_a2t(p, true)) return rc;
+  const size_t need = dfl_a2t_workspace_size(p->B, p->H, p->M, p->d);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  dfl::A2TArgs a = a2t_args(p);
+  a.dkv = static_cast<float*>(workspace);
+  hipError_t e = dfl::launch_a2t_bwd(a, p->dtype == DFL_BF16, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "atom-to-token backward launch");
   return 0;
 }
 

@@ -108,6 +108,22 @@ template <int DP> struct Mfma<bf16, DP> {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, acc, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, acc, 0, 0, 0);
   }
+  // Transposed PV product: D[c][i] += sum_j S^T[c][j] P[j][i] with P from the
+  // QK-type accumulator layout (lane <-> resident index i = l%16, streamed j) and
+  // S^T from an LDS array stored [c][j]; the result keeps lane <-> i, so
+  // per-resident-row scalars need no lane exchange.  st_row: row (c0 + l%16) at j0.
+  __device__ static __forceinline__ f32x4 pvt(const f32x4& p0, const f32x4& p1, const bf16* st_row, int lane,
+                                              f32x4 acc) {
+    const int g = lane >> 4;
+    bf16x8 a, b;
+    b[0] = (bf16)p0[0]; b[1] = (bf16)p0[1]; b[2] = (bf16)p0[2]; b[3] = (bf16)p0[3];
+    b[4] = (bf16)p1[0]; b[5] = (bf16)p1[1]; b[6] = (bf16)p1[2]; b[7] = (bf16)p1[3];
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(st_row + 4 * g);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(st_row + 16 + 4 * g);
+    a[0] = lo[0]; a[1] = lo[1]; a[2] = lo[2]; a[3] = lo[3];
+    a[4] = hi[0]; a[5] = hi[1]; a[6] = hi[2]; a[7] = hi[3];
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
   static constexpr bool SPLIT = true;
 };
 
@@ -144,6 +160,17 @@ template <int DP> struct Mfma<float, DP> {
   __device__ static __forceinline__ f32x4 pv_split(const f32x4& p0, const f32x4& p1, const float* vt_row, int lane,
                                                    f32x4 acc) {
     return pv(p0, p1, vt_row, lane, acc);
+  }
+  __device__ static __forceinline__ f32x4 pvt(const f32x4& p0, const f32x4& p1, const float* st_row, int lane,
+                                              f32x4 acc) {
+    const int g = lane >> 4;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(st_row + 4 * g);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(st_row + 16 + 4 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(lo[r], p0[r], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(hi[r], p1[r], acc, 0, 0, 0);
+    return acc;
   }
   static constexpr bool SPLIT = false;  // fp32 operands are exact already
 };

@@ -712,7 +712,10 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
                       dxa[k][2] = __builtin_fmaf(om, dx2, dxa[k][2]);
                       dw_acc = __builtin_fmaf(dC, dist / rd, dw_acc);
                     }
-                    if (use_pos) atomicAdd(&dpw[bias.bins[(size_t)i * N + j]], dC);
+                    if (use_pos) {
+                      const unsigned bk = (unsigned)bias.bins[(size_t)i * N + j];
+                      if (bk < 68u) atomicAdd(&dpw[bk], dC);
+                    }
                   }
                 }
               }

@@ -29,7 +29,10 @@ struct Bias {
   int N;
   __device__ __forceinline__ float operator()(int i, int j) const {
     float b = 0.f;
-    if (bins) b += posw[bins[(size_t)i * N + j]];
+    if (bins) {
+      const unsigned k = (unsigned)bins[(size_t)i * N + j];
+      if (k < 68u) b += posw[k];  // bins outside [0, 68) carry no bias
+    }
     if (xs) {
       const float dx = xs[3 * i] - xs[3 * j], dy = xs[3 * i + 1] - xs[3 * j + 1], dz = xs[3 * i + 2] - xs[3 * j + 2];
       const float dist = sqrtf(dx * dx + dy * dy + dz * dz);

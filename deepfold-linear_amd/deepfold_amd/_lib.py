@@ -68,6 +68,43 @@ class SinkhornBwdParams(ctypes.Structure):
     ]
 
 
+class AttnParams(ctypes.Structure):
+    """Mirror of ``dfl_attn_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("q", P), ("k", P), ("v", P), ("g", P),
+        ("q_stride_b", I64), ("q_stride_h", I64), ("q_stride_n", I64),
+        ("k_stride_b", I64), ("k_stride_h", I64), ("k_stride_n", I64),
+        ("q_mask", P), ("k_mask", P),
+        ("bias_mode", I32), ("pos_weight", P), ("pos_bins", P), ("bias", P),
+        ("window", I32),
+        ("B", I32), ("H", I32), ("Mq", I32), ("Nk", I32), ("d", I32),
+        ("scale", F32),
+        ("o", P), ("lse", P),
+        ("grad_o", P), ("dq", P), ("dk", P), ("dv", P), ("dg", P), ("dbias", P), ("dpos_weight", P),
+    ]
+
+
+class A2TParams(ctypes.Structure):
+    """Mirror of ``dfl_a2t_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("q", P), ("k", P), ("v", P),
+        ("starts", P), ("counts", P), ("token_mask", P),
+        ("B", I32), ("H", I32), ("N", I32), ("M", I32), ("d", I32),
+        ("scale", F32),
+        ("o", P), ("lse", P),
+        ("grad_o", P), ("dq", P), ("dk", P), ("dv", P),
+    ]
+
+
+DFL_ATTN_BIAS_NONE = 0
+DFL_ATTN_BIAS_BINS = 1
+DFL_ATTN_BIAS_DENSE = 2
+DFL_ATTN_BIAS_WINDOW = 3
+
 # (name, restype, argtypes) of every exported symbol; tests check that the .so
 # exports exactly what include/dfl_amd.h declares.
 SIGNATURES = [
@@ -77,6 +114,12 @@ SIGNATURES = [
     ("dfl_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
     ("dfl_sinkhorn_fwd", I32, [ctypes.POINTER(SinkhornFwdParams), P, ctypes.c_size_t, P]),
     ("dfl_sinkhorn_bwd", I32, [ctypes.POINTER(SinkhornBwdParams), P, ctypes.c_size_t, P]),
+    ("dfl_attn_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32, I32]),
+    ("dfl_attn_fwd", I32, [ctypes.POINTER(AttnParams), P]),
+    ("dfl_attn_bwd", I32, [ctypes.POINTER(AttnParams), P, ctypes.c_size_t, P]),
+    ("dfl_a2t_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
+    ("dfl_a2t_fwd", I32, [ctypes.POINTER(A2TParams), P]),
+    ("dfl_a2t_bwd", I32, [ctypes.POINTER(A2TParams), P, ctypes.c_size_t, P]),
 ]
 
 
@@ -131,9 +174,12 @@ def require_gpu(*tensors) -> torch.device:
 _ws_cache: dict = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-filled device workspace, cached per (device, stream) and grown on demand."""
-    key = (device.index, stream_handle(device))
+def workspace(device: torch.device, nbytes: int, kind: str = "sinkhorn") -> torch.Tensor:
+    """Zero-filled device workspace, cached per (device, stream, kind) and grown on demand.
+
+    Each kind of op gets its own buffer: the Sinkhorn kernels keep tagged exchange
+    words and an error word in theirs, which other ops must never overwrite."""
+    key = (device.index, stream_handle(device), kind)
     ws = _ws_cache.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)

@@ -5,7 +5,8 @@
  *
  * Conventions (every entry point):
  *  - Plain device pointers, explicit shapes and element strides, a dtype enum;
- *    no torch types.  Potentials, accumulators and every output are fp32.
+ *    no torch types.  Accumulation is fp32; Sinkhorn potentials and outputs are
+ *    fp32, attention outputs and gradients use the element type of q.
  *  - The caller allocates every output (zero-initialised: padded positions are
  *    left untouched) and a workspace of dfl_*_workspace_size() bytes.  A workspace
  *    must be zero-filled once when it is first allocated; after that it may be
@@ -144,6 +145,88 @@ typedef struct dfl_sinkhorn_bwd_params {
 } dfl_sinkhorn_bwd_params;
 
 int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Softmax attention: O = softmax(scale * Q K^T + bias, key mask) V, rows of
+ * masked queries zero, optional sigmoid gate O *= sigma(G).  One engine for
+ *  - flash_diffusion_attn (flash_diffusion_attn.py:485-622): self attention with
+ *    bias_mode = BINS (pos_weight[h, pos_bins]) or DENSE (pair bias (B,H,N,N));
+ *  - flash_atom_attn (flash_atom_attn.py:262-354): window = 1, 32-query windows
+ *    over keys [32w - 48, 32w + 80), optional bias_mode = WINDOW ((ceil(N/32),H,32,128));
+ *  - token_to_atom_attn (cross_attn_kernel.py:555-696): cross attention Mq x Nk.
+ * q, g: (B,H,Mq,d) and k, v: (B,H,Nk,d) elements of `dtype` with element strides
+ * (unit inner stride); bias (dense / window) has the element type of q and is
+ * contiguous.  q_mask (B,Mq), k_mask (B,Nk), pos_bins (B,Mq,Nk) int32 may be NULL.
+ * Keys masked out contribute nothing; a query with no valid key gets a zero row.
+ * Forward outputs: o (B,H,Mq,d) element type of q, contiguous; lse (B,H,Mq) fp32.
+ * Backward inputs: grad_o (B,H,Mq,d) contiguous, plus the forward's o and lse;
+ * outputs (element type of q, contiguous): dq, dk, dv; dg if g; dbias if a dense
+ * or window bias is given (may be NULL); dpos_weight (H,68) fp32 for BINS (may be NULL).
+ */
+enum dfl_attn_bias { DFL_ATTN_BIAS_NONE = 0, DFL_ATTN_BIAS_BINS = 1, DFL_ATTN_BIAS_DENSE = 2, DFL_ATTN_BIAS_WINDOW = 3 };
+
+typedef struct dfl_attn_params {
+  int dtype;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  long long q_stride_b, q_stride_h, q_stride_n;
+  long long k_stride_b, k_stride_h, k_stride_n;
+  const float* q_mask;
+  const float* k_mask;
+  int bias_mode;
+  const float* pos_weight;
+  const int* pos_bins;
+  const void* bias;
+  int window;
+  int B, H, Mq, Nk, d;
+  float scale;
+  void* o;
+  float* lse;
+  const void* grad_o;
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dg;
+  void* dbias;
+  float* dpos_weight;
+} dfl_attn_params;
+
+/* Bytes of backward workspace (no zeroing needed); the forward uses none. */
+size_t dfl_attn_workspace_size(int B, int H, int Mq, int Nk, int d);
+int dfl_attn_fwd(const dfl_attn_params* p, void* stream);
+int dfl_attn_bwd(const dfl_attn_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Atom-to-token attention (cross_attn_kernel.py:424-457, 496-552, 629-661):
+ * token n attends to atoms [starts[n], starts[n] + counts[n]) (clipped to [0, M));
+ * masked or empty tokens get zero rows.  q (B,H,N,d), k, v (B,H,M,d) contiguous,
+ * element type `dtype`; starts, counts (B,N) int32; token_mask (B,N) or NULL.
+ * Forward outputs o (B,H,N,d), lse (B,H,N) fp32.  Backward outputs dq (B,H,N,d),
+ * dk, dv (B,H,M,d), element type `dtype`; the workspace holds fp32 accumulators.
+ */
+typedef struct dfl_a2t_params {
+  int dtype;
+  const void* q;
+  const void* k;
+  const void* v;
+  const int* starts;
+  const int* counts;
+  const float* token_mask;
+  int B, H, N, M, d;
+  float scale;
+  void* o;
+  float* lse;
+  const void* grad_o;
+  void* dq;
+  void* dk;
+  void* dv;
+} dfl_a2t_params;
+
+size_t dfl_a2t_workspace_size(int B, int H, int M, int d);
+int dfl_a2t_fwd(const dfl_a2t_params* p, void* stream);
+int dfl_a2t_bwd(const dfl_a2t_params* p, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

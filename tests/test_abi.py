@@ -79,7 +79,9 @@ def test_struct_layout_matches_c(lib_path):
 
     structs = header_structs()
     mirrors = {"dfl_sinkhorn_fwd_params": _lib.SinkhornFwdParams,
-               "dfl_sinkhorn_bwd_params": _lib.SinkhornBwdParams}
+               "dfl_sinkhorn_bwd_params": _lib.SinkhornBwdParams,
+               "dfl_attn_params": _lib.AttnParams,
+               "dfl_a2t_params": _lib.A2TParams}
     assert set(mirrors) == set(structs)
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for sname, fields in structs.items():
@@ -104,15 +106,24 @@ def test_struct_layout_matches_c(lib_path):
             assert getattr(cls, f).offset == c_layout[(sname, f)], (sname, f)
 
 
-def test_op_refuses_cpu_tensors():
+def test_ops_refuse_cpu_tensors():
     import torch
-    from deepfold_amd import flash_sinkhorn_attn
+    from deepfold_amd import (atom_to_token_attn, flash_atom_attn, flash_diffusion_attn, flash_sinkhorn_attn,
+                              token_to_atom_attn)
 
     B, H, N, d = 1, 2, 8, 4
     q = torch.randn(B, H, N, d)
     with pytest.raises(RuntimeError, match="GPU"):
         flash_sinkhorn_attn(q, q, q, q, torch.zeros(B, N, 3), torch.zeros(H, 68), None, torch.ones(H),
                             torch.zeros(H), torch.zeros(B, H, N), torch.zeros(B, H, N))
+    bins = torch.zeros(B, N, N, dtype=torch.int32)
+    for call in (lambda: flash_diffusion_attn(q, q, q, torch.zeros(H, 68), bins),
+                 lambda: flash_atom_attn(q, q, q),
+                 lambda: token_to_atom_attn(q, q, q),
+                 lambda: atom_to_token_attn(q, q, q, torch.zeros(B, N, dtype=torch.int32),
+                                            torch.ones(B, N, dtype=torch.int32))):
+        with pytest.raises(RuntimeError, match="GPU"):
+            call()
 
 
 def test_missing_library_fails_loudly(tmp_path):
