@@ -148,12 +148,100 @@ def cpu_baseline(cpu, budget_s=12.0):
                        f"over the layer's {B * H} heads ({spent:.1f} s), scaled to one layer by valid plan elements")
 
 
+def attention_workload(which, dev):
+    """BASELINE configs[2] (diffusion attention, dense pair bias + gate) and
+    configs[3] (atom-window attention with window bias; token-to-atom cross
+    attention), synthetic data, seed 1000 + config#.  Returns (step_fn, info)."""
+    import torch
+    from deepfold_amd import flash_atom_attn, flash_diffusion_attn, token_to_atom_attn
+
+    bf = torch.bfloat16
+    if which == "cfg3":
+        B, H, N, D = 1, 16, 1024, 24
+        g = torch.Generator().manual_seed(1003)
+        Q, K, V = ((torch.randn(B, H, N, D, generator=g) / math.sqrt(D)).to(bf).to(dev) for _ in range(3))
+        G = torch.randn(B, H, N, D, generator=g).to(bf).to(dev)
+        bias = torch.randn(B, H, N, N, generator=g).to(bf).to(dev)
+        dO = torch.randn(B, H, N, D, generator=g).to(bf).to(dev)
+
+        def step():
+            q, k, v, gg, bb = (t.detach().requires_grad_(True) for t in (Q, K, V, G, bias))
+            flash_diffusion_attn(q, k, v, None, None, pair_bias=bb, gate=gg).backward(dO)
+
+        e = 2  # bf16 bytes
+        bytes_alg = 3 * H * N * N * e + 10 * B * H * N * D * e  # bias read fwd+bwd, dbias write; Q,K,V,G,O,dO,dQ,dK,dV,dG
+        flops = 14 * B * H * N * N * D
+        info = dict(workload="BASELINE configs[2]: flash diffusion attention fwd+bwd, dense pair bias + gate",
+                    B=B, H=H, N=N, d=D)
+        return step, info, bytes_alg, flops
+    if which == "cfg4":
+        H, D, M, NT = 4, 32, 8192, 341
+        W = M // 32
+        g = torch.Generator().manual_seed(1004)
+        Qa, Ka, Va = ((torch.randn(1, H, M, D, generator=g) / math.sqrt(D)).to(bf).to(dev) for _ in range(3))
+        wb = torch.randn(W, H, 32, 128, generator=g).to(bf).to(dev)
+        Kt, Vt = ((torch.randn(1, H, NT, D, generator=g) / math.sqrt(D)).to(bf).to(dev) for _ in range(2))
+        dOa = torch.randn(1, H, M, D, generator=g).to(bf).to(dev)
+        dOc = torch.randn(1, H, M, D, generator=g).to(bf).to(dev)
+
+        def step():
+            q, k, v, bb = (t.detach().requires_grad_(True) for t in (Qa, Ka, Va, wb))
+            flash_atom_attn(q, k, v, window_bias=bb).backward(dOa)
+            q2, k2, v2 = (t.detach().requires_grad_(True) for t in (Qa, Kt, Vt))
+            token_to_atom_attn(q2, k2, v2).backward(dOc)
+
+        e = 2
+        bytes_alg = (3 * W * H * 32 * 128 * e + 8 * H * M * D * e) + (6 * H * M * D * e + 4 * H * NT * D * e)
+        flops = 14 * H * M * 128 * D + 14 * H * M * NT * D
+        info = dict(workload="BASELINE configs[3]: atom-window attention (window bias) + token-to-atom attention, "
+                             "fwd+bwd", M=M, H=H, d=D, tokens=NT)
+        return step, info, bytes_alg, flops
+    raise SystemExit(f"unknown workload {which}")
+
+
+def bench_attention(args, which):
+    import torch
+    from deepfold_amd import _lib
+
+    dev = torch.device("cuda:0")
+    step, info, bytes_alg, flops = attention_workload(which, dev)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.launch_timings = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = {}
+    for name, s_, e_ in _lib.launch_timings:
+        per.setdefault(name, []).append(s_.elapsed_time(e_))
+    _lib.launch_timings = None
+    kernel_ms = {k: sum(v) / len(v) * len(v) / args.steps for k, v in per.items()}  # per step
+    ms = wall * 1e3 / args.steps
+    dev_ms = sum(kernel_ms.values())
+    out = {
+        "metric": f"{which} attention fwd+bwd ms/step", "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seed 1000 + config#)",
+        "config": info, "kernel_ms_per_step": {k: round(v, 4) for k, v in kernel_ms.items()},
+        "roofline": {"bound": "hbm", "achieved": round(bytes_alg / (dev_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": round(bytes_alg / (dev_ms * 1e-3) / PEAK_HBM, 4),
+                     "traffic": None, "algorithmic_bytes": bytes_alg},
+        "mfma": {"achieved_tflops": round(flops / (dev_ms * 1e-3) / 1e12, 2), "peak_tflops": PEAK_MFMA_BF16 / 1e12},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"],
+                    help="cfg2 (default): the headline flash-Sinkhorn layer; cfg3 / cfg4: attention rows")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB -> 256 MiB elementwise copy (torch.neg), used to "
                          "calibrate the FETCH_SIZE / WRITE_SIZE counters")
@@ -178,6 +266,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy": {"kernel": "torch.neg", "launches": 5, "read_bytes": 4 * n,
                                              "write_bytes": 4 * n}}), flush=True)
+        return
+    if args.workload != "cfg2":
+        bench_attention(args, args.workload)
         return
     cpu, t = make_workload(dev)
     for _ in range(args.warmup):
