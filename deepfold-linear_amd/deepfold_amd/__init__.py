@@ -6,9 +6,11 @@ Module names mirror vv137/deepfold-linear's ``deepfold.model.kernels`` /
 """
 
 from . import _lib  # noqa: F401
+from .cg import CGInfo, conjugate_gradient  # noqa: F401
 from .cross_attn_kernel import atom_to_token_attn, token_to_atom_attn  # noqa: F401
 from .flash_atom_attn import flash_atom_attn  # noqa: F401
 from .flash_diffusion_attn import flash_diffusion_attn  # noqa: F401
 from .flash_sinkhorn_attn import FlashSinkhornAttn, flash_sinkhorn_attn  # noqa: F401
+from .sinkhorn_kernel import FlashSinkhornFunction, flash_sinkhorn  # noqa: F401
 
 __version__ = "0.1.0"

@@ -108,8 +108,8 @@ def test_struct_layout_matches_c(lib_path):
 
 def test_ops_refuse_cpu_tensors():
     import torch
-    from deepfold_amd import (atom_to_token_attn, flash_atom_attn, flash_diffusion_attn, flash_sinkhorn_attn,
-                              token_to_atom_attn)
+    from deepfold_amd import (atom_to_token_attn, conjugate_gradient, flash_atom_attn, flash_diffusion_attn,
+                              flash_sinkhorn, flash_sinkhorn_attn, token_to_atom_attn)
 
     B, H, N, d = 1, 2, 8, 4
     q = torch.randn(B, H, N, d)
@@ -121,7 +121,10 @@ def test_ops_refuse_cpu_tensors():
                  lambda: flash_atom_attn(q, q, q),
                  lambda: token_to_atom_attn(q, q, q),
                  lambda: atom_to_token_attn(q, q, q, torch.zeros(B, N, dtype=torch.int32),
-                                            torch.ones(B, N, dtype=torch.int32))):
+                                            torch.ones(B, N, dtype=torch.int32)),
+                 lambda: flash_sinkhorn(q, q, q, torch.zeros(B, N, 3), torch.zeros(H, 68), None, torch.ones(H),
+                                        torch.zeros(H), torch.zeros(B, H, N), torch.zeros(B, H, N)),
+                 lambda: conjugate_gradient(lambda v: v, torch.ones(4))):
         with pytest.raises(RuntimeError, match="GPU"):
             call()
 
