@@ -27,7 +27,7 @@ struct SinkFwdArgs {
   int B, H, N, d;
   int K_iter;
   float lam, r0;
-  // outputs (caller zero-initialises; padded positions are left untouched)
+  // outputs (every position written; zeros where padded)
   float* o_flat;      // (B,N,H*d)
   float* x_centroid;  // (B,H,N,3)
   float* log_u;       // (B,H,N)
@@ -70,7 +70,7 @@ struct SinkBwdArgs {
   int mode;     // 0 = reference signs, 1 = analytic adjoint
   float cg_rtol;  // CG early stop on ||r|| <= rtol ||b|| (0 = run all iterations)
   int geo_grad;   // compute d x_res / d w_dist cost terms (x given and requested)
-  // outputs (caller zero-initialises)
+  // outputs (every position written; zeros where padded)
   float* dq;        // (B,H,N,d)
   float* dk;
   float* dv;

@@ -46,44 +46,59 @@ __device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const
                             int nr, float sc, const float* __restrict__ cres, const Bias& bias, float* out,
                             float* scratch) {
   using M = Mfma<T, DP>;
+  constexpr int SCH = sweep_sch<T, DP>();
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int g = lane >> 4;
   const float isc = 1.f / sc;
+  const int ks = wave < n_str_tiles ? (n_str_tiles - wave + BWD_NW - 1) / BWD_NW : 0;
   for (int c0 = 0; c0 < nr; c0 += SK_RT) {
     const int nc = min(SK_RT, nr - c0);
-    typename M::Frag bf[SK_RT];
-    f32x4 cinit[SK_RT];
     float s[SK_RT];
 #pragma unroll
-    for (int r = 0; r < SK_RT; ++r) {
-      s[r] = 0.f;
-      if (r < nc) {
-        M::load(bf[r], res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
-        const float ci = cres[(c0 + r) * 16 + (lane & 15)] * isc;
-        cinit[r] = f32x4{ci, ci, ci, ci};
+    for (int r = 0; r < SK_RT; ++r) s[r] = 0.f;
+    for (int k0 = 0; k0 < ks; k0 += SCH) {
+      // streamed fragments, column terms and weights stay in registers for all
+      // resident tiles; slots past the wave's last tile carry w = NEG_BIG (no
+      // bias lookup, exp2 -> 0) and z = 0
+      typename M::Frag af[SCH];
+      f32x4 w[SCH], z[SCH];
+#pragma unroll
+      for (int k = 0; k < SCH; ++k) {
+        const bool live = k0 + k < ks;
+        const int st = live ? wave + BWD_NW * (k0 + k) : wave;
+        M::load(af[k], str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+        w[k] = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+        z[k] = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
+        if (!live) {
+          w[k] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+          z[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
-    }
-    for (int st = wave; st < n_str_tiles; st += BWD_NW) {
-      typename M::Frag af;
-      M::load(af, str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
-      const f32x4 w = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
-      const f32x4 z = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
 #pragma unroll
       for (int r = 0; r < SK_RT; ++r) {
-        if (r < nc) {
-          const f32x4 acc = M::qk(af, bf[r], cinit[r]);
+        if (r >= nc) continue;
+        typename M::Frag bf;
+        M::load(bf, res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
+        const float ci = cres[(c0 + r) * 16 + (lane & 15)] * isc;
+        const f32x4 cinit = f32x4{ci, ci, ci, ci};
+        f32x4 x[SCH];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            float x = __builtin_fmaf(acc[k], sc, w[k]);
+        for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
+        float acc_s = 0.f;
+#pragma unroll
+        for (int k = 0; k < SCH; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
             if (GENERAL) {
               const int ires = (rt0 + c0 + r) * 16 + (lane & 15);
-              const int jstr = st * 16 + 4 * g + k;
-              if (w[k] > 0.5f * NEG_BIG) x += TRANS ? bias(jstr, ires) : bias(ires, jstr);
+              const int jstr = (wave + BWD_NW * (k0 + k)) * 16 + 4 * g + e;
+              if (w[k][e] > 0.5f * NEG_BIG) xv += TRANS ? bias(jstr, ires) : bias(ires, jstr);
             }
-            s[r] = __builtin_fmaf(fast_exp2(x), z[k], s[r]);
+            acc_s = __builtin_fmaf(fast_exp2(xv), z[k][e], acc_s);
           }
-        }
+        s[r] += acc_s;
       }
     }
 #pragma unroll
@@ -306,6 +321,20 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   int t0, t1;
   stripe(n_tiles, member, a.G, t0, t1);
   const int nr = t1 - t0;
+  // Every output position is written: rows past the last valid tile (owned by no
+  // stripe) are zeroed here, row i by member i % G; invalid stripe rows get zeros
+  // where the stripe's outputs are written.
+  for (int i = n_tiles * 16 + member; i < N; i += a.G) {
+    for (int c = threadIdx.x; c < d; c += BWD_NT) {
+      a.dq[(bh * N + i) * d + c] = 0.f;
+      a.dk[(bh * N + i) * d + c] = 0.f;
+      a.dv[(bh * N + i) * d + c] = 0.f;
+    }
+    if (threadIdx.x == 0) {
+      a.dlog_mu[bh * N + i] = 0.f;
+      a.dlog_nu[bh * N + i] = 0.f;
+    }
+  }
   if (n == 0 || nr <= 0) {
     // owns nothing: publish empty partials so the finaliser can sum every slot
     for (int k = threadIdx.x; k < 68; k += BWD_NT) a.dpw_part[wg_id * 68 + k] = 0.f;
@@ -480,11 +509,12 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int j = tile * 16 + 4 * g + r;
-            if (j < n && valid[j]) {
+            if (j < N) {
+              const bool jv = j < n && valid[j];
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 const int col = c * 16 + (lane & 15);
-                if (col < d) a.dv[(bh * N + j) * d + col] = dvacc[k][c][r];
+                if (col < d) a.dv[(bh * N + j) * d + col] = jv ? dvacc[k][c][r] : 0.f;
               }
             }
           }
@@ -604,10 +634,10 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     __syncthreads();
   }
   // marginal gradients (flash_sinkhorn_attn.py:645-646; analytic: d log_mu = kappa lambda_u = -kappa z_u)
-  for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) {
-    if (!valid[i]) continue;
-    a.dlog_mu[bh * N + i] = (a.mode == 1 ? -kappa : kappa) * zu[i];
-    a.dlog_nu[bh * N + i] = kappa * zvv[i];
+  for (int i = r_lo + (int)threadIdx.x; i < min(t1 * 16, N); i += BWD_NT) {
+    const bool iv = i < n && valid[i];
+    a.dlog_mu[bh * N + i] = iv ? (a.mode == 1 ? -kappa : kappa) * zu[i] : 0.f;
+    a.dlog_nu[bh * N + i] = iv ? kappa * zvv[i] : 0.f;
   }
 
   // per-row helper vectors for R2 / C2
@@ -741,11 +771,12 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int i = tile * 16 + 4 * g + r;
-            if (i < n && valid[i]) {
+            if (i < N) {
+              const bool iv = i < n && valid[i];
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 const int col = c * 16 + (lane & 15);
-                if (col < d) a.dq[(bh * N + i) * d + col] = -inv_sqrt_d * dqacc[k][c][r];
+                if (col < d) a.dq[(bh * N + i) * d + col] = iv ? -inv_sqrt_d * dqacc[k][c][r] : 0.f;
               }
             }
           }
@@ -868,11 +899,12 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int j = tile * 16 + 4 * g + r;
-            if (j < n && valid[j]) {
+            if (j < N) {
+              const bool jv = j < n && valid[j];
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 const int col = c * 16 + (lane & 15);
-                if (col < d) a.dk[(bh * N + j) * d + col] = -inv_sqrt_d * dkacc[k][c][r];
+                if (col < d) a.dk[(bh * N + j) * d + col] = jv ? -inv_sqrt_d * dkacc[k][c][r] : 0.f;
               }
             }
           }
@@ -924,6 +956,8 @@ __global__ void __launch_bounds__(256) sinkhorn_bwd_prep_kernel(SinkBwdArgs a) {
       s = sigm(to_f32(Gg[(size_t)i * a.sn + c]));
       a.dg[((size_t)bh * N + i) * d + c] = s * (1.f - s) * oa * go;
     }
+  } else if (a.g && i < N && c < d) {
+    a.dg[((size_t)bh * N + i) * d + c] = 0.f;
   }
   const float g = s * go;
   const T hi = from_f32<T>(g);
@@ -963,7 +997,7 @@ __global__ void sinkhorn_bwd_finalize_kernel(SinkBwdArgs a, float* dx, float* dp
     float s = 0.f;
     for (int b = 0; b < a.B; ++b)
       for (int m = 0; m < a.G; ++m) s += a.dpw_part[(((size_t)b * a.H + h) * a.G + m) * 68 + k];
-    if (dpw && a.bins) dpw[tid] = s;
+    if (dpw) dpw[tid] = s;  // zeros without position bins (their partials are zero)
   }
   if (tid < a.H) {
     float s = 0.f;

@@ -17,6 +17,8 @@ constexpr int SK_RT = 4;    // resident tiles per register chunk
 // Scratch floats needed by the sweeps of an NT-thread workgroup.
 template <int NT> constexpr int sweep_scratch() { return 2 * (NT / WAVE) * SK_RT * 16; }
 constexpr int LSE_SCRATCH = 2 * SK_NW * SK_RT * 16;
+// Streamed tiles a wave keeps in registers per pass of a sweep.
+template <typename T, int DP> constexpr int sweep_sch() { return (sizeof(T) == 2 && DP == 32) ? 6 : 4; }
 
 // Position-bin / geometry bias of the cost, in log2 units of the logit:
 //   bias(i, j) = -(log2 e / eps) * (pw[bins_ij] + w * d_ij / (r0 + d_ij)).
@@ -202,57 +204,77 @@ __device__ __forceinline__ void lse_sweep(const T* __restrict__ res_lds, const T
                           float* scratch, unsigned* s_reset, Pub publish) {
   using M = Mfma<T, DP>;
   constexpr int NW = NT / WAVE;
+  constexpr int SCH = sweep_sch<T, DP>();
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int g = lane >> 4;
   const float isc = 1.f / sc;
+  // this wave's streamed tiles: st = wave + NW * k, k < ks
+  const int ks = wave < n_str_tiles ? (n_str_tiles - wave + NW - 1) / NW : 0;
   for (int c0 = 0; c0 < nr; c0 += SK_RT) {
     const int nc = min(SK_RT, nr - c0);
-    typename M::Frag bf[SK_RT];
-    f32x4 cinit[SK_RT];
     float m[SK_RT], s[SK_RT];
 #pragma unroll
     for (int r = 0; r < SK_RT; ++r) {
       m[r] = NEG_BIG;
       s[r] = 0.f;
-      cinit[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (r < nc) {
-        M::load(bf[r], res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
-        if (!ONLINE) {
-          const float ci = -shift2[(c0 + r) * 16 + (lane & 15)] * isc;
-          cinit[r] = f32x4{ci, ci, ci, ci};
-        }
-      }
     }
-    for (int st = wave; st < n_str_tiles; st += NW) {
-      typename M::Frag af;
-      M::load(af, str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
-      const f32x4 w = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+    for (int k0 = 0; k0 < ks; k0 += SCH) {
+      // SCH streamed fragments and their column terms stay in registers for all
+      // resident tiles; slots past the wave's last tile repeat a valid tile with
+      // w = NEG_BIG, so they add exp2(-huge) = 0 without a branch.
+      typename M::Frag af[SCH];
+      f32x4 w[SCH];
+#pragma unroll
+      for (int k = 0; k < SCH; ++k) {
+        const bool live = k0 + k < ks;
+        const int st = live ? wave + NW * (k0 + k) : wave;
+        M::load(af[k], str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+        w[k] = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+        if (!live) w[k] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+      }
 #pragma unroll
       for (int r = 0; r < SK_RT; ++r) {
-        if (r < nc) {
-          const f32x4 acc = M::qk(af, bf[r], cinit[r]);
-          float x[4];
+        if (r >= nc) continue;
+        typename M::Frag bf;
+        M::load(bf, res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
+        f32x4 cinit = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (!ONLINE) {
+          const float ci = -shift2[(c0 + r) * 16 + (lane & 15)] * isc;
+          cinit = f32x4{ci, ci, ci, ci};
+        }
+        f32x4 x[SCH];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            x[k] = __builtin_fmaf(acc[k], sc, w[k]);
+        for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
+#pragma unroll
+        for (int k = 0; k < SCH; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
             if (GENERAL) {
               const int ires = (rt0 + c0 + r) * 16 + (lane & 15);
-              const int jstr = st * 16 + 4 * g + k;
-              if (w[k] > 0.5f * NEG_BIG) x[k] += TRANS ? bias(jstr, ires) : bias(ires, jstr);
+              const int jstr = (wave + NW * (k0 + k)) * 16 + 4 * g + e;
+              if (w[k][e] > 0.5f * NEG_BIG) xv += TRANS ? bias(jstr, ires) : bias(ires, jstr);
             }
+            x[k][e] = xv;
           }
-          if (ONLINE) {
-            const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-            const float mn = fmaxf(m[r], tm);
-            float acc_s = s[r] * fast_exp2(m[r] - mn);
+        if (ONLINE) {
+          float tm = NEG_BIG;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) acc_s += fast_exp2(x[k] - mn);
-            s[r] = acc_s;
-            m[r] = mn;
-          } else {
-            s[r] += (fast_exp2(x[0]) + fast_exp2(x[1])) + (fast_exp2(x[2]) + fast_exp2(x[3]));
-          }
+          for (int k = 0; k < SCH; ++k) tm = fmaxf(tm, fmaxf(fmaxf(x[k][0], x[k][1]), fmaxf(x[k][2], x[k][3])));
+          const float mn = fmaxf(m[r], tm);
+          float acc_s = s[r] * fast_exp2(m[r] - mn);
+#pragma unroll
+          for (int k = 0; k < SCH; ++k)
+            acc_s += (fast_exp2(x[k][0] - mn) + fast_exp2(x[k][1] - mn)) + (fast_exp2(x[k][2] - mn) + fast_exp2(x[k][3] - mn));
+          s[r] = acc_s;
+          m[r] = mn;
+        } else {
+          float acc_s = 0.f;
+#pragma unroll
+          for (int k = 0; k < SCH; ++k)
+            acc_s += (fast_exp2(x[k][0]) + fast_exp2(x[k][1])) + (fast_exp2(x[k][2]) + fast_exp2(x[k][3]));
+          s[r] += acc_s;
         }
       }
     }

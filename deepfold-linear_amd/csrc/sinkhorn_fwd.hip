@@ -78,6 +78,25 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   int t0, t1;
   stripe(n_tiles, member, a.G, t0, t1);
   const int nr = t1 - t0;
+  {
+    // Every output position is written: rows past the last valid tile, which no
+    // stripe owns, are zeroed here (row i by member i % G); invalid rows inside
+    // stripes are zeroed where the stripe's outputs are written.
+    const size_t bh0 = (size_t)b * a.H + h;
+    for (int i = n_tiles * 16 + member; i < N; i += a.G) {
+      for (int c = threadIdx.x; c < d; c += FWD_NT) {
+        a.o_avg[(bh0 * N + i) * d + c] = 0.f;
+        a.o_flat[((size_t)b * N + i) * (size_t)(a.H * d) + (size_t)h * d + c] = 0.f;
+      }
+      if (threadIdx.x < 3) a.x_centroid[(bh0 * N + i) * 3 + threadIdx.x] = 0.f;
+      if (threadIdx.x == 0) {
+        a.log_u[bh0 * N + i] = 0.f;
+        a.log_v[bh0 * N + i] = 0.f;
+        a.log_z[bh0 * N + i] = 0.f;
+        a.col_lse[bh0 * N + i] = 0.f;
+      }
+    }
+  }
   if (n == 0 || nr <= 0) return;  // owns nothing; no other member waits on it
 
   const size_t qoff = (size_t)b * a.sb + (size_t)h * a.sh;
@@ -235,11 +254,26 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       a.log_u[bh * N + irow] = u;
       a.log_z[bh * N + irow] = u + l2 * LN2;
       a.log_v[bh * N + irow] = vecV[irow] * LN2;
+    } else if (lane < 16 && irow < N) {  // invalid row of my stripe
+      const size_t o = (bh * N + irow) * 3;
+      a.x_centroid[o + 0] = a.x_centroid[o + 1] = a.x_centroid[o + 2] = 0.f;
+      a.log_u[bh * N + irow] = a.log_z[bh * N + irow] = a.log_v[bh * N + irow] = 0.f;
+      a.col_lse[bh * N + irow] = 0.f;
     }
     // O tile layout: lane holds O[row = 4g + r][col = c*16 + lane%16]
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = tile * 16 + 4 * g + r;
+      if (row < N && !(row < n && valid[row])) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int col = c * 16 + (lane & 15);
+          if (col < d) {
+            a.o_avg[(bh * N + row) * d + col] = 0.f;
+            a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = 0.f;
+          }
+        }
+      }
       if (row < n && valid[row]) {
         const float den = 1.f + 1e-6f * fast_exp2(mx2[qloc + 4 * g + r] - lse2[qloc + 4 * g + r]);
 #pragma unroll

@@ -79,13 +79,14 @@ class FlashSinkhornAttn(torch.autograd.Function):
         lu0, lv0 = _f32(log_u_init), _f32(log_v_init)
         m = _f32(mask)
         f32 = dict(device=dev, dtype=torch.float32)
-        o_flat = torch.zeros(B, N, H * d, **f32)
-        x_c = torch.zeros(B, H, N, 3, **f32)
-        log_u = torch.zeros(B, H, N, **f32)
-        log_v = torch.zeros(B, H, N, **f32)
-        o_avg = torch.zeros(B, H, N, d, **f32)
-        log_z = torch.zeros(B, H, N, **f32)
-        col_lse = torch.zeros(B, H, N, **f32)
+        # the kernel writes every position (zeros where padded)
+        o_flat = torch.empty(B, N, H * d, **f32)
+        x_c = torch.empty(B, H, N, 3, **f32)
+        log_u = torch.empty(B, H, N, **f32)
+        log_v = torch.empty(B, H, N, **f32)
+        o_avg = torch.empty(B, H, N, d, **f32)
+        log_z = torch.empty(B, H, N, **f32)
+        col_lse = torch.empty(B, H, N, **f32)
         lib = _lib.load()
         nbytes = lib.dfl_sinkhorn_workspace_size(B, H, N)
         ws = _lib.workspace(dev, nbytes)
@@ -129,19 +130,20 @@ class FlashSinkhornAttn(torch.autograd.Function):
             grad_o_flat = torch.zeros(B, N, H * d, **f32)
         go = grad_o_flat.detach().to(torch.float32).contiguous()
         gxc = None if grad_xc is None else grad_xc.detach().to(torch.float32).contiguous()
-        dq = torch.zeros(B, H, N, d, **f32)
-        dk = torch.zeros(B, H, N, d, **f32)
-        dv = torch.zeros(B, H, N, d, **f32)
-        dg = torch.zeros(B, H, N, d, **f32)
-        dlmu = torch.zeros(B, H, N, **f32)
-        dlnu = torch.zeros(B, H, N, **f32)
+        # the kernels write every position of these (zeros where padded)
+        dq = torch.empty(B, H, N, d, **f32)
+        dk = torch.empty(B, H, N, d, **f32)
+        dv = torch.empty(B, H, N, d, **f32)
+        dg = torch.empty(B, H, N, d, **f32)
+        dlmu = torch.empty(B, H, N, **f32)
+        dlnu = torch.empty(B, H, N, **f32)
         # optional outputs: NULL skips their per-element work in the kernel
         need_dx = x is not None and ctx.needs_input_grad[4]
         need_dpw = pw is not None and ctx.needs_input_grad[5]
         need_dw = wd is not None and ctx.needs_input_grad[8]
-        dx = torch.zeros(B, N, 3, **f32) if need_dx else None
-        dpw = torch.zeros(H, 68, **f32) if need_dpw else None
-        dw = torch.zeros(H, **f32) if need_dw else None
+        dx = torch.empty(B, N, 3, **f32) if need_dx else None
+        dpw = torch.empty(H, 68, **f32) if need_dpw else None
+        dw = torch.empty(H, **f32) if need_dw else None
         lib = _lib.load()
         ws = _lib.workspace(dev, lib.dfl_sinkhorn_workspace_size(B, H, N))
         sb, sh, sn, _ = q.stride()

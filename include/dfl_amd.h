@@ -7,8 +7,10 @@
  *  - Plain device pointers, explicit shapes and element strides, a dtype enum;
  *    no torch types.  Accumulation is fp32; Sinkhorn potentials and outputs are
  *    fp32, attention outputs and gradients use the element type of q.
- *  - The caller allocates every output (zero-initialised: padded positions are
- *    left untouched) and a workspace of dfl_*_workspace_size() bytes.  A workspace
+ *  - The caller allocates every output; the kernels write every position of it
+ *    (zeros at padded positions), so no initialisation is needed, except where
+ *    an entry point says otherwise.  The caller also provides a workspace of
+ *    dfl_*_workspace_size() bytes.  A workspace
  *    must be zero-filled once when it is first allocated; after that it may be
  *    reused by any number of calls without clearing.  Calls that share a
  *    workspace must not overlap in time.
@@ -98,7 +100,7 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
  * term of dC and d log_mu change sign).  Padded tokens (mask == 0) are excluded,
  * which equals evaluating each sample on its unpadded slice.
  * Inputs are the forward's inputs and saved outputs plus grad_o (B,N,H*d) fp32 and
- * grad_xc (B,H,N,3) fp32 (may be NULL).  Outputs (fp32, zero-initialised by the caller):
+ * grad_xc (B,H,N,3) fp32 (may be NULL).  Outputs (fp32, fully written):
  * dq, dk, dv, dg (B,H,N,d), dlog_mu, dlog_nu (B,H,N); optional (NULL = not requested,
  * which also skips their per-element work): dx_res (B,N,3), dpos_weight (H,68), dw_dist (H,).
  */
@@ -161,7 +163,9 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
  * Forward outputs: o (B,H,Mq,d) element type of q, contiguous; lse (B,H,Mq) fp32.
  * Backward inputs: grad_o (B,H,Mq,d) contiguous, plus the forward's o and lse;
  * outputs (element type of q, contiguous): dq, dk, dv; dg if g; dbias if a dense
- * or window bias is given (may be NULL); dpos_weight (H,68) fp32 for BINS (may be NULL).
+ * or window bias is given (may be NULL; a window bias gradient must be
+ * zero-filled by the caller: entries outside each window are not written);
+ * dpos_weight (H,68) fp32 for BINS (may be NULL).
  */
 enum dfl_attn_bias { DFL_ATTN_BIAS_NONE = 0, DFL_ATTN_BIAS_BINS = 1, DFL_ATTN_BIAS_DENSE = 2, DFL_ATTN_BIAS_WINDOW = 3 };
 
