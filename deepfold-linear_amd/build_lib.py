@@ -1,5 +1,7 @@
 """Build libdfl_amd.so in-tree with hipcc for gfx950.
 
+Every source compiles to its own object in parallel, then one link step.
+
 Usage: python deepfold-linear_amd/build_lib.py  (also called by __graft_entry__.build()).
 """
 
@@ -12,28 +14,48 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "deepfold_amd", "libdfl_amd.so")
-SOURCES = ["capi.hip", "sinkhorn_fwd.hip", "sinkhorn_bwd.hip", "attention.hip"]
+OBJ_DIR = os.path.join(HERE, "_build")
+SOURCES = ["capi.hip", "sinkhorn_fwd.hip", "sinkhorn_fwd_stream.hip", "sinkhorn_bwd.hip",
+           "sinkhorn_bwd_stream.hip", "attention.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # keep hipcc from forming packed-fp32 ops by itself
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
 
+def _clean(text: str) -> str:
+    return "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l)
+
+
 def build(verbose: bool = True) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    jobs = []
+    for src in SOURCES:
+        obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
+        cmd = [HIPCC, *FLAGS, "-c", "-o", obj, os.path.join(CSRC, src)]
+        if verbose:
+            print("[build]", " ".join(cmd), flush=True)
+        jobs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    errors = []
+    for src, _, proc in jobs:
+        out, _ = proc.communicate()
+        out = _clean(out)
+        if proc.returncode != 0:
+            errors.append(f"{src}: hipcc failed ({proc.returncode}):\n{out}")
+        elif out.strip() and verbose:
+            print(out, flush=True)
+    if errors:
+        raise RuntimeError("\n".join(errors))
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, *srcs]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *[obj for _, obj, _ in jobs]]
     if verbose:
         print("[build]", " ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    out = "\n".join(l for l in (proc.stdout + proc.stderr).splitlines() if "packed-fp32-ops" not in l)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{out}")
-    if out.strip() and verbose:
-        print(out, flush=True)
+        raise RuntimeError(f"link failed ({proc.returncode}):\n{_clean(proc.stdout + proc.stderr)}")
     os.replace(tmp, OUT)
     return OUT
 

@@ -13,12 +13,17 @@
 #include "sinkhorn_args.h"
 
 namespace dfl {
-size_t sinkhorn_fwd_lds_bytes(int N, int DP, int elem, int G);
+size_t sinkhorn_fwd_lds_bytes(int N, int DP, int elem, int G, bool stream);
 hipError_t launch_sinkhorn_fwd(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                bool coop);
-size_t sinkhorn_bwd_lds_bytes(int N, int DP, int elem, int G);
+hipError_t launch_sinkhorn_fwd_stream(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
+                                      bool coop);
+hipError_t launch_sinkhorn_pad(const PadArgs& p, bool bf16_in, int DP, hipStream_t stream);
+size_t sinkhorn_bwd_lds_bytes(int N, int DP, int elem, int G, int CH, bool stream);
 hipError_t launch_sinkhorn_bwd(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                bool coop);
+hipError_t launch_sinkhorn_bwd_stream(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
+                                      bool coop);
 hipError_t launch_sinkhorn_bwd_prep(const SinkBwdArgs& a, bool bf16_in, int DP, hipStream_t stream);
 hipError_t launch_sinkhorn_bwd_finalize(const SinkBwdArgs& a, float* dx, float* dpw, float* dw,
                                         hipStream_t stream);
@@ -101,6 +106,43 @@ size_t partials_bytes(int B, int H, int N, int G) {
 // Prepared backward operands, sized for the widest case (d <= 64, fp32):
 // go_hi, go_lo, go_t of B*H*Np*64 elements each, then D (B*H*Np floats).
 size_t prep_operand_bytes(int B, int H, int N) { return (size_t)B * H * np32(N) * 64 * 4; }
+
+// Stream-mode region (after the backward's prepared operands), sized for the
+// widest case: padded Q, K and transposed V (prep_operand_bytes each), padded
+// coordinates (B*Np*3 floats), then the backward's per-workgroup vectors.
+constexpr int STREAM_VECS = 19;  // dfl::BWD_STREAM_VECS
+constexpr size_t LDS_LIMIT = 160 * 1024;
+size_t stream_region_bytes(int B, int H, int N, int G) {
+  const size_t np = np32(N);
+  size_t b = 3 * prep_operand_bytes(B, H, N);
+  b += ((size_t)B * np * 3 * 4 + 255) / 256 * 256;
+  b += (size_t)B * H * G * STREAM_VECS * np * 4;
+  return (b + 255) / 256 * 256;
+}
+size_t stream_region_offset(int B, int H, int N, int G) {
+  size_t off = WS_HEADER + xch_words(B, H, N) * 8 + partials_bytes(B, H, N, G);
+  off += 3 * prep_operand_bytes(B, H, N) + (size_t)B * H * np32(N) * 4;
+  return (off + 255) / 256 * 256;
+}
+
+struct StreamPtrs {
+  void* qp;
+  void* kp;
+  void* vt;
+  float* xs_p;
+  float* vec;
+};
+StreamPtrs stream_ptrs(void* ws, int B, int H, int N, int G) {
+  unsigned char* base = static_cast<unsigned char*>(ws) + stream_region_offset(B, H, N, G);
+  const size_t opb = prep_operand_bytes(B, H, N);
+  StreamPtrs p;
+  p.qp = base;
+  p.kp = base + opb;
+  p.vt = base + 2 * opb;
+  p.xs_p = reinterpret_cast<float*>(base + 3 * opb);
+  p.vec = reinterpret_cast<float*>(base + 3 * opb + ((size_t)B * np32(N) * 3 * 4 + 255) / 256 * 256);
+  return p;
+}
 
 // Query-range splits of the attention dK/dV pass: enough workgroups to cover the
 // chip when keys are few (token-to-atom: 341 keys, 8192 queries).
@@ -192,10 +234,7 @@ const char* dfl_version(void) { return "deepfold_amd 0.1.0 (gfx950)"; }
 size_t dfl_sinkhorn_workspace_size(int B, int H, int N) {
   if (B <= 0 || H <= 0 || N <= 0) return 0;
   const int G = group_size(B, H, N);
-  size_t bytes = WS_HEADER + xch_words(B, H, N) * 8;
-  bytes += partials_bytes(B, H, N, G);
-  bytes += 3 * prep_operand_bytes(B, H, N) + (size_t)B * H * np32(N) * 4;
-  return (bytes + 255) / 256 * 256;
+  return stream_region_offset(B, H, N, G) + stream_region_bytes(B, H, N, G);
 }
 
 int dfl_workspace_error(const void* workspace, void* stream) {
@@ -225,11 +264,15 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
   if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
   const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
   if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_STREAM) return fail("unknown storage %d", p->storage);
   const int G = group_size(p->B, p->H, p->N);
   const int elem = p->dtype == DFL_BF16 ? 2 : 4;
-  const size_t lds = dfl::sinkhorn_fwd_lds_bytes(p->N, DP, elem, G);
-  if (lds > 160 * 1024)
-    return fail("N=%d, d=%d exceeds the LDS-resident limit of this build (needs %zu bytes)", p->N, p->d, lds);
+  const size_t lds_res = dfl::sinkhorn_fwd_lds_bytes(p->N, DP, elem, G, false);
+  const bool stream_mode = p->storage == DFL_STORAGE_STREAM || (p->storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT);
+  const size_t lds = stream_mode ? dfl::sinkhorn_fwd_lds_bytes(p->N, DP, elem, G, true) : lds_res;
+  if (lds > LDS_LIMIT)
+    return fail("N=%d, d=%d, %s storage needs %zu bytes of LDS per workgroup (limit %zu)", p->N, p->d,
+                stream_mode ? "stream" : "resident", lds, LDS_LIMIT);
 
   dfl::SinkFwdArgs a;
   memset(&a, 0, sizeof(a));
@@ -248,7 +291,23 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
   a.G = G;
   a.salt = next_salt();
   const bool coop = G > 1;  // members wait on each other: all must be co-resident
-  hipError_t e = dfl::launch_sinkhorn_fwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  hipError_t e;
+  if (stream_mode) {
+    const StreamPtrs sp = stream_ptrs(workspace, p->B, p->H, p->N, G);
+    dfl::PadArgs pa;
+    memset(&pa, 0, sizeof(pa));
+    pa.q = p->q; pa.k = p->k; pa.v = p->v;
+    pa.sb = p->stride_b; pa.sh = p->stride_h; pa.sn = p->stride_n;
+    pa.x = p->x_res; pa.mask = p->mask;
+    pa.B = p->B; pa.H = p->H; pa.N = p->N; pa.d = p->d;
+    pa.qp = sp.qp; pa.kp = sp.kp; pa.vt = sp.vt; pa.xs_p = sp.xs_p;
+    e = dfl::launch_sinkhorn_pad(pa, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "sinkhorn pad launch");
+    a.qp = sp.qp; a.kp = sp.kp; a.vt = sp.vt; a.xs_p = sp.xs_p;
+    e = dfl::launch_sinkhorn_fwd_stream(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  } else {
+    e = dfl::launch_sinkhorn_fwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  }
   if (e != hipSuccess) return hip_fail(e, "sinkhorn forward launch");
   return 0;
 }
@@ -270,11 +329,22 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
   const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
   if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_STREAM) return fail("unknown storage %d", p->storage);
   const int G = group_size(p->B, p->H, p->N);
   const int elem = p->dtype == DFL_BF16 ? 2 : 4;
-  const size_t lds = dfl::sinkhorn_bwd_lds_bytes(p->N, DP, elem, G);
-  if (lds > 160 * 1024)
-    return fail("N=%d, d=%d exceeds the LDS-resident limit of this build (needs %zu bytes)", p->N, p->d, lds);
+  int CH = ((p->N + 31) / 32) * 32 < 256 ? ((p->N + 31) / 32) * 32 : 256;  // streamed rows per LDS chunk
+  const size_t lds_res = dfl::sinkhorn_bwd_lds_bytes(p->N, DP, elem, G, CH, false);
+  const bool stream_mode = p->storage == DFL_STORAGE_STREAM || (p->storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT);
+  size_t lds = lds_res;
+  if (stream_mode) {
+    // the largest chunk (multiple of 32 rows) whose staging fits next to the stripes
+    for (; CH > 32 && dfl::sinkhorn_bwd_lds_bytes(p->N, DP, elem, G, CH, true) > LDS_LIMIT; CH -= 32) {
+    }
+    lds = dfl::sinkhorn_bwd_lds_bytes(p->N, DP, elem, G, CH, true);
+  }
+  if (lds > LDS_LIMIT)
+    return fail("N=%d, d=%d, %s storage needs %zu bytes of LDS per workgroup (limit %zu)", p->N, p->d,
+                stream_mode ? "stream" : "resident", lds, LDS_LIMIT);
 
   dfl::SinkBwdArgs a;
   memset(&a, 0, sizeof(a));
@@ -306,10 +376,26 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   a.dcoef = reinterpret_cast<float*>(cur + 3 * opb);
   a.G = G;
   a.salt = next_salt();
+  a.ch = CH;
   const bool coop = G > 1;
   hipError_t e = dfl::launch_sinkhorn_bwd_prep(a, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward prep launch");
-  e = dfl::launch_sinkhorn_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  if (stream_mode) {
+    const StreamPtrs sp = stream_ptrs(workspace, p->B, p->H, p->N, G);
+    dfl::PadArgs pa;
+    memset(&pa, 0, sizeof(pa));
+    pa.q = p->q; pa.k = p->k; pa.v = p->v;
+    pa.sb = p->stride_b; pa.sh = p->stride_h; pa.sn = p->stride_n;
+    pa.mask = p->mask;
+    pa.B = p->B; pa.H = p->H; pa.N = p->N; pa.d = p->d;
+    pa.qp = sp.qp; pa.kp = sp.kp;  // V^T and coordinates are not needed by the backward
+    e = dfl::launch_sinkhorn_pad(pa, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "sinkhorn pad launch");
+    a.qp = sp.qp; a.kp = sp.kp; a.vec_ws = sp.vec;
+    e = dfl::launch_sinkhorn_bwd_stream(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  } else {
+    e = dfl::launch_sinkhorn_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
+  }
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward launch");
   e = dfl::launch_sinkhorn_bwd_finalize(a, p->dx_res, p->dpos_weight, p->dw_dist, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward finalize launch");

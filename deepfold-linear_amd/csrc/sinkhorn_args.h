@@ -40,6 +40,11 @@ struct SinkFwdArgs {
   uint32_t* err;  // error word
   int G;          // workgroups per (b,h)
   uint32_t salt;  // 20-bit call salt for exchange tags
+  // stream mode only (sinkhorn_pad_kernel output): zero-padded operand copies
+  const void* qp;     // [B*H][Np][DP]
+  const void* kp;     // [B*H][Np][DP]
+  const void* vt;     // [B*H][DP][Np]
+  const float* xs_p;  // [B][Np][3]
 };
 
 // Backward (flash_sinkhorn_attn.py:246-667 semantics, plus analytic mode / CG).
@@ -90,6 +95,26 @@ struct SinkBwdArgs {
   float* dcoef;   // [B*H][Np]      D_i = gO_i.O_avg_i + dxc_i.xc_i
   int G;
   uint32_t salt;
+  int ch;         // streamed rows per LDS chunk in the heavy passes (multiple of 32)
+  // stream mode only
+  const void* qp;  // [B*H][Np][DP] zero-padded copies (sinkhorn_pad_kernel)
+  const void* kp;
+  float* vec_ws;   // per-workgroup vectors, BWD_STREAM_VECS * Np floats each
+};
+
+// Zero-padded operand copies for stream mode, written by sinkhorn_pad_kernel.
+struct PadArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  long long sb, sh, sn;
+  const float* x;     // (B,N,3) or null
+  const float* mask;  // (B,N) or null
+  int B, H, N, d;
+  void* qp;     // [B*H][Np][DP]
+  void* kp;     // [B*H][Np][DP]
+  void* vt;     // [B*H][DP][Np] (null: not needed)
+  float* xs_p;  // [B][Np][3] (null: not needed)
 };
 
 }  // namespace dfl

@@ -1,0 +1,1015 @@
+// Flash-Sinkhorn IFT backward on gfx950 (persistent per-(b,h) workgroup groups).
+//
+// Restates FlashSinkhornAttn.backward of vv137/deepfold-linear
+// (src/deepfold/model/kernels/flash_sinkhorn_attn.py:246-667) per (b,h), on the
+// valid tokens only (the reference ignores the mask; per-sample evaluation on the
+// unpadded slice is the consistent definition):
+//
+//   gO = sigma(G) dO,  dG = sigma(1-sigma) O_avg dO,  D_i = gO_i.O_i + dxc_i.xc_i
+//   T_ij = exp(u_i + L_ij + v_j - logZ_i)      (= S_row_ij)
+//   S_col_ij = exp(L_ij + u_i - col_lse_j)      (= T_ij r_i / c_j)
+//   gls = T (dT - D_i),  dT_ij = gO_i.V_j + dxc_i.x_j,  g_v = sum_i gls
+//   (I - kappa^2 S_row^T S_col) z_v = g_v,  z_u = kappa S_col z_v
+//   dC = -(1/eps) gls - (kappa/eps) z_u_i S_row + sgn (kappa/eps) z_v_j S_col
+//        (sgn = -1 reference, +1 analytic adjoint)
+//   dQ = -(1/sqrt d) dC K,  dK = -(1/sqrt d) dC^T Q,  dV = T^T gO, ...
+//
+// Phases inside one launch:
+//   P0  prologue: D_i for all rows, dG for my rows
+//   C1  column pass (resident j): g_v, dV, dx transport term      -> exchange g_v
+//   S   solve: reference Gauss-Seidel sweeps, or CG on
+//       (I - kappa^2 W^T W) y = D_c^{-1/2} g_v,  W = D_r^{-1/2} T D_c^{-1/2},
+//       one exchange per half-step; CG vectors are kept redundantly (and
+//       bit-identically) in every member
+//   R2  row pass (resident i): dQ, dx_i cost term, d w_dist, d pos_weight
+//   C2  column pass (resident j): dK, dx_j cost term
+// The heavy passes (C1, R2, C2) stream their operands through LDS in chunks.
+// Two storage modes (template flag STREAM):
+//   resident: the solve keeps Q and K of the whole (b,h) in LDS, and every
+//             length-N vector (potentials, D, g_v, z, CG vectors) lives in LDS;
+//   stream  : for long sequences the solve keeps only the member's Q and K
+//             stripes in LDS and streams the other operand from zero-padded
+//             global copies; the length-N vectors live in a per-workgroup region
+//             of the workspace (L1/L2-resident).
+#pragma once
+#include "sinkhorn_args.h"
+#include "sinkhorn_engine.h"
+
+#include <algorithm>
+
+namespace dfl {
+
+constexpr int BWD_NT = 512;             // 8 waves: two per SIMD
+constexpr int BWD_NW = BWD_NT / WAVE;
+constexpr int BWD_MAXT = 2;             // resident tiles per wave in the heavy passes
+constexpr int BWD_SCRATCH = sweep_scratch<BWD_NT>();
+constexpr int BWD_STREAM_SCRATCH = stream_scratch<BWD_NT>();
+// Length-Np float vectors of one workgroup: 13 vectors + coordinates and
+// grad x_centroid ([Np][3] each).  Stream mode keeps them in the workspace.
+constexpr int BWD_STREAM_VECS = 13 + 6;
+
+// ---------------------------------------------------------------------------
+// light sweep: out[q] = sum_j exp2(sc*<res_q, str_j> + cres[q] + w2_j (+bias)) * z_j
+// Every exponent is <= 0 here (S_col, T and W are bounded by 1), so no shift.
+template <typename T, int DP, bool GENERAL, bool TRANS>
+__device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
+                            const float* __restrict__ w2, const float* __restrict__ zv, int n_str_tiles, int rt0,
+                            int nr, float sc, const float* __restrict__ cres, const Bias& bias, float* out,
+                            float* scratch) {
+  using M = Mfma<T, DP>;
+  constexpr int SCH = sweep_sch<T, DP>();
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  const int g = lane >> 4;
+  const float isc = 1.f / sc;
+  const int ks = wave < n_str_tiles ? (n_str_tiles - wave + BWD_NW - 1) / BWD_NW : 0;
+  for (int c0 = 0; c0 < nr; c0 += SK_RT) {
+    const int nc = min(SK_RT, nr - c0);
+    float s[SK_RT];
+#pragma unroll
+    for (int r = 0; r < SK_RT; ++r) s[r] = 0.f;
+    for (int k0 = 0; k0 < ks; k0 += SCH) {
+      // streamed fragments, column terms and weights stay in registers for all
+      // resident tiles; slots past the wave's last tile carry w = NEG_BIG (no
+      // bias lookup, exp2 -> 0) and z = 0
+      typename M::Frag af[SCH];
+      f32x4 w[SCH], z[SCH];
+#pragma unroll
+      for (int k = 0; k < SCH; ++k) {
+        const bool live = k0 + k < ks;
+        const int st = live ? wave + BWD_NW * (k0 + k) : wave;
+        M::load(af[k], str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+        w[k] = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+        z[k] = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
+        if (!live) {
+          w[k] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+          z[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < SK_RT; ++r) {
+        if (r >= nc) continue;
+        typename M::Frag bf;
+        M::load(bf, res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
+        const float ci = cres[(c0 + r) * 16 + (lane & 15)] * isc;
+        const f32x4 cinit = f32x4{ci, ci, ci, ci};
+        f32x4 x[SCH];
+#pragma unroll
+        for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
+        float acc_s = 0.f;
+#pragma unroll
+        for (int k = 0; k < SCH; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
+            if (GENERAL) {
+              const int ires = (rt0 + c0 + r) * 16 + (lane & 15);
+              const int jstr = (wave + BWD_NW * (k0 + k)) * 16 + 4 * g + e;
+              if (w[k][e] > 0.5f * NEG_BIG) xv += TRANS ? bias(jstr, ires) : bias(ires, jstr);
+            }
+            acc_s = __builtin_fmaf(fast_exp2(xv), z[k][e], acc_s);
+          }
+        s[r] += acc_s;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < SK_RT; ++r)
+      if (r < nc) {
+        const float ss = sum_groups(s[r]);
+        if (lane < 16) scratch[(wave * SK_RT + r) * 16 + lane] = ss;
+      }
+    __syncthreads();
+    if ((int)threadIdx.x < nc * 16) {
+      const int q = threadIdx.x, r = q >> 4, l = q & 15;
+      float ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < BWD_NW; ++w) ss += scratch[(w * SK_RT + r) * 16 + l];
+      out[c0 * 16 + q] = ss;
+    }
+    __syncthreads();
+  }
+}
+
+// Deterministic block-wide sum of f(i) over i in [0, n) (same order in every block).
+template <typename F>
+__device__ __forceinline__ float block_sum(int n, F f, float* red) {
+  float acc = 0.f;
+  for (int i = threadIdx.x; i < n; i += BWD_NT) acc += f(i);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
+  const int wave = threadIdx.x / WAVE;
+  __syncthreads();
+  if ((threadIdx.x & (WAVE - 1)) == 0) red[wave] = acc;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < BWD_NW; ++w) tot += red[w];
+  __syncthreads();
+  return tot;
+}
+
+// Gather a published vector into dst (scale 1), zeroing invalid entries and the tail.
+__device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
+                                              const unsigned char* valid, uint32_t* err, int* s_flag) {
+  if (!xch_gather<BWD_NT>(buf, n, tag, dst, 1.f, err, s_flag)) return false;  // values as published
+  for (int i = threadIdx.x; i < Np; i += BWD_NT)
+    if (i >= n || !valid[i]) dst[i] = 0.f;
+  __syncthreads();
+  return true;
+}
+
+__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
+
+constexpr int STAGE_BATCH = 4;  // 16-byte loads each thread keeps in flight while staging
+
+// Rows [r0, r0 + CH) of a row-major [.][DP] operand into LDS dst[CH][DP]
+// (zero outside rows [0, n) and columns [0, d)).  `src` rows are `sn` elements
+// apart; 16-byte vector copies when d == DP and the rows are 16-byte aligned.
+template <typename T, int DP>
+__device__ __forceinline__ void stage_chunk(T* dst, const T* __restrict__ src, long long sn, int r0, int CH, int n,
+                                            int d) {
+  constexpr int VE = 16 / sizeof(T);
+  typedef __attribute__((__vector_size__(16))) int i32x4;
+  if (d == DP && sn % VE == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    constexpr int CPR = DP / VE;
+    const int total = CH * CPR;
+    // STAGE_BATCH loads in flight per thread before the first store
+    for (int c0 = threadIdx.x; c0 < total; c0 += STAGE_BATCH * BWD_NT) {
+      i32x4 v[STAGE_BATCH];
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c / CPR, k = c - row * CPR;
+        v[u] = i32x4{0, 0, 0, 0};
+        if (c < total && r0 + row < n) v[u] = *reinterpret_cast<const i32x4*>(src + (size_t)(r0 + row) * sn + k * VE);
+      }
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c / CPR, k = c - row * CPR;
+        if (c < total) *reinterpret_cast<i32x4*>(dst + (size_t)row * DP + k * VE) = v[u];
+      }
+    }
+    return;
+  }
+  for (int e = threadIdx.x; e < CH * DP; e += BWD_NT) {
+    const int row = e / DP, col = e - row * DP;
+    const int i = r0 + row;
+    T v = from_f32<T>(0.f);
+    if (i < n && col < d) v = src[(size_t)i * sn + col];
+    dst[e] = v;
+  }
+}
+
+// Transposed: dst[DP][CH] with dst[c][row] = src[r0 + row][c].
+template <typename T, int DP>
+__device__ __forceinline__ void stage_chunk_t(T* dst, const T* __restrict__ src, long long sn, int r0, int CH, int n,
+                                              int d) {
+  constexpr int VE = 16 / sizeof(T);
+  if (d == DP && sn % VE == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    typedef __attribute__((__vector_size__(16))) int i32x4;
+    constexpr int CPR = DP / VE;
+    const int total = CH * CPR;
+    for (int c0 = threadIdx.x; c0 < total; c0 += STAGE_BATCH * BWD_NT) {
+      i32x4 w[STAGE_BATCH];
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c % CH, k = c / CH;  // consecutive threads -> consecutive rows
+        w[u] = i32x4{0, 0, 0, 0};
+        if (c < total && r0 + row < n) w[u] = *reinterpret_cast<const i32x4*>(src + (size_t)(r0 + row) * sn + k * VE);
+      }
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const int row = c % CH, k = c / CH;
+        if (c < total) {
+          T v[VE];
+          __builtin_memcpy(v, &w[u], 16);
+#pragma unroll
+          for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * CH + row] = v[e];
+        }
+      }
+    }
+    return;
+  }
+  for (int e = threadIdx.x; e < CH * DP; e += BWD_NT) {
+    const int col = e / CH, row = e - col * CH;
+    const int i = r0 + row;
+    T v = from_f32<T>(0.f);
+    if (i < n && col < d) v = src[(size_t)i * sn + col];
+    dst[e] = v;
+  }
+}
+
+// Columns [r0, r0 + CH) of a prepared transposed operand src[DP][Np] into dst[DP][CH]
+// (Np and r0 are multiples of 32 and CH of 32, so rows are 16-byte aligned).
+template <typename T, int DP>
+__device__ __forceinline__ void stage_chunk_tt(T* dst, const T* __restrict__ src, int Np, int r0, int CH) {
+  constexpr int VE = 16 / sizeof(T);
+  typedef __attribute__((__vector_size__(16))) int i32x4;
+  const int per = CH / VE;
+  const int total = DP * per;
+  for (int c0 = threadIdx.x; c0 < total; c0 += STAGE_BATCH * BWD_NT) {
+    i32x4 v[STAGE_BATCH];
+#pragma unroll
+    for (int u = 0; u < STAGE_BATCH; ++u) {
+      const int c = c0 + u * BWD_NT;
+      const int k = c / per, e = c - k * per;
+      v[u] = i32x4{0, 0, 0, 0};
+      if (c < total && r0 + e * VE < Np) v[u] = *reinterpret_cast<const i32x4*>(src + (size_t)k * Np + r0 + e * VE);
+    }
+#pragma unroll
+    for (int u = 0; u < STAGE_BATCH; ++u) {
+      const int c = c0 + u * BWD_NT;
+      const int k = c / per, e = c - k * per;
+      if (c < total) *reinterpret_cast<i32x4*>(dst + (size_t)k * CH + e * VE) = v[u];
+    }
+  }
+}
+
+struct BwdShared {
+  int flag, tmp;
+  float posw[68];
+  float red[BWD_NW];
+};
+
+// Streamed rows per LDS chunk in resident mode (stream mode sizes it on the host).
+__host__ __device__ inline int bwd_chunk(int N) {
+  const int Np = ((N + 31) / 32) * 32;
+  return Np < 256 ? Np : 256;
+}
+__host__ __device__ inline int bwd_local_rows(int N, int G) { return 16 * (((N + 15) / 16 + G - 1) / G); }
+
+template <typename T, int DP, bool STREAM>
+__global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
+  using M = Mfma<T, DP>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ BwdShared sh;
+  int grp, member;
+  if (!group_of(a.B * a.H, a.G, grp, member)) return;  // surplus workgroup of the XCD-aligned grid
+  const int b = grp / a.H, h = grp % a.H;
+  const int N = a.N, d = a.d;
+  const int Np = ((N + 31) / 32) * 32;
+  const int CH = a.ch;
+  const int loc = bwd_local_rows(N, a.G);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  const int g = lane >> 4;
+  if (threadIdx.x == 0) sh.flag = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  const size_t bh = (size_t)b * a.H + h;
+  const size_t wg_id = bh * a.G + member;
+  // ---- LDS carve-up (must match sinkhorn_bwd_lds_bytes)
+  unsigned char* valid = smem;
+  const int res_rows = STREAM ? loc : Np;  // rows of Q and K kept in LDS by the solve
+  const size_t region = max((size_t)2 * res_rows * DP * sizeof(T), (size_t)4 * CH * DP * sizeof(T));
+  T* R0 = reinterpret_cast<T*>(smem + ((Np + 15) / 16) * 16);
+  float* after_region = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(R0) + region);
+  float* fv = STREAM ? a.vec_ws + wg_id * (size_t)BWD_STREAM_VECS * Np : after_region;
+  float* uu = fv;            // u (log2), rows
+  float* vv = uu + Np;       // v (log2), cols
+  float* lz = vv + Np;       // log Z (log2), rows
+  float* cl = lz + Np;       // col_lse (log2), cols
+  float* Dv = cl + Np;       // D_i, rows
+  float* gv = Dv + Np;       // g_v, cols
+  float* zu = gv + Np;       // z_u, rows
+  float* zvv = zu + Np;      // z_v, cols
+  float* cy = zvv + Np;      // CG y / scratch vector (cols)
+  float* cr = cy + Np;       // CG r (cols)
+  float* cp = cr + Np;       // CG p (cols)
+  float* ct = cp + Np;       // CG t (rows)
+  float* ctw = ct + Np;      // CG W x (rows)
+  float* xs = ctw + Np;      // x coordinates [Np][3]
+  float* dxc = xs + 3 * Np;  // grad x_centroid rows [Np][3]
+  float* lres = STREAM ? after_region : dxc + 3 * Np;  // per-local-row constants [loc]
+  float* lout = lres + loc;      // per-local-row results [loc]
+  float* dxs = lout + loc;       // dx accumulator for my stripe [loc][3]
+  float* dpw = dxs + 3 * loc;    // d pos_weight histogram [68]
+  float* scratch = dpw + 68;     // BWD_SCRATCH (resident) or BWD_STREAM_SCRATCH (stream) floats
+  const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &sh.tmp);
+  const int n_tiles = (n + 15) / 16;
+  int t0, t1;
+  stripe(n_tiles, member, a.G, t0, t1);
+  const int nr = t1 - t0;
+  // Every output position is written: rows past the last valid tile (owned by no
+  // stripe) are zeroed here, row i by member i % G; invalid stripe rows get zeros
+  // where the stripe's outputs are written.
+  for (int i = n_tiles * 16 + member; i < N; i += a.G) {
+    for (int c = threadIdx.x; c < d; c += BWD_NT) {
+      a.dq[(bh * N + i) * d + c] = 0.f;
+      a.dk[(bh * N + i) * d + c] = 0.f;
+      a.dv[(bh * N + i) * d + c] = 0.f;
+    }
+    if (threadIdx.x == 0) {
+      a.dlog_mu[bh * N + i] = 0.f;
+      a.dlog_nu[bh * N + i] = 0.f;
+    }
+  }
+  if (n == 0 || nr <= 0) {
+    // owns nothing: publish empty partials so the finaliser can sum every slot
+    for (int k = threadIdx.x; k < 68; k += BWD_NT) a.dpw_part[wg_id * 68 + k] = 0.f;
+    if (threadIdx.x == 0) a.dw_part[wg_id] = 0.f;
+    return;
+  }
+  const int r_lo = t0 * 16, r_hi = min(t1 * 16, n);
+
+  const size_t qoff = (size_t)b * a.sb + (size_t)h * a.sh;
+  const T* Qg = reinterpret_cast<const T*>(a.q) + qoff;
+  const T* Kg = reinterpret_cast<const T*>(a.k) + qoff;
+  const T* Vg = reinterpret_cast<const T*>(a.v) + qoff;
+  const T* gOh = reinterpret_cast<const T*>(a.go_hi) + bh * Np * DP;  // [Np][DP]
+  const T* gOlo = reinterpret_cast<const T*>(a.go_lo) + bh * Np * DP;  // [Np][DP]
+  const T* gOt = reinterpret_cast<const T*>(a.go_t) + bh * DP * Np;    // [DP][Np]
+  const float eps = a.eps[h];
+  const float kappa = a.lam / (a.lam + eps);
+  const float sc = LOG2E / (sqrtf((float)d) * eps);
+  const float inv_eps = 1.f / eps;
+  const float kape = kappa / eps;
+  const float sgn_col = a.mode == 1 ? 1.f : -1.f;
+  const float inv_sqrt_d = 1.f / sqrtf((float)d);
+  const bool has_dxc = a.grad_xc != nullptr;
+
+  // ---- per-(b,h) vectors (log2 units; invalid -> NEG_BIG / 0)
+  for (int i = threadIdx.x; i < Np; i += BWD_NT) {
+    const bool ok = i < n && valid[i];
+    uu[i] = ok ? a.log_u[bh * N + i] * LOG2E : NEG_BIG;
+    vv[i] = ok ? a.log_v[bh * N + i] * LOG2E : NEG_BIG;
+    lz[i] = ok ? a.log_z[bh * N + i] * LOG2E : 0.f;
+    cl[i] = ok ? a.col_lse[bh * N + i] * LOG2E : 0.f;
+    for (int c = 0; c < 3; ++c) {
+      xs[3 * i + c] = (a.x && i < n) ? a.x[((size_t)b * N + i) * 3 + c] : 0.f;
+      dxc[3 * i + c] = (has_dxc && ok) ? a.grad_xc[(bh * N + i) * 3 + c] : 0.f;
+    }
+  }
+  for (int q = threadIdx.x; q < 3 * loc; q += BWD_NT) dxs[q] = 0.f;
+  for (int k = threadIdx.x; k < 68; k += BWD_NT) dpw[k] = 0.f;
+  const float w_h = a.w_dist ? a.w_dist[h] : 0.f;
+  const bool use_geo = (a.x != nullptr) && (w_h != 0.f);
+  const bool use_pos = (a.bins != nullptr) && (a.pos_w != nullptr);
+  if (use_pos)
+    for (int k = threadIdx.x; k < 68; k += BWD_NT) sh.posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
+  __syncthreads();
+  Bias bias;
+  bias.bins = use_pos ? a.bins + (size_t)b * N * N : nullptr;
+  bias.posw = sh.posw;
+  bias.xs = use_geo ? xs : nullptr;
+  bias.geo_scale = -LOG2E * w_h / eps;
+  bias.r0 = a.r0;
+  bias.N = N;
+  const bool general = use_pos || use_geo;
+  const bool geo_grad = a.geo_grad != 0 && a.x != nullptr;
+
+  // ---- D_i (prep kernel) for all rows
+  const float* Dg = a.dcoef + bh * Np;
+  for (int i = threadIdx.x; i < Np; i += BWD_NT) Dv[i] = Dg[i];
+  __syncthreads();
+
+  uint64_t* xbase = a.xch + bh * 4 * (size_t)Np;
+  const uint32_t salt = a.salt << 12;
+  uint32_t phase = 0;
+  constexpr int NC = DP / 16;
+
+  // =========================================================================
+  // C1: column pass, resident j (my tiles), streamed i in chunks.
+  //   T = exp2(sc qk + (u-logZ)_i + v_j);  gls = T (dT - D_i);  g_v_j = sum_i gls
+  //   dV_j = sum_i T gO_i;  dx_tr_j = sum_i T dxc_i
+  {
+    T* Qc = R0;
+    T* gOc = Qc + (size_t)CH * DP;
+    T* gOl = gOc + (size_t)CH * DP;  // low halves of gO (bf16 only)
+    T* gOT = gOl + (size_t)CH * DP;  // [DP][CH]
+    float* a2 = ct;                  // (u - logZ) in log2, rows (ct is free until the solve)
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) a2[i] = (i < n && valid[i]) ? uu[i] - lz[i] : NEG_BIG;
+    __syncthreads();
+    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
+      // wave w owns resident tiles rt0 + w + 4*k, k < 4 (up to 16 tiles per batch)
+      constexpr int MAXT = BWD_MAXT;
+      typename M::Frag kf[MAXT], vf[MAXT];
+      f32x4 cinit[MAXT], dvacc[MAXT][NC];
+      float gva[MAXT], dxa[MAXT][3], xj[MAXT][3];
+      int ntile = 0;
+#pragma unroll
+      for (int k = 0; k < MAXT; ++k) {
+        const int rt = rt0 + wave + BWD_NW * k;
+        gva[k] = 0.f;
+        dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) dvacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (rt < nr) {
+          ++ntile;
+          const int j = (t0 + rt) * 16 + (lane & 15);
+          load_frag_global<T, DP>(kf[k], Kg, a.sn, j, n, d, lane);
+          load_frag_global<T, DP>(vf[k], Vg, a.sn, j, n, d, lane);
+          const float ci = vv[j] / sc;
+          cinit[k] = f32x4{ci, ci, ci, ci};
+          xj[k][0] = xs[3 * j]; xj[k][1] = xs[3 * j + 1]; xj[k][2] = xs[3 * j + 2];
+        }
+      }
+      for (int c0 = 0; c0 < n; c0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP>(Qc, Qg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(gOc, gOh, DP, c0, CH, Np, DP);
+        if (M::SPLIT) stage_chunk<T, DP>(gOl, gOlo, DP, c0, CH, Np, DP);
+        stage_chunk_tt<T, DP>(gOT, gOt, Np, c0, CH);
+        __syncthreads();
+        const int npair = (min(CH, n - c0) + 31) / 32;
+        for (int pr = 0; pr < npair; ++pr) {
+          typename M::Frag qa[2], ga[2], gl[2];
+          f32x4 wa[2], Dq[2];
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int sl = pr * 32 + hf * 16;  // chunk-local streamed tile base
+            M::load(qa[hf], Qc + (size_t)(sl + (lane & 15)) * DP, lane);
+            M::load(ga[hf], gOc + (size_t)(sl + (lane & 15)) * DP, lane);
+            if (M::SPLIT) M::load(gl[hf], gOl + (size_t)(sl + (lane & 15)) * DP, lane);
+            wa[hf] = *reinterpret_cast<const f32x4*>(a2 + c0 + sl + 4 * g);
+            Dq[hf] = *reinterpret_cast<const f32x4*>(Dv + c0 + sl + 4 * g);
+          }
+#pragma unroll
+          for (int k = 0; k < MAXT; ++k) {
+            if (k < ntile) {
+              const int j = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
+              f32x4 tv[2];
+#pragma unroll
+              for (int hf = 0; hf < 2; ++hf) {
+                const f32x4 acc = M::qk(qa[hf], kf[k], cinit[k]);
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                f32x4 dt = M::qk(ga[hf], vf[k], zero);
+                if (M::SPLIT) dt = M::qk(gl[hf], vf[k], dt);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const int i = c0 + pr * 32 + hf * 16 + 4 * g + r;
+                  float x = __builtin_fmaf(acc[r], sc, wa[hf][r]);
+                  if (general && wa[hf][r] > 0.5f * NEG_BIG) x += bias(i, j);
+                  const float tval = fast_exp2(x);
+                  float dtv = dt[r];
+                  if (has_dxc) {
+                    const float* dc = dxc + 3 * i;
+                    dtv += dc[0] * xj[k][0] + dc[1] * xj[k][1] + dc[2] * xj[k][2];
+                    dxa[k][0] = __builtin_fmaf(tval, dc[0], dxa[k][0]);
+                    dxa[k][1] = __builtin_fmaf(tval, dc[1], dxa[k][1]);
+                    dxa[k][2] = __builtin_fmaf(tval, dc[2], dxa[k][2]);
+                  }
+                  gva[k] = __builtin_fmaf(tval, dtv - Dq[hf][r], gva[k]);
+                  tv[hf][r] = tval;
+                }
+              }
+#pragma unroll
+              for (int c = 0; c < NC; ++c)
+                dvacc[k][c] = M::pv(tv[0], tv[1], gOT + (size_t)(c * 16 + (lane & 15)) * CH + pr * 32, lane,
+                                    dvacc[k][c]);
+            }
+          }
+        }
+      }
+      // epilogue for this batch of resident tiles
+#pragma unroll
+      for (int k = 0; k < MAXT; ++k) {
+        if (k < ntile) {
+          const int tile = t0 + rt0 + wave + BWD_NW * k;
+          const int jl = tile * 16 + (lane & 15);
+          const float gsum = sum_groups(gva[k]);
+          const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
+          if (lane < 16 && jl < n) {
+            lout[jl - r_lo] = gsum;
+            dxs[3 * (jl - r_lo) + 0] += d0;
+            dxs[3 * (jl - r_lo) + 1] += d1;
+            dxs[3 * (jl - r_lo) + 2] += d2;
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = tile * 16 + 4 * g + r;
+            if (j < N) {
+              const bool jv = j < n && valid[j];
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                const int col = c * 16 + (lane & 15);
+                if (col < d) a.dv[(bh * N + j) * d + col] = jv ? dvacc[k][c][r] : 0.f;
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    ++phase;
+    uint64_t* xg = xbase;  // slot 0: g_v
+    for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xg + j, lout[j - r_lo], salt | phase);
+    if (!gather_vector(xg, n, Np, salt | phase, gv, valid, a.err, &sh.flag)) return;
+  }
+
+  // =========================================================================
+  // S: solve (I - kappa^2 S_row^T S_col) z_v = g_v.
+  // resident: all rows of Q and K (global tile index); stream: my stripes (local tile index)
+  T* QS = R0;
+  T* KS = R0 + (size_t)res_rows * DP;
+  const T* Qp = STREAM ? reinterpret_cast<const T*>(a.qp) + bh * Np * DP : nullptr;
+  const T* Kp = STREAM ? reinterpret_cast<const T*>(a.kp) + bh * Np * DP : nullptr;
+  __syncthreads();
+  if constexpr (STREAM) {
+    stage_rows<T, DP>(QS, Qp + (size_t)r_lo * DP, DP, nr * 16, DP, loc);
+    stage_rows<T, DP>(KS, Kp + (size_t)r_lo * DP, DP, nr * 16, DP, loc);
+  } else {
+    stage_rows<T, DP>(QS, Qg, a.sn, n, d, Np);
+    stage_rows<T, DP>(KS, Kg, a.sn, n, d, Np);
+  }
+  __syncthreads();
+  // lout[q] = sum_j exp2(sc <res_q, str_j> + lres[q] + w2_j (+bias)) z_j over all
+  // streamed j; row = true: resident plan rows (Q) against streamed K.
+  auto wsum = [&](bool row, const float* w2, const float* z) {
+    if constexpr (STREAM) {
+      if (row) {
+        if (general) stream_sweep<BWD_NT, T, DP, SW_WSUM, true, false>(QS, Kp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+        else stream_sweep<BWD_NT, T, DP, SW_WSUM, false, false>(QS, Kp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+      } else {
+        if (general) stream_sweep<BWD_NT, T, DP, SW_WSUM, true, true>(KS, Qp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+        else stream_sweep<BWD_NT, T, DP, SW_WSUM, false, true>(KS, Qp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+      }
+    } else {
+      if (row) {
+        if (general) light_sweep<T, DP, true, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
+        else light_sweep<T, DP, false, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
+      } else {
+        if (general) light_sweep<T, DP, true, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
+        else light_sweep<T, DP, false, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
+      }
+    }
+  };
+  uint64_t* xA = xbase + Np;      // slot 1
+  uint64_t* xB = xbase + 2 * Np;  // slot 2
+  if (a.solver == 0) {
+    // reference Gauss-Seidel (flash_sinkhorn_attn.py:471-542): z_u = 0, z_v = g_v
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) { zu[i] = 0.f; zvv[i] = gv[i]; }
+    float* mcl = cy;  // -col_lse (log2) on valid columns
+    float* a2 = cr;   // u - logZ (log2) on valid rows
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) {
+      const bool ok = i < n && valid[i];
+      mcl[i] = ok ? -cl[i] : NEG_BIG;
+      a2[i] = ok ? uu[i] - lz[i] : NEG_BIG;
+    }
+    __syncthreads();
+    for (int it = 0; it < a.iters; ++it) {
+      // z_u_i = kappa sum_j S_col_ij z_v_j   (resident rows: cres = u_i)
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = uu[r_lo + q];
+      __syncthreads();
+      wsum(true, mcl, zvv);
+      ++phase;
+      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, kappa * lout[i - r_lo], salt | phase);
+      if (!gather_vector(xA, n, Np, salt | phase, zu, valid, a.err, &sh.flag)) return;
+      // z_v_j = g_v_j + kappa sum_i T_ij z_u_i   (resident cols: cres = v_j)
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = vv[r_lo + q];
+      __syncthreads();
+      wsum(false, a2, zu);
+      ++phase;
+      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT)
+        xch_put(xB + j, gv[j] + kappa * lout[j - r_lo], salt | phase);
+      if (!gather_vector(xB, n, Np, salt | phase, zvv, valid, a.err, &sh.flag)) return;
+    }
+  } else {
+    // CG on (I - kappa^2 W^T W) y = D_c^{-1/2} g_v, W_ij = exp2(sc qk + alpha_i + beta_j)
+    float* al = zu;   // alpha_i = u - logZ/2 (rows); zu is rebuilt after the solve
+    float* be = zvv;  // beta_j = (v - col_lse)/2 (cols)
+    float* cs = gv;   // s = W^T t; g_v is not read again once r and p are set
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) {
+      const bool ok = i < n && valid[i];
+      al[i] = ok ? uu[i] - 0.5f * lz[i] : NEG_BIG;
+      be[i] = ok ? 0.5f * (vv[i] - cl[i]) : NEG_BIG;
+      const float bj = ok ? gv[i] * fast_exp2(-0.5f * (vv[i] + cl[i])) : 0.f;
+      cy[i] = 0.f;
+      cr[i] = bj;
+      cp[i] = bj;
+      ctw[i] = 0.f;
+    }
+    __syncthreads();
+    float rr = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red);
+    // cg_rtol > 0: stop once ||r|| <= rtol ||b|| (utils/cg.py:63-80).  cg_rtol == 0:
+    // exactly `iters` iterations; a residual that reaches zero stays zero (alpha = beta = 0).
+    // rr, pAp and rr_new are bit-identical in every member, so the exit is uniform.
+    const bool early_exit = a.cg_rtol > 0.f;
+    const float stop2 = a.cg_rtol * a.cg_rtol * rr;
+    const float k2 = kappa * kappa;
+    for (int it = 0; it < a.iters; ++it) {
+      if (early_exit && (rr <= stop2 || rr == 0.f)) break;
+      // t_i = sum_j W_ij p_j (my rows)
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = al[r_lo + q];
+      __syncthreads();
+      wsum(true, be, cp);
+      ++phase;
+      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, lout[i - r_lo], salt | phase);
+      if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) return;
+      // s_j = sum_i W_ij t_i (my cols)
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = be[r_lo + q];
+      __syncthreads();
+      wsum(false, al, ct);
+      ++phase;
+      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase);
+      if (!gather_vector(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag)) return;
+      // CG update, identical in every member (utils/cg.py:70-92 with x0 = 0)
+      const float pAp = block_sum(Np, [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red);
+      if (early_exit && pAp == 0.f) break;
+      const float alpha = (pAp != 0.f && rr != 0.f) ? rr / pAp : 0.f;
+      for (int i = threadIdx.x; i < Np; i += BWD_NT) {
+        cy[i] += alpha * cp[i];
+        cr[i] -= alpha * (cp[i] - k2 * cs[i]);
+        ctw[i] += alpha * ct[i];
+      }
+      __syncthreads();
+      const float rr_new = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red);
+      const float beta = rr != 0.f ? rr_new / rr : 0.f;
+      for (int i = threadIdx.x; i < Np; i += BWD_NT) cp[i] = cr[i] + beta * cp[i];
+      rr = rr_new;
+      __syncthreads();
+    }
+    // z_v = D_c^{1/2} y, z_u = kappa D_r^{1/2} (W y)
+    for (int i = threadIdx.x; i < Np; i += BWD_NT) {
+      const bool ok = i < n && valid[i];
+      zvv[i] = ok ? cy[i] * fast_exp2(0.5f * (vv[i] + cl[i])) : 0.f;
+      zu[i] = ok ? kappa * ctw[i] * fast_exp2(0.5f * lz[i]) : 0.f;
+    }
+    __syncthreads();
+  }
+  // marginal gradients (flash_sinkhorn_attn.py:645-646; analytic: d log_mu = kappa lambda_u = -kappa z_u)
+  for (int i = r_lo + (int)threadIdx.x; i < min(t1 * 16, N); i += BWD_NT) {
+    const bool iv = i < n && valid[i];
+    a.dlog_mu[bh * N + i] = iv ? (a.mode == 1 ? -kappa : kappa) * zu[i] : 0.f;
+    a.dlog_nu[bh * N + i] = iv ? kappa * zvv[i] : 0.f;
+  }
+
+  // per-row helper vectors for R2 / C2
+  float* a2 = cy;   // u - logZ (log2), rows
+  float* lc = cr;   // v + col_lse (log2) = log c_j, cols
+  for (int i = threadIdx.x; i < Np; i += BWD_NT) {
+    const bool ok = i < n && valid[i];
+    a2[i] = ok ? uu[i] - lz[i] : NEG_BIG;
+    lc[i] = ok ? vv[i] + cl[i] : 0.f;
+  }
+  __syncthreads();
+
+  float dw_acc = 0.f;  // thread-local part of d w_dist (R2 lanes)
+
+  // =========================================================================
+  // R2: row pass, resident i, streamed j in chunks: dQ, dx_i (cost), dw, dpw
+  {
+    T* Kc = R0;
+    T* Vc = Kc + (size_t)CH * DP;
+    T* KT = Vc + (size_t)CH * DP;  // [DP][CH]
+    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
+      constexpr int MAXT = BWD_MAXT;
+      typename M::Frag qf[MAXT], gf[MAXT], gfl[MAXT];
+      f32x4 cinit[MAXT], dqacc[MAXT][NC];
+      float lzi[MAXT], zui[MAXT], Di[MAXT], xi[MAXT][3], dci[MAXT][3], dxa[MAXT][3];
+      int ntile = 0;
+#pragma unroll
+      for (int k = 0; k < MAXT; ++k) {
+        const int rt = rt0 + wave + BWD_NW * k;
+        dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) dqacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (rt < nr) {
+          ++ntile;
+          const int i = (t0 + rt) * 16 + (lane & 15);
+          load_frag_global<T, DP>(qf[k], Qg, a.sn, i, n, d, lane);
+          load_frag_global<T, DP>(gf[k], gOh, DP, i, Np, DP, lane);
+          if (M::SPLIT) load_frag_global<T, DP>(gfl[k], gOlo, DP, i, Np, DP, lane);
+          const float ci = a2[i] / sc;
+          cinit[k] = f32x4{ci, ci, ci, ci};
+          lzi[k] = lz[i];
+          zui[k] = zu[i];
+          Di[k] = Dv[i];
+          xi[k][0] = xs[3 * i]; xi[k][1] = xs[3 * i + 1]; xi[k][2] = xs[3 * i + 2];
+          dci[k][0] = dxc[3 * i]; dci[k][1] = dxc[3 * i + 1]; dci[k][2] = dxc[3 * i + 2];
+        }
+      }
+      for (int c0 = 0; c0 < n; c0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP>(Kc, Kg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(Vc, Vg, a.sn, c0, CH, n, d);
+        stage_chunk_t<T, DP>(KT, Kg, a.sn, c0, CH, n, d);
+        __syncthreads();
+        const int npair = (min(CH, n - c0) + 31) / 32;
+        for (int pr = 0; pr < npair; ++pr) {
+          typename M::Frag ka[2], va[2];
+          f32x4 wv[2], wl[2], wz[2];
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int sl = pr * 32 + hf * 16;
+            M::load(ka[hf], Kc + (size_t)(sl + (lane & 15)) * DP, lane);
+            M::load(va[hf], Vc + (size_t)(sl + (lane & 15)) * DP, lane);
+            wv[hf] = *reinterpret_cast<const f32x4*>(vv + c0 + sl + 4 * g);
+            wl[hf] = *reinterpret_cast<const f32x4*>(lc + c0 + sl + 4 * g);
+            wz[hf] = *reinterpret_cast<const f32x4*>(zvv + c0 + sl + 4 * g);
+          }
+#pragma unroll
+          for (int k = 0; k < MAXT; ++k) {
+            if (k < ntile) {
+              const int i = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
+              f32x4 dcv[2];
+#pragma unroll
+              for (int hf = 0; hf < 2; ++hf) {
+                const f32x4 acc = M::qk(ka[hf], qf[k], cinit[k]);
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                f32x4 dt = M::qk(va[hf], gf[k], zero);
+                if (M::SPLIT) dt = M::qk(va[hf], gfl[k], dt);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const int j = c0 + pr * 32 + hf * 16 + 4 * g + r;
+                  const bool jok = wv[hf][r] > 0.5f * NEG_BIG;
+                  float x = __builtin_fmaf(acc[r], sc, wv[hf][r]);
+                  if (general && jok) x += bias(i, j);
+                  const float tval = fast_exp2(x);
+                  const float scol = jok ? fast_exp2(x + lzi[k] - wl[hf][r]) : 0.f;
+                  float dtv = dt[r];
+                  if (has_dxc) dtv += dci[k][0] * xs[3 * j] + dci[k][1] * xs[3 * j + 1] + dci[k][2] * xs[3 * j + 2];
+                  const float gls = tval * (dtv - Di[k]);
+                  float dC = -inv_eps * gls - kape * zui[k] * tval + sgn_col * kape * wz[hf][r] * scol;
+                  if (!jok) dC = 0.f;
+                  dcv[hf][r] = dC;
+                  if ((geo_grad || use_pos) && jok && i < n && valid[i]) {
+                    if (geo_grad) {
+                      // backward tiles clamp the distance at 1e-8 (flash_sinkhorn_attn.py:45, 624-634);
+                      // d w_dist is non-zero even where w_dist == 0
+                      const float dx0 = xi[k][0] - xs[3 * j], dx1 = xi[k][1] - xs[3 * j + 1], dx2 = xi[k][2] - xs[3 * j + 2];
+                      const float dist = fmaxf(sqrtf(dx0 * dx0 + dx1 * dx1 + dx2 * dx2), 1e-8f);
+                      const float rd = a.r0 + dist;
+                      const float om = dC * w_h * a.r0 / (rd * rd * dist);
+                      dxa[k][0] = __builtin_fmaf(om, dx0, dxa[k][0]);
+                      dxa[k][1] = __builtin_fmaf(om, dx1, dxa[k][1]);
+                      dxa[k][2] = __builtin_fmaf(om, dx2, dxa[k][2]);
+                      dw_acc = __builtin_fmaf(dC, dist / rd, dw_acc);
+                    }
+                    if (use_pos) {
+                      const unsigned bk = (unsigned)bias.bins[(size_t)i * N + j];
+                      if (bk < 68u) atomicAdd(&dpw[bk], dC);
+                    }
+                  }
+                }
+              }
+#pragma unroll
+              for (int c = 0; c < NC; ++c)
+                dqacc[k][c] = M::pv(dcv[0], dcv[1], KT + (size_t)(c * 16 + (lane & 15)) * CH + pr * 32, lane,
+                                    dqacc[k][c]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < MAXT; ++k) {
+        if (k < ntile) {
+          const int tile = t0 + rt0 + wave + BWD_NW * k;
+          const int il = tile * 16 + (lane & 15);
+          const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
+          if (lane < 16 && il < n) {
+            dxs[3 * (il - r_lo) + 0] += d0;
+            dxs[3 * (il - r_lo) + 1] += d1;
+            dxs[3 * (il - r_lo) + 2] += d2;
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = tile * 16 + 4 * g + r;
+            if (i < N) {
+              const bool iv = i < n && valid[i];
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                const int col = c * 16 + (lane & 15);
+                if (col < d) a.dq[(bh * N + i) * d + col] = iv ? -inv_sqrt_d * dqacc[k][c][r] : 0.f;
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // =========================================================================
+  // C2: column pass, resident j, streamed i in chunks: dK, dx_j (cost)
+  {
+    T* Qc = R0;
+    T* gOc = Qc + (size_t)CH * DP;
+    T* gOl = gOc + (size_t)CH * DP;  // low halves of gO (bf16 only)
+    T* QT = gOl + (size_t)CH * DP;   // [DP][CH]
+    float* a2s = a2;
+    float* zus = zu;
+    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
+      constexpr int MAXT = BWD_MAXT;
+      typename M::Frag kf[MAXT], vf[MAXT];
+      f32x4 cinit[MAXT], dkacc[MAXT][NC];
+      float lcj[MAXT], zvj[MAXT], xj[MAXT][3], dxa[MAXT][3];
+      int ntile = 0;
+#pragma unroll
+      for (int k = 0; k < MAXT; ++k) {
+        const int rt = rt0 + wave + BWD_NW * k;
+        dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) dkacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (rt < nr) {
+          ++ntile;
+          const int j = (t0 + rt) * 16 + (lane & 15);
+          load_frag_global<T, DP>(kf[k], Kg, a.sn, j, n, d, lane);
+          load_frag_global<T, DP>(vf[k], Vg, a.sn, j, n, d, lane);
+          const float ci = vv[j] / sc;
+          cinit[k] = f32x4{ci, ci, ci, ci};
+          lcj[k] = lc[j];
+          zvj[k] = zvv[j];
+          xj[k][0] = xs[3 * j]; xj[k][1] = xs[3 * j + 1]; xj[k][2] = xs[3 * j + 2];
+        }
+      }
+      for (int c0 = 0; c0 < n; c0 += CH) {
+        __syncthreads();
+        stage_chunk<T, DP>(Qc, Qg, a.sn, c0, CH, n, d);
+        stage_chunk<T, DP>(gOc, gOh, DP, c0, CH, Np, DP);
+        if (M::SPLIT) stage_chunk<T, DP>(gOl, gOlo, DP, c0, CH, Np, DP);
+        stage_chunk_t<T, DP>(QT, Qg, a.sn, c0, CH, n, d);
+        __syncthreads();
+        const int npair = (min(CH, n - c0) + 31) / 32;
+        for (int pr = 0; pr < npair; ++pr) {
+          typename M::Frag qa[2], ga[2], gl[2];
+          f32x4 wa[2], wlz[2], wzu[2], wD[2];
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int sl = pr * 32 + hf * 16;
+            M::load(qa[hf], Qc + (size_t)(sl + (lane & 15)) * DP, lane);
+            M::load(ga[hf], gOc + (size_t)(sl + (lane & 15)) * DP, lane);
+            if (M::SPLIT) M::load(gl[hf], gOl + (size_t)(sl + (lane & 15)) * DP, lane);
+            wa[hf] = *reinterpret_cast<const f32x4*>(a2s + c0 + sl + 4 * g);
+            wlz[hf] = *reinterpret_cast<const f32x4*>(lz + c0 + sl + 4 * g);
+            wzu[hf] = *reinterpret_cast<const f32x4*>(zus + c0 + sl + 4 * g);
+            wD[hf] = *reinterpret_cast<const f32x4*>(Dv + c0 + sl + 4 * g);
+          }
+#pragma unroll
+          for (int k = 0; k < MAXT; ++k) {
+            if (k < ntile) {
+              const int j = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
+              const bool jok = j < n && valid[j];
+              f32x4 dcv[2];
+#pragma unroll
+              for (int hf = 0; hf < 2; ++hf) {
+                const f32x4 acc = M::qk(qa[hf], kf[k], cinit[k]);
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                f32x4 dt = M::qk(ga[hf], vf[k], zero);
+                if (M::SPLIT) dt = M::qk(gl[hf], vf[k], dt);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const int i = c0 + pr * 32 + hf * 16 + 4 * g + r;
+                  const bool iok = wa[hf][r] > 0.5f * NEG_BIG;
+                  float x = __builtin_fmaf(acc[r], sc, wa[hf][r]);
+                  if (general && iok) x += bias(i, j);
+                  const float tval = fast_exp2(x);
+                  const float scol = (iok && jok) ? fast_exp2(x + wlz[hf][r] - lcj[k]) : 0.f;
+                  float dtv = dt[r];
+                  if (has_dxc) dtv += dxc[3 * i] * xj[k][0] + dxc[3 * i + 1] * xj[k][1] + dxc[3 * i + 2] * xj[k][2];
+                  const float gls = tval * (dtv - wD[hf][r]);
+                  float dC = -inv_eps * gls - kape * wzu[hf][r] * tval + sgn_col * kape * zvj[k] * scol;
+                  if (!iok || !jok) dC = 0.f;
+                  dcv[hf][r] = dC;
+                  if (geo_grad && use_geo && iok && jok) {
+                    const float dx0 = xs[3 * i] - xj[k][0], dx1 = xs[3 * i + 1] - xj[k][1], dx2 = xs[3 * i + 2] - xj[k][2];
+                    const float dist = fmaxf(sqrtf(dx0 * dx0 + dx1 * dx1 + dx2 * dx2), 1e-8f);
+                    const float rd = a.r0 + dist;
+                    const float om = dC * w_h * a.r0 / (rd * rd * dist);
+                    dxa[k][0] = __builtin_fmaf(-om, dx0, dxa[k][0]);
+                    dxa[k][1] = __builtin_fmaf(-om, dx1, dxa[k][1]);
+                    dxa[k][2] = __builtin_fmaf(-om, dx2, dxa[k][2]);
+                  }
+                }
+              }
+#pragma unroll
+              for (int c = 0; c < NC; ++c)
+                dkacc[k][c] = M::pv(dcv[0], dcv[1], QT + (size_t)(c * 16 + (lane & 15)) * CH + pr * 32, lane,
+                                    dkacc[k][c]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < MAXT; ++k) {
+        if (k < ntile) {
+          const int tile = t0 + rt0 + wave + BWD_NW * k;
+          const int jl = tile * 16 + (lane & 15);
+          const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
+          if (lane < 16 && jl < n) {
+            dxs[3 * (jl - r_lo) + 0] += d0;
+            dxs[3 * (jl - r_lo) + 1] += d1;
+            dxs[3 * (jl - r_lo) + 2] += d2;
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = tile * 16 + 4 * g + r;
+            if (j < N) {
+              const bool jv = j < n && valid[j];
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                const int col = c * 16 + (lane & 15);
+                if (col < d) a.dk[(bh * N + j) * d + col] = jv ? -inv_sqrt_d * dkacc[k][c][r] : 0.f;
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- partials: dx for my stripe, dpw / dw of this workgroup
+  for (int q = threadIdx.x; q < 3 * (r_hi - r_lo); q += BWD_NT)
+    a.dx_part[(bh * N + r_lo) * 3 + q] = dxs[q];
+  // d w_dist: per-thread partials summed in a fixed order
+  {
+    float acc = dw_acc;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
+    if (lane == 0) sh.red[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float tot = 0.f;
+      for (int w = 0; w < BWD_NW; ++w) tot += sh.red[w];
+      a.dw_part[wg_id] = tot;
+    }
+  }
+  for (int k = threadIdx.x; k < 68; k += BWD_NT) a.dpw_part[wg_id * 68 + k] = dpw[k];
+}
+
+// ---------------------------------------------------------------------------
+// LDS bytes of the main kernel for a chunk of CH streamed rows.
+inline size_t sinkhorn_bwd_lds_bytes_t(int N, int DP, int elem, int G, int CH, bool stream) {
+  const size_t Np = ((N + 31) / 32) * 32;
+  const size_t loc = bwd_local_rows(N, G);
+  const size_t res_rows = stream ? loc : Np;
+  size_t bytes = ((Np + 15) / 16) * 16;                                   // valid
+  bytes += std::max(2 * res_rows * DP * elem, (size_t)4 * CH * DP * elem);  // operand region
+  if (!stream) bytes += (size_t)BWD_STREAM_VECS * Np * 4;                 // vectors, xs, dxc
+  bytes += (2 * loc + 3 * loc + 68) * 4;                                  // lres, lout, dxs, dpw
+  bytes += (size_t)(stream ? BWD_STREAM_SCRATCH : BWD_SCRATCH) * 4;
+  return bytes;
+}
+
+template <typename T, int DP, bool STREAM>
+static hipError_t launch_bwd_t(const SinkBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
+  auto kern = sinkhorn_bwd_kernel<T, DP, STREAM>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid(grid_blocks(a.B * a.H, a.G)), block(BWD_NT);
+  SinkBwdArgs copy = a;
+  if (coop) {
+    void* args[] = {&copy};
+    return hipLaunchCooperativeKernel((const void*)kern, grid, block, args, (unsigned)lds, stream);
+  }
+  hipLaunchKernelGGL(kern, grid, block, lds, stream, copy);
+  return hipGetLastError();
+}
+
+template <bool STREAM>
+hipError_t launch_bwd_mode(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+  if (bf16_in) {
+    if (DP == 32) return launch_bwd_t<bf16, 32, STREAM>(a, lds, stream, coop);
+    if (DP == 64) return launch_bwd_t<bf16, 64, STREAM>(a, lds, stream, coop);
+  } else {
+    if (DP == 32) return launch_bwd_t<float, 32, STREAM>(a, lds, stream, coop);
+    if (DP == 64) return launch_bwd_t<float, 64, STREAM>(a, lds, stream, coop);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace dfl

@@ -7,6 +7,7 @@
 // j); in a column sweep the roles swap.  NT = threads per workgroup.
 #pragma once
 #include "common.h"
+#include "sinkhorn_args.h"
 
 namespace dfl {
 
@@ -30,6 +31,10 @@ struct Bias {
   float r0;
   int N;
   __device__ __forceinline__ float operator()(int i, int j) const {
+    // Tile rounding can hand in rows up to 15 past the last one; their results
+    // are discarded, and clamping keeps every read inside the (N, N) bins.
+    i = min(i, N - 1);
+    j = min(j, N - 1);
     float b = 0.f;
     if (bins) {
       const unsigned k = (unsigned)bins[(size_t)i * N + j];
@@ -344,6 +349,228 @@ __device__ __forceinline__ bool group_of(int n_groups, int G, int& group, int& m
 __device__ __forceinline__ void stripe(int n_tiles, int member, int G, int& t0, int& t1) {
   t0 = (int)((long long)n_tiles * member / G);
   t1 = (int)((long long)n_tiles * (member + 1) / G);
+}
+
+// ---------------------------------------------------------------------------
+// Stream mode (sequences whose Q and K do not fit in LDS).
+//
+// Only the workgroup's own stripe of resident rows sits in LDS ([nr*16][DP],
+// local tile index).  The streamed operand is read straight from a zero-padded
+// copy in global memory ([Np][DP], rows >= n and masked rows zero), which stays
+// L2-resident.  A wave takes streamed tiles st = wave + NW*k and keeps the
+// accumulators of up to STREAM_RB resident tiles in registers, so each streamed
+// tile is fetched once per batch of STREAM_RB resident tiles; the next group of
+// SCH streamed fragments is in flight while the current group is consumed.
+constexpr int STREAM_RB = 8;
+// Streamed fragments per group (double-buffered in registers).
+template <typename T, int DP> constexpr int stream_sch() { return (sizeof(T) == 4 && DP == 64) ? 2 : 4; }
+template <int NT> constexpr int stream_scratch() { return 2 * (NT / WAVE) * STREAM_RB * 16; }
+
+enum { SW_LSE_ONLINE = 0, SW_LSE_FIXED = 1, SW_WSUM = 2 };
+
+// For every local resident row q in [0, nr*16), with
+//   x_qj = sc * <res_q, str_j> + w2_j (+ bias(i_q, j)),  i_q = 16*t0 + q:
+//   SW_LSE_ONLINE: out[q] = log2 sum_j exp2(x_qj)            (running max; mx[q] = max_j x_qj if mx)
+//   SW_LSE_FIXED : out[q] = c_q + log2 sum_j exp2(x_qj - c_q) (c_q = cres[q]; caller guarantees range)
+//   SW_WSUM      : out[q] = sum_j exp2(x_qj + cres[q]) z_j    (every exponent <= 0)
+// out may alias cres.  publish(q, out_q) runs on the thread that finishes row q.
+// TRANS: the streamed index is the plan's row index (only matters for the bias).
+// Called by the whole block.
+template <int NT, typename T, int DP, int KIND, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void stream_sweep(const T* __restrict__ res, const T* __restrict__ str,
+                                             const float* __restrict__ w2, const float* __restrict__ zv,
+                                             int n_str_tiles, int t0, int nr, float sc,
+                                             const float* __restrict__ cres, const Bias& bias, float* out,
+                                             float* mx, float* scratch, unsigned* s_reset, Pub publish) {
+  using M = Mfma<T, DP>;
+  using Frag = typename M::Frag;
+  constexpr int NW = NT / WAVE;
+  constexpr int RB = STREAM_RB;
+  constexpr int SCH = stream_sch<T, DP>();
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  const int g = lane >> 4;
+  const float isc = 1.f / sc;
+  const int ks = wave < n_str_tiles ? (n_str_tiles - wave + NW - 1) / NW : 0;
+  {
+    // An opaque zero offset on every base pointer: a kernel inlines several
+    // instances of this sweep inside its iteration loop, and without it the
+    // compiler hoists each instance's address arithmetic out of that loop,
+    // where the sum no longer fits the register file.
+    int opq = 0;
+    asm volatile("" : "+s"(opq));
+    res += opq;
+    str += opq;
+    w2 += opq;
+    zv += opq;
+    cres += opq;
+  }
+  // slots past the wave's last tile repeat tile `wave` with w = NEG_BIG (exp2 -> 0), z = 0
+  auto load_group = [&](int k0, Frag* af, f32x4* w, f32x4* z) {
+#pragma unroll
+    for (int k = 0; k < SCH; ++k) {
+      const bool live = k0 + k < ks;
+      const int st = live ? wave + NW * (k0 + k) : wave;
+      M::load(af[k], str + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+      w[k] = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+      if (KIND == SW_WSUM) z[k] = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
+      if (!live) {
+        w[k] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+        z[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  for (int rb0 = 0; rb0 < nr; rb0 += RB) {
+    const int nb = min(RB, nr - rb0);
+    float m[RB], s[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      m[r] = NEG_BIG;
+      s[r] = 0.f;
+    }
+    Frag af[SCH], an[SCH];
+    f32x4 w[SCH], wn[SCH], z[SCH], zn[SCH];
+    if (ks > 0) load_group(0, af, w, z);
+    for (int k0 = 0; k0 < ks; k0 += SCH) {
+      const bool more = k0 + SCH < ks;
+      if (more) load_group(k0 + SCH, an, wn, zn);
+      // The resident fragments are loop-invariant; an opaque row offset keeps
+      // them as LDS reads inside the loop instead of RB hoisted register copies.
+      int lrow = lane & 15;
+      asm volatile("" : "+v"(lrow));
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        if (r < nb) {
+          const int q = (rb0 + r) * 16 + (lane & 15);
+          Frag bf;
+          M::load(bf, res + (size_t)((rb0 + r) * 16 + lrow) * DP, lane);
+          f32x4 cinit = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (KIND != SW_LSE_ONLINE) {
+            const float ci = (KIND == SW_LSE_FIXED ? -cres[q] : cres[q]) * isc;
+            cinit = f32x4{ci, ci, ci, ci};
+          }
+          f32x4 x[SCH];
+#pragma unroll
+          for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
+#pragma unroll
+          for (int k = 0; k < SCH; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
+              if (GENERAL) {
+                const int ires = t0 * 16 + q;
+                const int jstr = (wave + NW * (k0 + k)) * 16 + 4 * g + e;
+                if (w[k][e] > 0.5f * NEG_BIG) xv += TRANS ? bias(jstr, ires) : bias(ires, jstr);
+              }
+              x[k][e] = xv;
+            }
+          if (KIND == SW_LSE_ONLINE) {
+            float tm = NEG_BIG;
+#pragma unroll
+            for (int k = 0; k < SCH; ++k) tm = fmaxf(tm, fmaxf(fmaxf(x[k][0], x[k][1]), fmaxf(x[k][2], x[k][3])));
+            const float mn = fmaxf(m[r], tm);
+            float acc_s = s[r] * fast_exp2(m[r] - mn);
+#pragma unroll
+            for (int k = 0; k < SCH; ++k)
+              acc_s += (fast_exp2(x[k][0] - mn) + fast_exp2(x[k][1] - mn)) +
+                       (fast_exp2(x[k][2] - mn) + fast_exp2(x[k][3] - mn));
+            s[r] = acc_s;
+            m[r] = mn;
+          } else if (KIND == SW_LSE_FIXED) {
+            float acc_s = 0.f;
+#pragma unroll
+            for (int k = 0; k < SCH; ++k)
+              acc_s += (fast_exp2(x[k][0]) + fast_exp2(x[k][1])) + (fast_exp2(x[k][2]) + fast_exp2(x[k][3]));
+            s[r] += acc_s;
+          } else {
+            float acc_s = 0.f;
+#pragma unroll
+            for (int k = 0; k < SCH; ++k)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc_s = __builtin_fmaf(fast_exp2(x[k][e]), z[k][e], acc_s);
+            s[r] += acc_s;
+          }
+        }
+      }
+      if (more) {
+#pragma unroll
+        for (int k = 0; k < SCH; ++k) {
+          af[k] = an[k];
+          w[k] = wn[k];
+          z[k] = zn[k];
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      if (r < nb) {
+        float mm = 0.f, ss;
+        if (KIND == SW_LSE_ONLINE) {
+          mm = max_groups(m[r]);
+          ss = sum_groups(s[r] * fast_exp2(m[r] - mm));
+        } else {
+          ss = sum_groups(s[r]);
+        }
+        if (lane < 16) {
+          scratch[(wave * RB + r) * 16 + lane] = mm;
+          scratch[NW * RB * 16 + (wave * RB + r) * 16 + lane] = ss;
+        }
+      }
+    }
+    __syncthreads();
+    if (s_reset && threadIdx.x == 0) *s_reset = 0u;
+    for (int q = threadIdx.x; q < nb * 16; q += NT) {
+      const int r = q >> 4, l = q & 15;
+      float res_q;
+      if (KIND == SW_LSE_ONLINE) {
+        float mm = NEG_BIG;
+#pragma unroll
+        for (int w_ = 0; w_ < NW; ++w_) mm = fmaxf(mm, scratch[(w_ * RB + r) * 16 + l]);
+        float ss = 0.f;
+#pragma unroll
+        for (int w_ = 0; w_ < NW; ++w_)
+          ss += scratch[NW * RB * 16 + (w_ * RB + r) * 16 + l] * fast_exp2(scratch[(w_ * RB + r) * 16 + l] - mm);
+        res_q = mm + fast_log2(ss);
+        if (mx) mx[rb0 * 16 + q] = mm;
+      } else {
+        float ss = 0.f;
+#pragma unroll
+        for (int w_ = 0; w_ < NW; ++w_) ss += scratch[NW * RB * 16 + (w_ * RB + r) * 16 + l];
+        res_q = KIND == SW_LSE_FIXED ? cres[rb0 * 16 + q] + fast_log2(ss) : ss;
+      }
+      out[rb0 * 16 + q] = res_q;
+      publish(rb0 * 16 + q, res_q);
+    }
+    __syncthreads();
+  }
+}
+
+
+// One thread per (b, h, i, c), i < Np, c < DP: copies of Q, K (row-major) and V
+// (transposed) with zeros on masked rows, rows >= N and columns >= d.
+template <typename T, int DP>
+__global__ void __launch_bounds__(256) sinkhorn_pad_kernel(PadArgs p) {
+  const int N = p.N, d = p.d;
+  const int Np = ((N + 31) / 32) * 32;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t row = e / DP;
+  const int c = (int)(e % DP);
+  const int bh = (int)(row / Np), i = (int)(row % Np);
+  if (bh >= p.B * p.H) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const bool ok = i < N && (p.mask ? p.mask[(size_t)b * N + i] > 0.5f : true);
+  const size_t off = (size_t)b * p.sb + (size_t)h * p.sh + (size_t)i * p.sn + c;
+  T qv = from_f32<T>(0.f), kv = from_f32<T>(0.f), vv = from_f32<T>(0.f);
+  if (ok && c < d) {
+    qv = reinterpret_cast<const T*>(p.q)[off];
+    kv = reinterpret_cast<const T*>(p.k)[off];
+    vv = reinterpret_cast<const T*>(p.v)[off];
+  }
+  reinterpret_cast<T*>(p.qp)[row * DP + c] = qv;
+  reinterpret_cast<T*>(p.kp)[row * DP + c] = kv;
+  if (p.vt) reinterpret_cast<T*>(p.vt)[((size_t)bh * DP + c) * Np + i] = vv;
+  if (p.xs_p && h == 0 && c < 3)
+    p.xs_p[((size_t)b * Np + i) * 3 + c] = (p.x && i < N) ? p.x[((size_t)b * N + i) * 3 + c] : 0.f;
 }
 
 }  // namespace dfl

@@ -1,0 +1,514 @@
+// Flash-Sinkhorn forward: persistent per-(b,h) workgroup groups on gfx950.
+//
+// Restates the UOT log-domain Sinkhorn of vv137/deepfold-linear
+// (src/deepfold/model/kernels/flash_sinkhorn_attn.py:144-218, same math as
+// sinkhorn_kernel.py:1106-1492) without materialising the N x N plan:
+//
+//   u_i = kappa (log mu_i - LSE_j(L_ij + v_j))      (row update, valid j)
+//   v_j = kappa (log nu_j - LSE_i(L_ij + u_i))      (column update, valid i)
+//   L_ij = -C_ij / eps_h,  C_ij = -(q_i.k_j)/sqrt(d) + pw_h[bins_ij] + w_h d_ij/(r0 + d_ij)
+//
+// Work split: each (b,h) is served by a group of G workgroups.  Member m owns a
+// contiguous stripe of 16-row tiles, used as plan rows in the row update and as
+// plan columns in the column update.  The cost tile is recomputed on MFMA every
+// sweep.  After each half-iteration the stripe's new potentials are published
+// as tagged 64-bit words and every member gathers the full vector (common.h).
+//
+// Two storage modes (template flag STREAM):
+//   resident: Q and K of the whole (b,h) stay in LDS for all iterations;
+//   stream  : only the member's own Q and K stripes sit in LDS; the streamed
+//             operand is read from zero-padded copies in global memory
+//             (sinkhorn_pad_kernel), which stay L2-resident.  Used when the
+//             resident layout does not fit in 160 KB of LDS (long sequences).
+//
+// All logits are handled in log2 units (x * log2 e) so that exp2 maps onto
+// v_exp_f32 directly.
+#pragma once
+#include "sinkhorn_args.h"
+#include "sinkhorn_engine.h"
+
+namespace dfl {
+
+constexpr int FWD_NT = 512;  // 8 waves: two per SIMD for latency hiding
+constexpr int FWD_NW = FWD_NT / WAVE;
+// Largest |change| of a potential between two sweeps (log2 units) for which the
+// previous LSE is used as the exponent shift: every term is then <= 2^delta and
+// the sum >= 2^-delta, far inside fp32 range.
+constexpr float FIXED_SHIFT_MAX_DELTA = 64.f;
+// Stream mode: streamed rows per LDS chunk of the transport-output pass.
+constexpr int FWD_OCH = 128;
+
+__host__ __device__ inline int fwd_local_rows(int N, int G) { return 16 * (((N + 15) / 16 + G - 1) / G); }
+// Stream mode: rows of the K region (the K stripe; the output pass reuses it for
+// one K chunk and one transposed V chunk).
+__host__ __device__ inline int fwd_kregion_rows(int N, int G) {
+  const int l = fwd_local_rows(N, G);
+  return l > 2 * FWD_OCH ? l : 2 * FWD_OCH;
+}
+
+template <typename T, int DP, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void fwd_sweep(bool online, const T* res, const T* str, const float* w2, int n_tiles,
+                                          int t0, int nr, float sc, const Bias& bias, float* lse, float* mx,
+                                          float* scratch, unsigned* s_reset, Pub pub) {
+  if (online)
+    lse_sweep<FWD_NT, T, DP, GENERAL, TRANS, true>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, lse, mx, scratch,
+                                                   s_reset, pub);
+  else
+    lse_sweep<FWD_NT, T, DP, GENERAL, TRANS, false>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, lse, mx, scratch,
+                                                    s_reset, pub);
+}
+
+// Stream mode: res is the member's stripe (local tiles), str the padded global copy.
+template <typename T, int DP, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void fwd_sweep_stream(bool online, const T* res, const T* str, const float* w2,
+                                                 int n_tiles, int t0, int nr, float sc, const Bias& bias, float* lse,
+                                                 float* mx, float* scratch, unsigned* s_reset, Pub pub) {
+  if (online)
+    stream_sweep<FWD_NT, T, DP, SW_LSE_ONLINE, GENERAL, TRANS>(res, str, w2, nullptr, n_tiles, t0, nr, sc, lse, bias,
+                                                               lse, mx, scratch, s_reset, pub);
+  else
+    stream_sweep<FWD_NT, T, DP, SW_LSE_FIXED, GENERAL, TRANS>(res, str, w2, nullptr, n_tiles, t0, nr, sc, lse, bias,
+                                                              lse, mx, scratch, s_reset, pub);
+}
+
+// Outputs of one resident 16-row tile after the transport pass.  oacc holds
+// sum_j p_ij V_j in the accumulator layout (lane: row 4g + r, column c*16 + l%16);
+// xc0..2 the lane's partial sums of p_ij x_j for row tile*16 + l%16.  l2 is this
+// lane's row LSE (log2) and lse2_t / mx2_t point at the tile's 16 row entries.
+template <typename T, int DP>
+__device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int h, int tile, int n,
+                                               const unsigned char* valid, const float* lse2_t, const float* mx2_t,
+                                               const float* vecU, const float* vecV, const f32x4* oacc, float xc0,
+                                               float xc1, float xc2, const T* Gg, int lane) {
+  constexpr int NC = DP / 16;
+  const int N = a.N, d = a.d;
+  const int g = lane >> 4;
+  const size_t bh = (size_t)b * a.H + h;
+  const int irow = tile * 16 + (lane & 15);
+  const float l2 = lse2_t[lane & 15];
+  xc0 = sum_groups(xc0);
+  xc1 = sum_groups(xc1);
+  xc2 = sum_groups(xc2);
+  // T_norm = p / (1 + 1e-6 * 2^(max - lse))  <=>  reference T / (sum T + 1e-6), T = e^(s - max)
+  if (lane < 16 && irow < n && valid[irow]) {
+    const float den = 1.f + 1e-6f * fast_exp2(mx2_t[lane] - l2);
+    const size_t o = (bh * N + irow) * 3;
+    a.x_centroid[o + 0] = xc0 / den;
+    a.x_centroid[o + 1] = xc1 / den;
+    a.x_centroid[o + 2] = xc2 / den;
+    const float u = vecU[irow] * LN2;
+    a.log_u[bh * N + irow] = u;
+    a.log_z[bh * N + irow] = u + l2 * LN2;
+    a.log_v[bh * N + irow] = vecV[irow] * LN2;
+  } else if (lane < 16 && irow < N) {  // invalid row of my stripe
+    const size_t o = (bh * N + irow) * 3;
+    a.x_centroid[o + 0] = a.x_centroid[o + 1] = a.x_centroid[o + 2] = 0.f;
+    a.log_u[bh * N + irow] = a.log_z[bh * N + irow] = a.log_v[bh * N + irow] = 0.f;
+    a.col_lse[bh * N + irow] = 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = tile * 16 + 4 * g + r;
+    if (row < N && !(row < n && valid[row])) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = c * 16 + (lane & 15);
+        if (col < d) {
+          a.o_avg[(bh * N + row) * d + col] = 0.f;
+          a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = 0.f;
+        }
+      }
+    }
+    if (row < n && valid[row]) {
+      const float den = 1.f + 1e-6f * fast_exp2(mx2_t[4 * g + r] - lse2_t[4 * g + r]);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int col = c * 16 + (lane & 15);
+        if (col < d) {
+          const float o = oacc[c][r] / den;
+          a.o_avg[(bh * N + row) * d + col] = o;
+          const float sg = Gg ? 1.f / (1.f + __expf(-to_f32(Gg[(size_t)row * a.sn + col]))) : 1.f;
+          a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = sg * o;
+        }
+      }
+    }
+  }
+}
+
+template <typename T, int DP, bool STREAM>
+__global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_flag, s_tmp;
+  __shared__ unsigned s_du, s_dv;
+  __shared__ float s_posw[68];
+  int grp, member;
+  if (!group_of(a.B * a.H, a.G, grp, member)) return;  // surplus workgroup of the XCD-aligned grid
+  const int b = grp / a.H, h = grp % a.H;
+  const int N = a.N, d = a.d;
+  const int Np = ((N + 31) / 32) * 32;
+  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; }
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- LDS carve-up (must match sinkhorn_fwd_lds_bytes)
+  const int loc = fwd_local_rows(N, a.G);
+  const int q_rows = STREAM ? loc : Np;
+  const int k_rows = STREAM ? fwd_kregion_rows(N, a.G) : Np;
+  unsigned char* valid = smem;
+  T* QS = reinterpret_cast<T*>(smem + ((Np + 15) / 16) * 16);     // resident: all rows; stream: my stripe
+  T* KS = QS + (size_t)q_rows * DP;
+  float* vecU = reinterpret_cast<float*>(KS + (size_t)k_rows * DP);  // u of all rows (log2)
+  float* vecV = vecU + Np;                                          // v of all columns (log2)
+  float* xs = vecV + Np;                                            // resident only: [Np][3]
+  float* lse_r = xs + (STREAM ? 0 : 3 * Np);  // row LSE of my rows (log2); shift of the next row sweep
+  float* lse_c = lse_r + loc;   // column LSE of my columns (log2)
+  float* mx2 = lse_c + loc;     // row maxima of the final sweep
+  float* lmu_l = mx2 + loc;     // log mu of my rows
+  float* lnu_l = lmu_l + loc;   // log nu of my columns
+  float* scratch = lnu_l + loc;
+
+  const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &s_tmp);
+  const int n_tiles = (n + 15) / 16;
+  int t0, t1;
+  stripe(n_tiles, member, a.G, t0, t1);
+  const int nr = t1 - t0;
+  {
+    // Every output position is written: rows past the last valid tile, which no
+    // stripe owns, are zeroed here (row i by member i % G); invalid rows inside
+    // stripes are zeroed where the stripe's outputs are written.
+    const size_t bh0 = (size_t)b * a.H + h;
+    for (int i = n_tiles * 16 + member; i < N; i += a.G) {
+      for (int c = threadIdx.x; c < d; c += FWD_NT) {
+        a.o_avg[(bh0 * N + i) * d + c] = 0.f;
+        a.o_flat[((size_t)b * N + i) * (size_t)(a.H * d) + (size_t)h * d + c] = 0.f;
+      }
+      if (threadIdx.x < 3) a.x_centroid[(bh0 * N + i) * 3 + threadIdx.x] = 0.f;
+      if (threadIdx.x == 0) {
+        a.log_u[bh0 * N + i] = 0.f;
+        a.log_v[bh0 * N + i] = 0.f;
+        a.log_z[bh0 * N + i] = 0.f;
+        a.col_lse[bh0 * N + i] = 0.f;
+      }
+    }
+  }
+  if (n == 0 || nr <= 0) return;  // owns nothing; no other member waits on it
+
+  const size_t bh = (size_t)b * a.H + h;
+  const size_t qoff = (size_t)b * a.sb + (size_t)h * a.sh;
+  const T* Qg = reinterpret_cast<const T*>(a.q) + qoff;
+  const T* Kg = reinterpret_cast<const T*>(a.k) + qoff;
+  const T* Vg = reinterpret_cast<const T*>(a.v) + qoff;
+  const T* Gg = a.g ? reinterpret_cast<const T*>(a.g) + qoff : nullptr;
+  // stream mode: padded copies of this (b,h)
+  const T* Qp = STREAM ? reinterpret_cast<const T*>(a.qp) + bh * Np * DP : nullptr;
+  const T* Kp = STREAM ? reinterpret_cast<const T*>(a.kp) + bh * Np * DP : nullptr;
+  const int r_lo = t0 * 16;
+  if constexpr (STREAM) {
+    stage_rows<T, DP>(QS, Qp + (size_t)r_lo * DP, DP, nr * 16, DP, loc);
+    stage_rows<T, DP>(KS, Kp + (size_t)r_lo * DP, DP, nr * 16, DP, loc);
+  } else {
+    stage_rows<T, DP>(QS, Qg, a.sn, n, d, Np);
+    stage_rows<T, DP>(KS, Kg, a.sn, n, d, Np);
+  }
+
+  const float eps = a.eps[h];
+  const float kappa = a.lam / (a.lam + eps);
+  const float sc = LOG2E / (sqrtf((float)d) * eps);
+  for (int q = threadIdx.x; q < nr * 16; q += FWD_NT) {
+    const int i = r_lo + q;
+    lmu_l[q] = i < n ? a.log_mu[bh * N + i] : 0.f;
+    lnu_l[q] = i < n ? a.log_nu[bh * N + i] : 0.f;
+  }
+  for (int i = threadIdx.x; i < Np; i += FWD_NT) {
+    const bool ok = i < n && valid[i];
+    vecU[i] = ok ? (a.u_init ? a.u_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
+    vecV[i] = ok ? (a.v_init ? a.v_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
+  }
+  const float w_h = a.w_dist ? a.w_dist[h] : 0.f;
+  const bool use_geo = (a.x != nullptr) && (w_h != 0.f);
+  const bool use_pos = (a.bins != nullptr) && (a.pos_w != nullptr);
+  if (use_pos)
+    for (int k = threadIdx.x; k < 68; k += FWD_NT) s_posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
+  // coordinates of this batch row: LDS (resident) or the padded global copy (stream)
+  const float* xsrc = xs;
+  if constexpr (STREAM) {
+    xsrc = a.xs_p + (size_t)b * Np * 3;
+  } else {
+    for (int e = threadIdx.x; e < 3 * Np; e += FWD_NT) xs[e] = (a.x && e < 3 * n) ? a.x[(size_t)b * N * 3 + e] : 0.f;
+  }
+  __syncthreads();
+  Bias bias;
+  bias.bins = use_pos ? a.bins + (size_t)b * N * N : nullptr;
+  bias.posw = s_posw;
+  bias.xs = use_geo ? xsrc : nullptr;
+  bias.geo_scale = -LOG2E * w_h / eps;
+  bias.r0 = a.r0;
+  bias.N = N;
+  const bool general = use_pos || use_geo;
+
+  // sweep dispatch: ROW = plan rows resident (Q), streamed K against v; else the transpose
+  auto sweep = [&](bool row, bool online, float* lse, float* mx, unsigned* s_reset, auto pub) {
+    if constexpr (STREAM) {
+      const T* res = row ? QS : KS;
+      const T* str = row ? Kp : Qp;
+      const float* w2 = row ? vecV : vecU;
+      if (row) {
+        if (general) fwd_sweep_stream<T, DP, true, false>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+        else fwd_sweep_stream<T, DP, false, false>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+      } else {
+        if (general) fwd_sweep_stream<T, DP, true, true>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+        else fwd_sweep_stream<T, DP, false, true>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+      }
+    } else {
+      const T* res = row ? QS : KS;
+      const T* str = row ? KS : QS;
+      const float* w2 = row ? vecV : vecU;
+      if (row) {
+        if (general) fwd_sweep<T, DP, true, false>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+        else fwd_sweep<T, DP, false, false>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+      } else {
+        if (general) fwd_sweep<T, DP, true, true>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+        else fwd_sweep<T, DP, false, true>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+      }
+    }
+  };
+
+  uint64_t* xu = a.xch + bh * 2 * (size_t)Np;  // u words
+  uint64_t* xv = xu + Np;                       // v words
+  const uint32_t salt = a.salt << 12;
+  uint32_t phase = 0;
+
+  for (int it = 0; it < a.K_iter; ++it) {
+    // ---- row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j)) for my rows
+    ++phase;
+    {
+      const uint32_t tag = salt | phase;
+      const bool online = it == 0 || __uint_as_float(s_dv) > FIXED_SHIFT_MAX_DELTA;
+      auto pub = [&](int q, float l2) {
+        const int i = r_lo + q;
+        if (i < n) xch_put(xu + i, kappa * (lmu_l[q] - l2 * LN2), tag);
+      };
+      sweep(true, online, lse_r, nullptr, &s_du, pub);
+      if (!gather_potential<FWD_NT>(xu, n, tag, vecU, valid, a.err, &s_flag, &s_du)) return;
+    }
+    // ---- column update: v_j = kappa (log nu_j - LSE_i(L_ij + u_i)) for my columns
+    ++phase;
+    {
+      const uint32_t tag = salt | phase;
+      const bool online = it == 0 || __uint_as_float(s_du) > FIXED_SHIFT_MAX_DELTA;
+      const bool last = it == a.K_iter - 1;
+      auto pub = [&](int q, float l2) {
+        const int j = r_lo + q;
+        if (j < n) {
+          xch_put(xv + j, kappa * (lnu_l[q] - l2 * LN2), tag);
+          if (last && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
+        }
+      };
+      sweep(false, online, lse_c, nullptr, &s_dv, pub);
+      if (!gather_potential<FWD_NT>(xv, n, tag, vecV, valid, a.err, &s_flag, &s_dv)) return;
+    }
+  }
+  if (a.K_iter == 0) {
+    auto pub = [&](int q, float l2) {
+      const int j = r_lo + q;
+      if (j < n && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
+    };
+    sweep(false, true, lse_c, nullptr, nullptr, pub);
+  }
+
+  // ---- final row LSE with the last v: exact log Z and the row maximum
+  sweep(true, true, lse_r, mx2, nullptr, NoPublish());
+  const float* lse2 = lse_r;
+
+  // ---- transport output for my rows: O_avg = T_norm V, x_c = T_norm x.
+  using M = Mfma<T, DP>;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  const int g = lane >> 4;
+  constexpr int NC = DP / 16;
+  if constexpr (!STREAM) {
+    // V^T replaces Q in LDS; resident Q fragments are read from global memory.
+    T* VT = QS;  // [DP][Np]
+    __syncthreads();
+    stage_rows_t<T, DP>(VT, Vg, a.sn, n, d, Np);
+    __syncthreads();
+    const int n_pairs = (n_tiles + 1) / 2;
+    for (int rt = wave; rt < nr; rt += FWD_NW) {
+      const int tile = t0 + rt;
+      const int qloc = rt * 16;
+      const int irow = tile * 16 + (lane & 15);  // this lane's row in the P layout
+      typename M::Frag qf;
+      load_frag_global<T, DP>(qf, Qg, a.sn, irow, n, d, lane);
+      const float l2 = lse2[qloc + (lane & 15)];
+      f32x4 oacc[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float xc0 = 0.f, xc1 = 0.f, xc2 = 0.f;
+      for (int sp = 0; sp < n_pairs; ++sp) {
+        f32x4 p[2];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int st = 2 * sp + half;
+          p[half] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (st < n_tiles) {
+            typename M::Frag af;
+            M::load(af, KS + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+            const f32x4 w = *reinterpret_cast<const f32x4*>(vecV + st * 16 + 4 * g);
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 acc = M::qk(af, qf, zero);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+              const int j = st * 16 + 4 * g + kk;
+              float x = __builtin_fmaf(acc[kk], sc, w[kk]);
+              if (general && w[kk] > 0.5f * NEG_BIG) x += bias(irow, j);
+              const float pv = fast_exp2(x - l2);
+              p[half][kk] = pv;
+              xc0 = __builtin_fmaf(pv, xs[3 * j], xc0);
+              xc1 = __builtin_fmaf(pv, xs[3 * j + 1], xc1);
+              xc2 = __builtin_fmaf(pv, xs[3 * j + 2], xc2);
+            }
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          oacc[c] = M::pv_split(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
+      }
+      fwd_write_tile<T, DP>(a, b, h, tile, n, valid, lse2 + qloc, mx2 + qloc, vecU, vecV, oacc, xc0, xc1, xc2, Gg,
+                            lane);
+    }
+  } else {
+    // Stream mode: K and V^T pass through LDS in chunks of FWD_OCH streamed rows
+    // (the K stripe region is free now); resident Q fragments come from the Q stripe.
+    T* KC = KS;                             // [FWD_OCH][DP]
+    T* VC = KS + (size_t)FWD_OCH * DP;      // [DP][FWD_OCH]
+    const T* Vt = reinterpret_cast<const T*>(a.vt) + bh * (size_t)DP * Np;
+    constexpr int OB = 2;  // resident tiles per wave per batch
+    constexpr int VE = 16 / sizeof(T);
+    typedef __attribute__((__vector_size__(16))) int i32x4;
+    for (int rb0 = 0; rb0 < nr; rb0 += OB * FWD_NW) {
+      typename M::Frag qf[OB];
+      f32x4 oacc[OB][NC];
+      float xc[OB][3], l2v[OB];
+#pragma unroll
+      for (int k = 0; k < OB; ++k) {
+        const int rt = rb0 + wave + FWD_NW * k;
+        xc[k][0] = xc[k][1] = xc[k][2] = 0.f;
+        l2v[k] = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) oacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (rt < nr) {
+          M::load(qf[k], QS + (size_t)(rt * 16 + (lane & 15)) * DP, lane);
+          l2v[k] = lse2[rt * 16 + (lane & 15)];
+        }
+      }
+      for (int c0 = 0; c0 < n_tiles * 16; c0 += FWD_OCH) {
+        __syncthreads();
+        stage_rows<T, DP>(KC, Kp + (size_t)c0 * DP, DP, min(FWD_OCH, Np - c0), DP, FWD_OCH);
+        for (int e = threadIdx.x; e < DP * (FWD_OCH / VE); e += FWD_NT) {
+          const int c = e / (FWD_OCH / VE), jv = e - c * (FWD_OCH / VE);
+          i32x4 v = {0, 0, 0, 0};
+          if (c0 + jv * VE < Np) v = *reinterpret_cast<const i32x4*>(Vt + (size_t)c * Np + c0 + jv * VE);
+          *reinterpret_cast<i32x4*>(VC + (size_t)c * FWD_OCH + jv * VE) = v;
+        }
+        __syncthreads();
+        const int npair = (min(FWD_OCH, n_tiles * 16 - c0) + 31) / 32;
+        for (int sp = 0; sp < npair; ++sp) {
+          typename M::Frag af[2];
+          f32x4 w[2];
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int st = c0 / 16 + 2 * sp + half;
+            const int ls = st < n_tiles ? 2 * sp + half : 2 * sp;  // a dead half repeats a live tile
+            M::load(af[half], KC + (size_t)(ls * 16 + (lane & 15)) * DP, lane);
+            w[half] = *reinterpret_cast<const f32x4*>(vecV + (c0 / 16 + ls) * 16 + 4 * g);
+            if (st >= n_tiles) w[half] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+          }
+#pragma unroll
+          for (int k = 0; k < OB; ++k) {
+            const int rt = rb0 + wave + FWD_NW * k;
+            if (rt < nr) {
+              const int irow = (t0 + rt) * 16 + (lane & 15);
+              f32x4 p[2];
+#pragma unroll
+              for (int half = 0; half < 2; ++half) {
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                const f32x4 acc = M::qk(af[half], qf[k], zero);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                  const int j = c0 + (2 * sp + half) * 16 + 4 * g + kk;
+                  float x = __builtin_fmaf(acc[kk], sc, w[half][kk]);
+                  if (general && w[half][kk] > 0.5f * NEG_BIG) x += bias(irow, j);
+                  const float pv = fast_exp2(x - l2v[k]);
+                  p[half][kk] = pv;
+                  const int jj = min(j, Np - 1);  // pv = 0 past the last tile
+                  xc[k][0] = __builtin_fmaf(pv, xsrc[3 * jj], xc[k][0]);
+                  xc[k][1] = __builtin_fmaf(pv, xsrc[3 * jj + 1], xc[k][1]);
+                  xc[k][2] = __builtin_fmaf(pv, xsrc[3 * jj + 2], xc[k][2]);
+                }
+              }
+#pragma unroll
+              for (int c = 0; c < NC; ++c)
+                oacc[k][c] = M::pv_split(p[0], p[1], VC + (size_t)(c * 16 + (lane & 15)) * FWD_OCH + sp * 32, lane,
+                                         oacc[k][c]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < OB; ++k) {
+        const int rt = rb0 + wave + FWD_NW * k;
+        if (rt < nr)
+          fwd_write_tile<T, DP>(a, b, h, t0 + rt, n, valid, lse2 + rt * 16, mx2 + rt * 16, vecU, vecV, oacc[k],
+                                xc[k][0], xc[k][1], xc[k][2], Gg, lane);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stream) {
+  const size_t Np = ((N + 31) / 32) * 32;
+  const size_t loc = fwd_local_rows(N, G);
+  size_t bytes = ((Np + 15) / 16) * 16;  // valid
+  if (stream) {
+    bytes += (loc + fwd_kregion_rows(N, G)) * DP * elem;  // Q stripe, K stripe / output chunks
+    bytes += 2 * Np * 4;                                   // vecU, vecV
+    bytes += 5 * loc * 4;                                  // lse_r, lse_c, mx2, lmu_l, lnu_l
+    bytes += (size_t)stream_scratch<FWD_NT>() * 4;
+  } else {
+    bytes += 2 * Np * DP * elem;          // QS, KS
+    bytes += (2 * Np + 3 * Np) * 4;       // vecU, vecV, xs
+    bytes += 5 * loc * 4;                 // lse_r, lse_c, mx2, lmu_l, lnu_l
+    bytes += (size_t)sweep_scratch<FWD_NT>() * 4;
+  }
+  return bytes;
+}
+
+template <typename T, int DP, bool STREAM>
+static hipError_t launch_fwd_t(const SinkFwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
+  auto kern = sinkhorn_fwd_kernel<T, DP, STREAM>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid(grid_blocks(a.B * a.H, a.G)), block(FWD_NT);
+  SinkFwdArgs copy = a;
+  if (coop) {
+    void* args[] = {&copy};
+    return hipLaunchCooperativeKernel((const void*)kern, grid, block, args, (unsigned)lds, stream);
+  }
+  hipLaunchKernelGGL(kern, grid, block, lds, stream, copy);
+  return hipGetLastError();
+}
+
+template <bool STREAM>
+hipError_t launch_fwd_mode(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+  if (bf16_in) {
+    if (DP == 32) return launch_fwd_t<bf16, 32, STREAM>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<bf16, 64, STREAM>(a, lds, stream, coop);
+  } else {
+    if (DP == 32) return launch_fwd_t<float, 32, STREAM>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<float, 64, STREAM>(a, lds, stream, coop);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace dfl

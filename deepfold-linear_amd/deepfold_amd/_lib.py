@@ -22,6 +22,9 @@ DFL_IFT_FIXED_POINT = 0
 DFL_IFT_CG = 1
 DFL_IFT_REFERENCE = 0
 DFL_IFT_ANALYTIC = 1
+DFL_STORAGE_AUTO = 0
+DFL_STORAGE_RESIDENT = 1
+DFL_STORAGE_STREAM = 2
 
 _lock = threading.Lock()
 _lib = None
@@ -46,6 +49,7 @@ class SinkhornFwdParams(ctypes.Structure):
         ("K_iter", I32), ("lam", F32), ("r_0", F32),
         ("o_flat", P), ("x_centroid", P), ("log_u", P), ("log_v", P),
         ("o_avg", P), ("log_z", P), ("col_lse", P),
+        ("storage", I32),
     ]
 
 
@@ -65,6 +69,7 @@ class SinkhornBwdParams(ctypes.Structure):
         ("solver", I32), ("iters", I32), ("mode", I32), ("cg_rtol", F32),
         ("dq", P), ("dk", P), ("dv", P), ("dg", P),
         ("dlog_mu", P), ("dlog_nu", P), ("dx_res", P), ("dpos_weight", P), ("dw_dist", P),
+        ("storage", I32),
     ]
 
 

@@ -16,6 +16,10 @@ Keyword-only extensions (defaults reproduce the reference):
 * ``ift_mode``: ``"reference"`` (the reference's signs) or ``"analytic"`` (the true
   implicit adjoint; differs in the sign of the z_v*S_col term of dC and of d log_mu).
 * ``cg_rtol``: CG stops early once ||r|| <= cg_rtol ||b|| (0: run all steps).
+* ``storage``: ``"auto"`` (default), ``"resident"`` or ``"stream"``: where the
+  kernels keep Q, K and the length-N vectors.  Resident keeps a whole (b,h) in
+  LDS; stream keeps one stripe per workgroup and streams the rest through L2
+  (long sequences such as N = 4096, d = 64).  Auto picks resident when it fits.
 
 Padding: tokens with mask == 0 are excluded from the transport plan in both
 passes; outputs at padded positions are zero (the reference's x_centroid rows
@@ -32,6 +36,7 @@ from . import _lib
 
 _SOLVERS = {"fixed_point": _lib.DFL_IFT_FIXED_POINT, "cg": _lib.DFL_IFT_CG}
 _MODES = {"reference": _lib.DFL_IFT_REFERENCE, "analytic": _lib.DFL_IFT_ANALYTIC}
+_STORAGE = {"auto": _lib.DFL_STORAGE_AUTO, "resident": _lib.DFL_STORAGE_RESIDENT, "stream": _lib.DFL_STORAGE_STREAM}
 
 
 def _qkvg(Q, K, V, G):
@@ -59,7 +64,7 @@ class FlashSinkhornAttn(torch.autograd.Function):
     ``apply`` takes the reference's 17 positional arguments (Q_ln, K_ln, V, G,
     x_res, pos_weight, pos_bins, eps, w_dist, log_mu, log_nu, K_iter, lam, r_0,
     log_u_init, log_v_init, mask), always batched, optionally followed by
-    ift_solver, ift_iters, ift_mode, cg_rtol.
+    ift_solver, ift_iters, ift_mode, cg_rtol, storage.
     Returns o_flat (B,N,H*d), x_centroid (B,H,N,3), log_u, log_v (B,H,N), all fp32.
     """
 
@@ -78,6 +83,9 @@ class FlashSinkhornAttn(torch.autograd.Function):
         lmu, lnu = _f32(log_mu), _f32(log_nu)
         lu0, lv0 = _f32(log_u_init), _f32(log_v_init)
         m = _f32(mask)
+        storage = opts[4] if len(opts) > 4 and opts[4] is not None else "auto"
+        if storage not in _STORAGE:
+            raise ValueError(f"storage must be one of {sorted(_STORAGE)}, got {storage!r}")
         f32 = dict(device=dev, dtype=torch.float32)
         # the kernel writes every position (zeros where padded)
         o_flat = torch.empty(B, N, H * d, **f32)
@@ -100,7 +108,7 @@ class FlashSinkhornAttn(torch.autograd.Function):
             _lib.ptr(lu0), _lib.ptr(lv0), _lib.ptr(m),
             B, H, N, d, int(K_iter), float(lam), float(r_0),
             o_flat.data_ptr(), x_c.data_ptr(), log_u.data_ptr(), log_v.data_ptr(),
-            o_avg.data_ptr(), log_z.data_ptr(), col_lse.data_ptr())
+            o_avg.data_ptr(), log_z.data_ptr(), col_lse.data_ptr(), _STORAGE[storage])
         rc = _lib.timed_launch("sinkhorn_fwd", dev, lambda: lib.dfl_sinkhorn_fwd(
             ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
         _lib.check(rc, "dfl_sinkhorn_fwd")
@@ -116,14 +124,14 @@ class FlashSinkhornAttn(torch.autograd.Function):
             raise ValueError(f"ift_mode must be one of {sorted(_MODES)}, got {mode!r}")
         ctx.save_for_backward(q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c)
         ctx.meta = (B, H, N, d, dt, float(lam), float(r_0), solver, int(iters), mode, rtol, len(opts),
-                    Q_ln.dtype, G is not None)
+                    Q_ln.dtype, G is not None, storage)
         ctx.set_materialize_grads(False)
         return o_flat, x_c, log_u, log_v
 
     @staticmethod
     def backward(ctx, grad_o_flat, grad_xc, grad_lu_unused, grad_lv_unused):
         (q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c) = ctx.saved_tensors
-        (B, H, N, d, dt, lam, r_0, solver, iters, mode, rtol, n_opts, in_dtype, has_g) = ctx.meta
+        (B, H, N, d, dt, lam, r_0, solver, iters, mode, rtol, n_opts, in_dtype, has_g, storage) = ctx.meta
         dev = q.device
         f32 = dict(device=dev, dtype=torch.float32)
         if grad_o_flat is None:
@@ -160,7 +168,7 @@ class FlashSinkhornAttn(torch.autograd.Function):
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
             dlmu.data_ptr(), dlnu.data_ptr(),
             _lib.ptr(dx) if need_dx else None, _lib.ptr(dpw) if need_dpw else None,
-            _lib.ptr(dw) if need_dw else None)
+            _lib.ptr(dw) if need_dw else None, _STORAGE[storage])
         rc = _lib.timed_launch("sinkhorn_bwd", dev, lambda: lib.dfl_sinkhorn_bwd(
             ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
         _lib.check(rc, "dfl_sinkhorn_bwd")
@@ -193,6 +201,7 @@ def flash_sinkhorn_attn(
     ift_iters: int | None = None,
     ift_mode: str = "reference",
     cg_rtol: float = 0.0,
+    storage: str = "auto",
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Flash-Sinkhorn attention (flash_sinkhorn_attn.py:670-795).
 
@@ -213,7 +222,7 @@ def flash_sinkhorn_attn(
         mask = mask.unsqueeze(0) if mask is not None else None
     out = FlashSinkhornAttn.apply(Q_ln, K_ln, V, G, x_res, pos_weight, pos_bins, eps, w_dist, log_mu,
                                   log_nu, K_iter, lam, r_0, log_u_init, log_v_init, mask,
-                                  ift_solver, ift_iters, ift_mode, cg_rtol)
+                                  ift_solver, ift_iters, ift_mode, cg_rtol, storage)
     if unbatched:
         return tuple(t.squeeze(0) for t in out)
     return out

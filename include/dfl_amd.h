@@ -55,7 +55,14 @@ int dfl_workspace_error(const void* workspace, void* stream);
  * Outputs o_flat (B,N,H*d), x_centroid (B,H,N,3), log_u, log_v (B,H,N); saved for the
  * backward: o_avg (B,H,N,d), log_z (B,H,N) = LSE_j(u_i + L_ij + v_j) and
  * col_lse (B,H,N) = LSE_i(L_ij + u_i) of the last column update.
+ * storage selects where the kernels keep Q, K and the length-N vectors:
+ * DFL_STORAGE_AUTO (0) picks RESIDENT when it fits in LDS, else STREAM;
+ * RESIDENT keeps all of them in LDS (fails with an argument error if they do not
+ * fit); STREAM keeps only each workgroup's stripe in LDS and streams the rest
+ * through L2 (long sequences, e.g. N = 4096, d = 64).  Results agree to rounding.
  */
+enum dfl_storage { DFL_STORAGE_AUTO = 0, DFL_STORAGE_RESIDENT = 1, DFL_STORAGE_STREAM = 2 };
+
 typedef struct dfl_sinkhorn_fwd_params {
   int dtype;
   const void* q;
@@ -84,6 +91,7 @@ typedef struct dfl_sinkhorn_fwd_params {
   float* o_avg;
   float* log_z;
   float* col_lse;
+  int storage;
 } dfl_sinkhorn_fwd_params;
 
 size_t dfl_sinkhorn_workspace_size(int B, int H, int N);
@@ -103,6 +111,7 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
  * grad_xc (B,H,N,3) fp32 (may be NULL).  Outputs (fp32, fully written):
  * dq, dk, dv, dg (B,H,N,d), dlog_mu, dlog_nu (B,H,N); optional (NULL = not requested,
  * which also skips their per-element work): dx_res (B,N,3), dpos_weight (H,68), dw_dist (H,).
+ * storage: as for the forward (the two calls choose independently).
  */
 enum dfl_ift_solver { DFL_IFT_FIXED_POINT = 0, DFL_IFT_CG = 1 };
 enum dfl_ift_mode { DFL_IFT_REFERENCE = 0, DFL_IFT_ANALYTIC = 1 };
@@ -144,6 +153,7 @@ typedef struct dfl_sinkhorn_bwd_params {
   float* dx_res;
   float* dpos_weight;
   float* dw_dist;
+  int storage;
 } dfl_sinkhorn_bwd_params;
 
 int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);

@@ -1,0 +1,188 @@
+"""GPU parity of the stream storage mode (long sequences) of the flash-Sinkhorn path.
+
+Stream mode keeps one stripe of Q/K per workgroup in LDS and streams the rest
+from zero-padded copies through L2.  It is forced here (storage="stream") at
+sizes the numpy oracle finishes in seconds, compared with the resident mode
+where both fit, and run at BASELINE configs[4] (B=1, H=16, N=4096, d=64, bf16,
+where only stream mode fits) against the dense torch checker on the GPU.
+Bars as in the north star: 1e-4 relative (fp32 inputs), 2e-2 (bf16 inputs).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_rel, max_rel_err
+from oracle import sinkhorn as ref
+from oracle import sinkhorn_dense_torch as dense
+from test_gpu_sinkhorn_bwd import GRADS, compare, grad_inputs, run_gpu_bwd
+from test_gpu_sinkhorn_fwd import make_inputs, oracle_inputs, run_gpu
+
+pytestmark = pytest.mark.gpu
+
+S = dict(storage="stream")
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("B,H,N,d,eps,K", [
+    (1, 4, 256, 32, [1.0] * 4, 20),      # BASELINE config 1 shape
+    (2, 2, 70, 16, [0.5, 2.0], 7),       # ragged tile, small d
+    (1, 2, 100, 64, [0.25, 1.0], 5),     # d = 64
+    (1, 1, 16, 8, [1.0], 3),             # single tile
+    (1, 1, 600, 32, [0.5], 6),           # 38 tiles over 16 members: multi-tile stripes
+])
+def test_stream_forward_matches_oracle(dtype, tol, B, H, N, d, eps, K):
+    inp = make_inputs(B, H, N, d, seed=100 + N + d, eps=eps)
+    got = run_gpu(inp, K, dtype, **S)
+    want = ref.forward(**oracle_inputs(inp, dtype), K_iter=K)
+    for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+        assert_close_rel(gv, want[name], tol, name)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_stream_forward_general_cost(dtype, tol):
+    inp = make_inputs(2, 4, 40, 32, seed=5, eps=[0.5, 1.0, 2.0, 4.0], pos_geo=True)
+    got = run_gpu(inp, 6, dtype, **S)
+    want = ref.forward(**oracle_inputs(inp, dtype), K_iter=6)
+    for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+        assert_close_rel(gv, want[name], tol, name)
+
+
+def test_stream_forward_masked_equals_unpadded():
+    B, H, N, d = 3, 2, 96, 32
+    inp = make_inputs(B, H, N, d, seed=9, eps=[0.5, 1.0])
+    lengths = [96, 61, 17]
+    mask = torch.zeros(B, N)
+    for b, n in enumerate(lengths):
+        mask[b, :n] = 1
+    got = run_gpu(inp, 8, torch.bfloat16, mask=mask, **S)
+    oi = oracle_inputs(inp, torch.bfloat16)
+    oi["mask"] = mask.numpy()
+    fo, _ = ref.backward_masked(dict(oi, K_iter=8, lam=1.0, r_0=10.0), None)
+    for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+        assert_close_rel(gv, fo[name], 2e-2, name)
+        for b, n in enumerate(lengths):
+            assert np.all((gv[b, n:] if name == "o_flat" else gv[b, :, n:]) == 0)
+
+
+@pytest.mark.parametrize("B,H,N,d,eps,K", [
+    (1, 2, 48, 32, [0.5, 1.0], 6),
+    (2, 2, 70, 16, [0.5, 2.0], 7),
+    (1, 2, 100, 64, [0.25, 1.0], 5),
+    (1, 1, 600, 32, [0.5], 6),
+])
+def test_stream_backward_reference_fp32(B, H, N, d, eps, K):
+    inp = make_inputs(B, H, N, d, seed=200 + N, eps=eps)
+    go, gxc = grad_inputs(B, H, N, d, seed=300 + N, with_xc=True)
+    got = run_gpu_bwd(inp, K, torch.float32, go, gxc, **S)
+    oi = oracle_inputs(inp, torch.float32)
+    fo = ref.forward(**oi, K_iter=K)
+    want = ref.backward_reference(dict(oi, K_iter=K), fo, go.numpy(), gxc.numpy())
+    compare(got, want, 1e-4, "stream-fp32-ref")
+
+
+def test_stream_backward_cg_matches_oracle():
+    B, H, N, d = 1, 2, 64, 32
+    inp = make_inputs(B, H, N, d, seed=51, eps=[0.5, 0.25])
+    go, gxc = grad_inputs(B, H, N, d, seed=52, with_xc=True)
+    got = run_gpu_bwd(inp, 20, torch.float32, go, gxc, ift_solver="cg", ift_iters=20, **S)
+    oi = oracle_inputs(inp, torch.float32)
+    fo = ref.forward(**oi, K_iter=20)
+    want = ref.backward_reference(dict(oi, K_iter=20), fo, go.numpy(), gxc.numpy(), solver="cg", n_cg=20)
+    compare(got, want, 1e-4, "stream-cg")
+
+
+@pytest.mark.parametrize("solver,iters", [("fixed_point", None), ("cg", 20)])
+def test_stream_backward_masked_bf16(solver, iters):
+    B, H, N, d = 2, 2, 96, 32
+    K = 12
+    inp = make_inputs(B, H, N, d, seed=71, eps=[0.5, 1.0])
+    go, _ = grad_inputs(B, H, N, d, seed=72)
+    lengths = [96, 61]
+    mask = torch.zeros(B, N)
+    for b, n in enumerate(lengths):
+        mask[b, :n] = 1
+        go[b, n:] = 0
+    got = run_gpu_bwd(inp, K, torch.bfloat16, go, None, mask=mask, ift_solver=solver, ift_iters=iters, **S)
+    oi = oracle_inputs(inp, torch.bfloat16)
+    oi["mask"] = mask.numpy()
+    _, want = ref.backward_masked(dict(oi, K_iter=K, lam=1.0, r_0=10.0), go.numpy(), None,
+                                  solver=solver, n_cg=iters)
+    compare(got, want, 2e-2, f"stream-masked-{solver}", skip=("pos_weight", "w_dist", "x_res"))
+    for b, n in enumerate(lengths):
+        for k in ("Q", "K", "V", "G"):
+            assert np.all(got[k][b, :, n:] == 0), k
+
+
+def test_stream_backward_general_cost_fp32():
+    B, H, N, d = 2, 2, 40, 32
+    inp = make_inputs(B, H, N, d, seed=81, eps=[0.5, 2.0], pos_geo=True)
+    go, gxc = grad_inputs(B, H, N, d, seed=82, with_xc=True)
+    got = run_gpu_bwd(inp, 5, torch.float32, go, gxc, **S)
+    oi = oracle_inputs(inp, torch.float32)
+    fo = ref.forward(**oi, K_iter=5)
+    want = ref.backward_reference(dict(oi, K_iter=5), fo, go.numpy(), gxc.numpy())
+    compare(got, want, 1e-4, "stream-general")
+
+
+def test_stream_equals_resident():
+    """Where both storage modes fit they compute the same thing (summation order aside)."""
+    B, H, N, d = 2, 4, 512, 32
+    inp = make_inputs(B, H, N, d, seed=91, eps=[0.5, 1.0, 0.25, 2.0])
+    go, gxc = grad_inputs(B, H, N, d, seed=92, with_xc=True)
+    kw = dict(ift_solver="cg", ift_iters=15)
+    fr = run_gpu(inp, 12, torch.bfloat16, storage="resident")
+    fs = run_gpu(inp, 12, torch.bfloat16, storage="stream")
+    for name, a, b in zip(("o_flat", "x_centroid", "log_u", "log_v"), fr, fs):
+        assert max_rel_err(b, a) <= 1e-4, name
+    gr = run_gpu_bwd(inp, 12, torch.bfloat16, go, gxc, storage="resident", **kw)
+    gs = run_gpu_bwd(inp, 12, torch.bfloat16, go, gxc, storage="stream", **kw)
+    for k in GRADS:
+        if k in gr:
+            assert max_rel_err(gs[k], gr[k]) <= 1e-4, k
+
+
+def test_baseline_config5_full_size():
+    """B=1, H=16, N=4096, d=64, bf16, Dirichlet(5) marginals,
+    eps=0.25, K=100, IFT with 30 CG steps (storage auto -> stream).  Checked against
+    the dense torch restatement (fp32, same bf16-rounded inputs) on the GPU."""
+    from deepfold_amd import flash_sinkhorn_attn
+
+    B, H, N, d = 1, 16, 4096, 64
+    K_iter, n_cg, eps_v = 100, 30, 0.25
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1005)
+    Q = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    Kt = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    V = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    G = torch.zeros(B, H, N, d, dtype=torch.bfloat16)
+    rng = np.random.default_rng(1005)
+    lmu = torch.from_numpy(np.log(rng.dirichlet(5.0 * np.ones(N), size=(B, H)))).float()
+    lnu = torch.from_numpy(np.log(rng.dirichlet(5.0 * np.ones(N), size=(B, H)))).float()
+    dO = torch.randn(B, N, H * d, generator=g).to(torch.bfloat16).float()
+    eps = torch.full((H,), eps_v)
+    print(f"[cfg5] B={B} H={H} N={N} d={d} K={K_iter} n_cg={n_cg}", flush=True)
+
+    leaves = [t.to(dev).requires_grad_(True) for t in (Q, Kt, V, G)]
+    lm, ln = lmu.to(dev).requires_grad_(True), lnu.to(dev).requires_grad_(True)
+    o, xc, lu, lv = flash_sinkhorn_attn(*leaves, torch.zeros(B, N, 3, device=dev), torch.zeros(H, 68, device=dev),
+                                        None, eps.to(dev), torch.zeros(H, device=dev), lm, ln, K_iter=K_iter,
+                                        ift_solver="cg", ift_iters=n_cg)
+    o.backward(dO.to(dev))
+    torch.cuda.synchronize()
+
+    f = lambda t: t.to(dev).float()
+    fo = dense.forward(f(Q), f(Kt), f(V), f(G), f(eps), f(lmu), f(lnu), K_iter)
+    gd = dense.backward_cg(f(Q), f(Kt), f(V), f(G), f(eps), fo, f(dO), n_cg)
+    errs = {}
+    for name, got, want in (("o_flat", o, fo["o_flat"]), ("log_u", lu, fo["log_u"]), ("log_v", lv, fo["log_v"]),
+                            ("dQ", leaves[0].grad, gd["Q"]), ("dK", leaves[1].grad, gd["K"]),
+                            ("dV", leaves[2].grad, gd["V"]), ("dG", leaves[3].grad, gd["G"]),
+                            ("dlog_mu", lm.grad, gd["log_mu"]), ("dlog_nu", ln.grad, gd["log_nu"])):
+        errs[name] = float((got.float() - want).abs().max() / want.abs().max())
+    print("[cfg5] max rel err vs dense fp32 checker: " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()),
+          flush=True)
+    for k, v in errs.items():
+        assert v <= 2e-2, (k, v)
