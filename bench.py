@@ -1,15 +1,22 @@
 """Benchmark: flash-Sinkhorn forward + IFT backward per layer on one MI355X.
 
-Workload: B=2, H=8, N=768 padded, d=32, bf16 inputs
-with fp32 accumulation, ragged valid lengths n_b ~ U[384, 768] with a padding
-mask, eps=0.5, 50 Sinkhorn iterations, 20 CG iterations in the IFT solve,
-upstream gradient dO ~ N(0,1).  Synthetic data, seed 1002 (= 1000 + config#).
-Unspecified terms are neutral: no position bins, w_dist = 0, x_res = 0, G = 0.
+Default workload (the metric's configuration): B=2,
+H=8, N=768 padded, d=32, bf16 inputs with fp32 accumulation, ragged valid
+lengths n_b ~ U[384, 768] with a padding mask, eps=0.5, 50 Sinkhorn iterations,
+20 CG iterations in the IFT solve, upstream gradient dO ~ N(0,1).  Synthetic
+data, seed 1002 (= 1000 + config#).  Unspecified terms are neutral: no position
+bins, w_dist = 0, x_res = 0, G = 0.
 
 One "step" = one forward (flash_sinkhorn_attn) + one backward (autograd) of the
 layer, inputs resident in HBM.  Prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+                    [--workload cfg2|cfg5|cfg3|cfg4]
+    python bench.py --rocpd-summary RESULTS.db    (CPU only: kernel table of a rocprofv3 run)
+
+Opt-in workloads: cfg5 = BASELINE configs[4] (B=1, H=16, N=4096, d=64, bf16,
+Dirichlet(5) marginals, eps=0.25, K=100, 30 CG steps; stream storage mode);
+cfg3 / cfg4 = the attention rows (configs[2] and [3]).
 """
 
 from __future__ import annotations
@@ -30,54 +37,68 @@ PEAK_HBM = 8.0e12
 # v_exp_f32 rate used by BASELINE.md's exp roof (quarter-rate estimate).
 PEAK_EXP_NOMINAL = 9.8e12
 
-CFG = dict(B=2, H=8, N=768, d=32, eps=0.5, K_iter=50, n_cg=20, seed=1002)
+SINKHORN = {
+    "cfg2": dict(B=2, H=8, N=768, d=32, eps=0.5, K_iter=50, n_cg=20, seed=1002, ragged=True, dirichlet=False,
+                 workload="BASELINE configs[1]: flash-Sinkhorn fwd + IFT(CG) bwd"),
+    "cfg5": dict(B=1, H=16, N=4096, d=64, eps=0.25, K_iter=100, n_cg=30, seed=1005, ragged=False, dirichlet=True,
+                 workload="BASELINE configs[4]: large-scale flash-Sinkhorn fwd + IFT(CG) bwd (stream storage)"),
+}
 
 
-def make_workload(device, dtype=None):
+def make_workload(cfg, device, dtype=None):
+    """Synthetic inputs of one Sinkhorn configuration, built on the CPU (seeded) and copied."""
+    import numpy as np
     import torch
 
     dtype = dtype or torch.bfloat16
-    B, H, N, d = CFG["B"], CFG["H"], CFG["N"], CFG["d"]
-    g = torch.Generator().manual_seed(CFG["seed"])
-    lengths = torch.randint(384, 769, (B,), generator=g).tolist()
+    B, H, N, d = cfg["B"], cfg["H"], cfg["N"], cfg["d"]
+    g = torch.Generator().manual_seed(cfg["seed"])
+    lengths = torch.randint(384, N + 1, (B,), generator=g).tolist() if cfg["ragged"] else [N] * B
     Q = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(dtype)
     K = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(dtype)
     V = (torch.randn(B, H, N, d, generator=g) / math.sqrt(d)).to(dtype)
     G = torch.zeros(B, H, N, d, dtype=dtype)
     mask = torch.zeros(B, N)
     log_m = torch.zeros(B, H, N)
+    log_n = torch.zeros(B, H, N)
+    rng = np.random.default_rng(cfg["seed"])
     for b, n in enumerate(lengths):
         mask[b, :n] = 1.0
-        log_m[b, :, :n] = -math.log(n)
+        if cfg["dirichlet"]:
+            log_m[b, :, :n] = torch.from_numpy(np.log(rng.dirichlet(5.0 * np.ones(n), size=H))).float()
+            log_n[b, :, :n] = torch.from_numpy(np.log(rng.dirichlet(5.0 * np.ones(n), size=H))).float()
+        else:
+            log_m[b, :, :n] = -math.log(n)
+            log_n[b, :, :n] = -math.log(n)
     dO = torch.randn(B, N, H * d, generator=g).to(dtype).float()
     dO = dO * mask[:, :, None]
     x = torch.zeros(B, N, 3)
     pw = torch.zeros(H, 68)
-    eps = torch.full((H,), CFG["eps"])
+    eps = torch.full((H,), cfg["eps"])
     wd = torch.zeros(H)
     cpu = dict(Q=Q, K=K, V=V, G=G, x_res=x, pos_weight=pw, eps=eps, w_dist=wd, log_mu=log_m,
-               log_nu=log_m.clone(), mask=mask, dO=dO, lengths=lengths)
+               log_nu=log_n, mask=None if not cfg["ragged"] else mask, dO=dO, lengths=lengths)
     dev = {k: (v.to(device) if hasattr(v, "to") else v) for k, v in cpu.items()}
     return cpu, dev
 
 
-def step(t):
+def step(cfg, t):
     from deepfold_amd import flash_sinkhorn_attn
 
     q, k, v, g = (t[n].detach().requires_grad_(True) for n in ("Q", "K", "V", "G"))
     o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], t["w_dist"],
-                                        t["log_mu"], t["log_nu"], K_iter=CFG["K_iter"], mask=t["mask"],
-                                        ift_solver="cg", ift_iters=CFG["n_cg"])
+                                        t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
+                                        ift_solver="cg", ift_iters=cfg["n_cg"])
     o.backward(t["dO"])
     return q.grad
 
 
-def algorithmic_counts(lengths):
-    """Per-layer algorithmic work (BASELINE.md section 2 / SURVEY.md section 8d):
-    E = sum_b H n_b^2 valid plan elements; forward 2K LSE sweeps at 2d flops +
-    one output sweep at 4d; backward n_CG matvec sweeps at 2d + g_v sweep 6d +
-    gradient sweep 8d; one exp per element per sweep."""
-    H, d, K, ncg = CFG["H"], CFG["d"], CFG["K_iter"], CFG["n_cg"]
+def algorithmic_counts(cfg, lengths):
+    """Per-layer algorithmic work: E = sum_b H n_b^2 valid
+    plan elements; forward 2K LSE sweeps at 2d flops + one output sweep at 4d;
+    backward n_CG matvec sweeps at 2d + g_v sweep 6d + gradient sweep 8d; one
+    exp per element per sweep."""
+    H, d, K, ncg = cfg["H"], cfg["d"], cfg["K_iter"], cfg["n_cg"]
     E = sum(H * n * n for n in lengths)
     f_fwd = E * d * (4 * K + 4)
     f_bwd = E * d * (14 + 2 * ncg)
@@ -86,23 +107,38 @@ def algorithmic_counts(lengths):
     return E, f_fwd, f_bwd, x_fwd, x_bwd
 
 
-def profiled_traffic(kernel):
-    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 FETCH_SIZE /
+def profiled_traffic(kernel, profile="sinkhorn_cfg2_bench.md"):
+    """HBM bytes per launch of ``kernel`` from a committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (calibrated against a copy kernel), or None."""
     import re
 
-    path = os.path.join(ROOT, "profiles", "sinkhorn_cfg2_bench.md")
+    path = os.path.join(ROOT, "profiles", profile)
     if not os.path.exists(path):
         return None
     m = re.search(rf"^\s*{kernel} hbm_bytes_per_launch = (\d+)", open(path).read(), flags=re.M)
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(cpu, budget_s=12.0):
-    """Time the numpy oracle (float32, one thread) on a bounded sample of the
-    layer: full forward (K=50) + reference fixed-point IFT backward (50 sweeps)
-    of whole (b, h) heads, cycling over the heads until ~budget_s of CPU time is
-    spent, then scaled by plan elements to one layer (B*H heads)."""
+def _head_inputs(cfg, cpu, b, h, K_iter):
+    n = cpu["lengths"][b]
+    sl = lambda a: a[b:b + 1, h:h + 1, :n].float().numpy()
+    return dict(Q=sl(cpu["Q"]), K=sl(cpu["K"]), V=sl(cpu["V"]), G=sl(cpu["G"]),
+                x_res=cpu["x_res"][b:b + 1, :n].numpy(), pos_weight=cpu["pos_weight"][h:h + 1].numpy(),
+                pos_bins=None, eps=cpu["eps"][h:h + 1].numpy(), w_dist=cpu["w_dist"][h:h + 1].numpy(),
+                log_mu=cpu["log_mu"][b:b + 1, h:h + 1, :n].numpy(),
+                log_nu=cpu["log_nu"][b:b + 1, h:h + 1, :n].numpy(),
+                K_iter=K_iter, lam=1.0, r_0=10.0)
+
+
+def cpu_baseline(cfg, cpu, budget_s=12.0):
+    """The numpy oracle (float32, one thread) on a bounded sample of the layer:
+    dense forward + the reference's fixed-point IFT backward (K_back = K_iter
+    sweeps, flash_sinkhorn_attn.py:471-542) of whole (b, h) heads.
+
+    cfg2: full heads (K = 50), cycling over the heads until ~budget_s of CPU time
+    is spent, scaled to one layer by valid plan elements.
+    cfg5: one head at K = 4 and K = 12; the per-iteration slope and the intercept
+    are extrapolated to K = 100 and scaled to the 16 heads (labelled as such)."""
     import numpy as np
 
     try:
@@ -112,40 +148,139 @@ def cpu_baseline(cpu, budget_s=12.0):
     sys.path.insert(0, ROOT)
     from oracle import sinkhorn as ref
 
-    B, H, d = CFG["B"], CFG["H"], CFG["d"]
+    B, H, d, K = cfg["B"], cfg["H"], cfg["d"], cfg["K_iter"]
     lengths = cpu["lengths"]
-    spent, sampled, heads = 0.0, 0, []
     ctx = threadpool_limits(limits=1) if threadpool_limits else None
+
+    def one_head(b, h, k_iter):
+        inp = _head_inputs(cfg, cpu, b, h, k_iter)
+        n = lengths[b]
+        go = cpu["dO"].reshape(B, -1, H, d)[b:b + 1, :n, h, :].numpy()
+        t0 = time.perf_counter()
+        fo = ref.forward(**inp, dtype=np.float32)
+        ref.backward_reference(inp, fo, go, None, K_back=k_iter, dtype=np.float32)
+        return time.perf_counter() - t0
+
     try:
-        order = [(b, h) for h in range(H) for b in range(B)] * 64  # alternate samples
-        for b, h in order:
-            n = lengths[b]
-            sl = lambda a: a[b:b + 1, h:h + 1, :n].float().numpy()
-            inp = dict(Q=sl(cpu["Q"]), K=sl(cpu["K"]), V=sl(cpu["V"]), G=sl(cpu["G"]),
-                       x_res=cpu["x_res"][b:b + 1, :n].numpy(), pos_weight=cpu["pos_weight"][h:h + 1].numpy(),
-                       pos_bins=None, eps=cpu["eps"][h:h + 1].numpy(), w_dist=cpu["w_dist"][h:h + 1].numpy(),
-                       log_mu=cpu["log_mu"][b:b + 1, h:h + 1, :n].numpy(),
-                       log_nu=cpu["log_nu"][b:b + 1, h:h + 1, :n].numpy(),
-                       K_iter=CFG["K_iter"], lam=1.0, r_0=10.0)
-            go = cpu["dO"].reshape(B, -1, H, d)[b:b + 1, :n, h, :].numpy()
-            t0 = time.perf_counter()
-            fo = ref.forward(**inp, dtype=np.float32)
-            ref.backward_reference(inp, fo, go, None, K_back=CFG["K_iter"], dtype=np.float32)
-            spent += time.perf_counter() - t0
-            sampled += 1
-            heads.append((b, h))
-            if spent > budget_s:
-                break
+        if not cfg["dirichlet"]:
+            spent, heads = 0.0, []
+            for b, h in [(b, h) for h in range(H) for b in range(B)] * 64:  # alternate samples
+                spent += one_head(b, h, K)
+                heads.append((b, h))
+                if spent > budget_s:
+                    break
+            e_all = sum(H * n * n for n in lengths)
+            e_smp = sum(lengths[b] ** 2 for b, _ in heads)
+            value = spent * e_all / e_smp
+            sample = (f"numpy oracle (float32, 1 thread): dense forward K={K} + reference fixed-point IFT backward "
+                      f"({K} sweeps), {len(heads)} (b,h) head solves cycling over the layer's {B * H} heads "
+                      f"({spent:.1f} s), scaled to one layer by valid plan elements")
+        else:
+            k1, k2 = 4, 12
+            t1, t2 = one_head(0, 0, k1), one_head(0, 0, k2)
+            slope = (t2 - t1) / (k2 - k1)
+            per_head = t1 + slope * (K - k1)
+            value = per_head * B * H
+            sample = (f"numpy oracle (float32, 1 thread), one ({lengths[0]}-token) head: forward + reference "
+                      f"fixed-point IFT backward at K=K_back={k1} ({t1:.1f} s) and {k2} ({t2:.1f} s), "
+                      f"linearly extrapolated to K=K_back={K} and scaled to {B * H} heads")
     finally:
         if ctx is not None:
             ctx.__exit__(None, None, None)
-    # per-head cost scales with n_b^2: extrapolate by the sampled share of plan elements
-    e_all = sum(H * n * n for n in lengths)
-    e_smp = sum(lengths[b] ** 2 for b, _ in heads)
-    return dict(value=round(spent * e_all / e_smp * 1e3, 1), unit="ms/layer", cores=1, kind="port",
-                sample=f"numpy oracle (float32, 1 thread): dense forward K={CFG['K_iter']} + reference "
-                       f"fixed-point IFT backward ({CFG['K_iter']} sweeps), {sampled} (b,h) head solves cycling "
-                       f"over the layer's {B * H} heads ({spent:.1f} s), scaled to one layer by valid plan elements")
+    return dict(value=round(value * 1e3, 1), unit="ms/layer", cores=1, kind="port", sample=sample)
+
+
+def bench_sinkhorn(args, name):
+    import torch
+    from deepfold_amd import _lib
+
+    cfg = SINKHORN[name]
+    dev = torch.device("cuda:0")
+    cpu, t = make_workload(cfg, dev)
+    for _ in range(args.warmup):
+        step(cfg, t)
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` steps, kernel launches bracketed by events on the launch stream
+    _lib.launch_timings = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(cfg, t)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    timings = _lib.launch_timings
+    _lib.launch_timings = None
+    per = {}
+    for kname, s, e in timings:
+        per.setdefault(kname, []).append(s.elapsed_time(e))
+    avg = {k: sum(v) / len(v) for k, v in per.items()}
+    ms_per_step = wall * 1e3 / args.steps
+
+    E, f_fwd, f_bwd, x_fwd, x_bwd = algorithmic_counts(cfg, cpu["lengths"])
+    dom = max(avg, key=avg.get)
+    f_dom = f_fwd if dom == "sinkhorn_fwd" else f_bwd
+    x_dom = x_fwd if dom == "sinkhorn_fwd" else x_bwd
+    achieved = f_dom / (avg[dom] * 1e-3)
+    traffic = profiled_traffic(dom, "sinkhorn_cfg2_bench.md" if name == "cfg2" else f"sinkhorn_{name}_bench.md")
+    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
+    metric = ("flash-Sinkhorn fwd+IFT-bwd ms/layer @B2,H8,N768,d32 bf16; % of MFMA/HBM roof" if name == "cfg2"
+              else f"flash-Sinkhorn fwd+IFT-bwd ms/layer @B{cfg['B']},H{cfg['H']},N{cfg['N']},d{cfg['d']} bf16")
+    out = {
+        "metric": metric,
+        "value": round(ms_per_step, 4),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": (f"synthetic (seed {cfg['seed']}): Q,K,V ~ N(0,1)/sqrt(d), "
+                 + ("ragged n_b ~ U[384,768], " if cfg["ragged"] else "Dirichlet(5) marginals, ")
+                 + "dO ~ N(0,1)"),
+        "config": {"workload": cfg["workload"], "B": cfg["B"], "H": cfg["H"], "N": cfg["N"], "d": cfg["d"],
+                   "n_b": cpu["lengths"], "eps": cfg["eps"], "K_iter": cfg["K_iter"], "n_cg": cfg["n_cg"],
+                   "valid_plan_elements": E},
+        "kernel_ms": {k: round(v, 4) for k, v in avg.items()},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
+                     "peak": PEAK_MFMA_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_BF16, 5),
+                     "traffic": traffic},
+        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_NOMINAL,
+                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
+                         "layer_t_roof_ms": t_roof * 1e3, "layer_frac": t_roof * 1e3 / ms_per_step},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg, cpu)
+    print(json.dumps(out), flush=True)
+
+
+def rocpd_summary(db_path):
+    """Markdown table (calls, total/avg/min/max us, share) of every kernel in a
+    rocprofv3 results database; used for the committed profiles/ summaries."""
+    import sqlite3
+
+    con = sqlite3.connect(db_path)
+    short = lambda name: name if len(name) <= 90 else name[:87] + "..."
+    rows = con.execute("select name, count(*), sum(duration), avg(duration), min(duration), max(duration) "
+                       "from kernels group by name order by sum(duration) desc").fetchall()
+    if rows:
+        total = sum(r[2] for r in rows) or 1
+        print("| kernel | calls | total us | avg us | min us | max us | % |")
+        print("|---|---|---|---|---|---|---|")
+        for name, n, tot, avg, mn, mx in rows:
+            print(f"| `{short(name)}` | {n} | {tot / 1e3:.1f} | {avg / 1e3:.2f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} | "
+                  f"{100.0 * tot / total:.1f} |")
+    pmc = con.execute("select name, counter_name, count(*), avg(counter_value), min(counter_value), "
+                      "max(counter_value) from pmc_events group by name, counter_name "
+                      "order by name, counter_name").fetchall()
+    if pmc:
+        print("| kernel | counter | dispatches | avg per dispatch | min | max |")
+        print("|---|---|---|---|---|---|")
+        for name, counter, n, avg, mn, mx in pmc:
+            print(f"| `{short(name)}` | {counter} | {n} | {avg:.1f} | {mn:.1f} | {mx:.1f} |")
 
 
 def attention_workload(which, dev):
@@ -240,20 +375,25 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4"],
-                    help="cfg2 (default): the headline flash-Sinkhorn layer; cfg3 / cfg4: attention rows")
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg5", "cfg3", "cfg4"],
+                    help="cfg2 (default): the headline flash-Sinkhorn layer; cfg5: the N=4096 layer; "
+                         "cfg3 / cfg4: attention rows")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB -> 256 MiB elementwise copy (torch.neg), used to "
                          "calibrate the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--rocpd-summary", metavar="DB", help="print the kernel table of a rocprofv3 results "
+                    "database (no GPU needed) and exit")
     args = ap.parse_args()
+    if args.rocpd_summary:
+        rocpd_summary(args.rocpd_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the flash-Sinkhorn "
               "path shards by (b, h) with no communication, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
     import torch
-    import deepfold_amd
-    from deepfold_amd import _lib
+    import deepfold_amd  # noqa: F401
 
     os.environ["DFL_AMD_CHECK"] = "0"
     dev = torch.device("cuda:0")
@@ -267,65 +407,10 @@ def main():
         print(json.dumps({"calibrate_copy": {"kernel": "torch.neg", "launches": 5, "read_bytes": 4 * n,
                                              "write_bytes": 4 * n}}), flush=True)
         return
-    if args.workload != "cfg2":
+    if args.workload in SINKHORN:
+        bench_sinkhorn(args, args.workload)
+    else:
         bench_attention(args, args.workload)
-        return
-    cpu, t = make_workload(dev)
-    for _ in range(args.warmup):
-        step(t)
-    torch.cuda.synchronize()
-
-    # timed region: exactly `steps` steps, kernel launches bracketed by events
-    _lib.launch_timings = []
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(t)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    timings = _lib.launch_timings
-    _lib.launch_timings = None
-    per = {}
-    for name, s, e in timings:
-        per.setdefault(name, []).append(s.elapsed_time(e))
-    avg = {k: sum(v) / len(v) for k, v in per.items()}
-    ms_per_step = wall * 1e3 / args.steps
-
-    E, f_fwd, f_bwd, x_fwd, x_bwd = algorithmic_counts(cpu["lengths"])
-    dom = max(avg, key=avg.get)
-    f_dom = f_fwd if dom == "sinkhorn_fwd" else f_bwd
-    x_dom = x_fwd if dom == "sinkhorn_fwd" else x_bwd
-    achieved = f_dom / (avg[dom] * 1e-3)
-    traffic = profiled_traffic(dom)
-    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
-
-    out = {
-        "metric": "flash-Sinkhorn fwd+IFT-bwd ms/layer @B2,H8,N768,d32 bf16; % of MFMA/HBM roof",
-        "value": round(ms_per_step, 4),
-        "unit": "ms/layer",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seed 1002): Q,K,V ~ N(0,1)/sqrt(d), ragged n_b ~ U[384,768], dO ~ N(0,1)",
-        "config": {"workload": "BASELINE configs[1]: flash-Sinkhorn fwd + IFT(CG) bwd", "B": CFG["B"],
-                   "H": CFG["H"], "N": CFG["N"], "d": CFG["d"], "n_b": cpu["lengths"], "eps": CFG["eps"],
-                   "K_iter": CFG["K_iter"], "n_cg": CFG["n_cg"], "valid_plan_elements": E},
-        "kernel_ms": {k: round(v, 4) for k, v in avg.items()},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
-                     "peak": PEAK_MFMA_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_BF16, 5),
-                     "traffic": traffic},
-        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_NOMINAL,
-                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
-                         "layer_t_roof_ms": t_roof * 1e3, "layer_frac": t_roof * 1e3 / ms_per_step},
-    }
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(cpu)
-    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":
