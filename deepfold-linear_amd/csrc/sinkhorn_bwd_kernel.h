@@ -41,7 +41,9 @@ namespace dfl {
 
 constexpr int BWD_NT = 512;             // 8 waves: two per SIMD
 constexpr int BWD_NW = BWD_NT / WAVE;
-constexpr int BWD_MAXT = 2;             // resident tiles per wave in the heavy passes
+// Resident tiles per wave in the heavy passes: two at d <= 32; one at d = 64,
+// where two tiles' fragments and accumulators exceed the register file.
+template <int DP> constexpr int bwd_maxt() { return DP <= 32 ? 2 : 1; }
 constexpr int BWD_SCRATCH = sweep_scratch<BWD_NT>();
 constexpr int BWD_STREAM_SCRATCH = stream_scratch<BWD_NT>();
 // Length-Np float vectors of one workgroup: 13 vectors + coordinates and
@@ -424,9 +426,9 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     float* a2 = ct;                  // (u - logZ) in log2, rows (ct is free until the solve)
     for (int i = threadIdx.x; i < Np; i += BWD_NT) a2[i] = (i < n && valid[i]) ? uu[i] - lz[i] : NEG_BIG;
     __syncthreads();
-    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
-      // wave w owns resident tiles rt0 + w + 4*k, k < 4 (up to 16 tiles per batch)
-      constexpr int MAXT = BWD_MAXT;
+    for (int rt0 = 0; rt0 < nr; rt0 += bwd_maxt<DP>() * BWD_NW) {
+      // wave w owns resident tiles rt0 + w + BWD_NW*k, k < MAXT
+      constexpr int MAXT = bwd_maxt<DP>();
       typename M::Frag kf[MAXT], vf[MAXT];
       f32x4 cinit[MAXT], dvacc[MAXT][NC];
       float gva[MAXT], dxa[MAXT][3], xj[MAXT][3];
@@ -696,8 +698,8 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* Kc = R0;
     T* Vc = Kc + (size_t)CH * DP;
     T* KT = Vc + (size_t)CH * DP;  // [DP][CH]
-    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
-      constexpr int MAXT = BWD_MAXT;
+    for (int rt0 = 0; rt0 < nr; rt0 += bwd_maxt<DP>() * BWD_NW) {
+      constexpr int MAXT = bwd_maxt<DP>();
       typename M::Frag qf[MAXT], gf[MAXT], gfl[MAXT];
       f32x4 cinit[MAXT], dqacc[MAXT][NC];
       float lzi[MAXT], zui[MAXT], Di[MAXT], xi[MAXT][3], dci[MAXT][3], dxa[MAXT][3];
@@ -832,8 +834,8 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* QT = gOl + (size_t)CH * DP;   // [DP][CH]
     float* a2s = a2;
     float* zus = zu;
-    for (int rt0 = 0; rt0 < nr; rt0 += BWD_MAXT * BWD_NW) {
-      constexpr int MAXT = BWD_MAXT;
+    for (int rt0 = 0; rt0 < nr; rt0 += bwd_maxt<DP>() * BWD_NW) {
+      constexpr int MAXT = bwd_maxt<DP>();
       typename M::Frag kf[MAXT], vf[MAXT];
       f32x4 cinit[MAXT], dkacc[MAXT][NC];
       float lcj[MAXT], zvj[MAXT], xj[MAXT][3], dxa[MAXT][3];

@@ -362,8 +362,13 @@ __device__ __forceinline__ void stripe(int n_tiles, int member, int G, int& t0, 
 // tile is fetched once per batch of STREAM_RB resident tiles; the next group of
 // SCH streamed fragments is in flight while the current group is consumed.
 constexpr int STREAM_RB = 8;
-// Streamed fragments per group (double-buffered in registers).
-template <typename T, int DP> constexpr int stream_sch() { return (sizeof(T) == 4 && DP == 64) ? 2 : 4; }
+// Streamed fragments per group (double-buffered in registers).  The weighted
+// sum also carries the streamed weights, so it takes half the group where
+// fragments are wide (d = 64 or fp32).
+template <typename T, int DP, int KIND>
+constexpr int stream_sch() {
+  return (KIND == 2 && (DP == 64 || sizeof(T) == 4)) || (sizeof(T) == 4 && DP == 64) ? 2 : 4;
+}
 template <int NT> constexpr int stream_scratch() { return 2 * (NT / WAVE) * STREAM_RB * 16; }
 
 enum { SW_LSE_ONLINE = 0, SW_LSE_FIXED = 1, SW_WSUM = 2 };
@@ -386,7 +391,7 @@ __device__ __forceinline__ void stream_sweep(const T* __restrict__ res, const T*
   using Frag = typename M::Frag;
   constexpr int NW = NT / WAVE;
   constexpr int RB = STREAM_RB;
-  constexpr int SCH = stream_sch<T, DP>();
+  constexpr int SCH = stream_sch<T, DP, KIND>();
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int g = lane >> 4;
