@@ -10,6 +10,7 @@
 
 #include "../../include/dfl_amd.h"
 #include "attn_args.h"
+#include "dense_args.h"
 #include "sinkhorn_args.h"
 
 namespace dfl {
@@ -31,6 +32,13 @@ hipError_t launch_attn_fwd(const AttnArgs& a, bool bf16_in, int DP, hipStream_t 
 hipError_t launch_attn_bwd(const AttnArgs& a, bool bf16_in, int DP, hipStream_t s);
 hipError_t launch_a2t_fwd(const A2TArgs& a, bool bf16_in, hipStream_t s);
 hipError_t launch_a2t_bwd(const A2TArgs& a, bool bf16_in, hipStream_t s);
+hipError_t dense_sinkhorn_init(const DenseSinkArgs& a, hipStream_t s);
+hipError_t dense_sinkhorn_iteration(const DenseSinkArgs& a, int k, hipStream_t s);
+hipError_t dense_sinkhorn_finish(const DenseSinkArgs& a, int k, hipStream_t s);
+hipError_t dense_sinkhorn_backward(const DenseSinkBwdArgs& a, hipStream_t s);
+hipError_t dense_zero(float* p, size_t n, hipStream_t s);
+hipError_t dense_transport_forward(const DenseTransportArgs& a, hipStream_t s);
+hipError_t dense_transport_backward(const DenseTransportArgs& a, hipStream_t s);
 }  // namespace dfl
 
 namespace {
@@ -454,6 +462,155 @@ int dfl_a2t_bwd(const dfl_a2t_params* p, void* workspace, size_t workspace_bytes
   a.dkv = static_cast<float*>(workspace);
   hipError_t e = dfl::launch_a2t_bwd(a, p->dtype == DFL_BF16, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "atom-to-token backward launch");
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Dense (materialised-cost) Sinkhorn
+size_t dfl_dense_sinkhorn_workspace_size(int B, int H, int N, int K) {
+  if (B <= 0 || H <= 0 || N <= 0 || K < 0) return 0;
+  const size_t bhn = (size_t)B * H * N;
+  return ((size_t)2 * (K + 1) * 4 + 255) / 256 * 256 + (2 * bhn * 4 + 255) / 256 * 256;
+}
+
+int dfl_dense_sinkhorn_fwd(const dfl_dense_sinkhorn_params* p, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (!p) return fail("params is NULL");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0) return fail("B, H, N must be positive");
+  if (p->K < 0 || p->K > 100000) return fail("K=%d outside [0, 100000]", p->K);
+  if (!p->C || !p->log_mu || !p->log_nu || !p->eps || !p->log_u || !p->log_v || !p->history)
+    return fail("required pointer is NULL");
+  if (p->threshold >= 0.f && p->check_every <= 0) return fail("check_every must be positive");
+  const size_t need = dfl_dense_sinkhorn_workspace_size(p->B, p->H, p->N, p->K);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  const size_t bhn = (size_t)p->B * p->H * p->N;
+  dfl::DenseSinkArgs a;
+  memset(&a, 0, sizeof(a));
+  a.C = p->C; a.log_mu = p->log_mu; a.log_nu = p->log_nu; a.eps = p->eps;
+  a.u_init = p->log_u_init; a.v_init = p->log_v_init; a.mask = p->mask;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.K = p->K; a.lam = p->lam;
+  const size_t slices = (size_t)(p->K + 1) * bhn;
+  a.hist_u = p->history;
+  a.hist_v = p->history + slices;
+  a.hist_r = p->history + 2 * slices;
+  a.hist_c = p->history + 3 * slices;
+  const bool early = p->threshold >= 0.f;
+  a.delta = early ? static_cast<uint32_t*>(workspace) : nullptr;
+  a.log_u = p->log_u; a.log_v = p->log_v;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dfl::dense_sinkhorn_init(a, s);
+  if (e != hipSuccess) return hip_fail(e, "dense sinkhorn init launch");
+  int done = 0;
+  for (int k = 1; k <= p->K; ++k) {
+    e = dfl::dense_sinkhorn_iteration(a, k, s);
+    if (e != hipSuccess) return hip_fail(e, "dense sinkhorn iteration launch");
+    done = k;
+    if (early && k % p->check_every == 0) {
+      uint32_t words[2] = {0, 0};
+      e = hipMemcpyAsync(words, a.delta + 2 * k, sizeof(words), hipMemcpyDeviceToHost, s);
+      if (e != hipSuccess) return hip_fail(e, "dense sinkhorn change copy");
+      e = hipStreamSynchronize(s);
+      if (e != hipSuccess) return hip_fail(e, "dense sinkhorn change sync");
+      float du, dv;
+      memcpy(&du, &words[0], 4);
+      memcpy(&dv, &words[1], 4);
+      if ((du > dv ? du : dv) < p->threshold) break;
+    }
+  }
+  e = dfl::dense_sinkhorn_finish(a, done, s);
+  if (e != hipSuccess) return hip_fail(e, "dense sinkhorn finish launch");
+  if (p->iters_done) *p->iters_done = done;
+  return 0;
+}
+
+int dfl_dense_sinkhorn_bwd(const dfl_dense_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (!p) return fail("params is NULL");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0) return fail("B, H, N must be positive");
+  if (p->K < 0 || p->K > p->K_max) return fail("K=%d outside [0, K_max=%d]", p->K, p->K_max);
+  if (!p->C || !p->eps || !p->history || !p->dC || !p->dlog_mu || !p->dlog_nu) return fail("required pointer is NULL");
+  const size_t need = dfl_dense_sinkhorn_workspace_size(p->B, p->H, p->N, p->K_max);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  const size_t bhn = (size_t)p->B * p->H * p->N;
+  dfl::DenseSinkBwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.C = p->C; a.eps = p->eps; a.mask = p->mask;
+  const size_t slices = (size_t)(p->K_max + 1) * bhn;
+  a.hist_u = p->history;
+  a.hist_v = p->history + slices;
+  a.hist_r = p->history + 2 * slices;
+  a.hist_c = p->history + 3 * slices;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.K = p->K; a.lam = p->lam;
+  a.grad_u = p->grad_log_u; a.grad_v = p->grad_log_v;
+  a.dC = p->dC; a.dlog_mu = p->dlog_mu; a.dlog_nu = p->dlog_nu;
+  a.dlog_u_init = p->dlog_u_init; a.dlog_v_init = p->dlog_v_init;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  float* vecs = reinterpret_cast<float*>(ws + ((size_t)2 * (p->K_max + 1) * 4 + 255) / 256 * 256);
+  a.gv = vecs;
+  a.avec = vecs + bhn;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (p->K == 0) {  // outputs are the (masked) initial potentials: dC, d log mu, d log nu vanish
+    e = dfl::dense_zero(p->dC, bhn * p->N, s);
+    if (e == hipSuccess) e = dfl::dense_zero(p->dlog_mu, bhn, s);
+    if (e == hipSuccess) e = dfl::dense_zero(p->dlog_nu, bhn, s);
+    if (e != hipSuccess) return hip_fail(e, "dense sinkhorn backward zero launch");
+  }
+  e = dfl::dense_sinkhorn_backward(a, s);
+  if (e != hipSuccess) return hip_fail(e, "dense sinkhorn backward launch");
+  return 0;
+}
+
+size_t dfl_dense_transport_workspace_size(int B, int H, int N, int d) {
+  if (B <= 0 || H <= 0 || N <= 0 || d <= 0) return 0;
+  const size_t bhn = (size_t)B * H * N;
+  return (bhn * d * 4 + 255) / 256 * 256 + (bhn * 3 * 4 + 255) / 256 * 256;
+}
+
+static int check_transport(const dfl_dense_transport_params* p) {
+  if (!p) return fail("params is NULL");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0 || p->d <= 0) return fail("B, H, N, d must be positive");
+  if (p->d > 64) return fail("head dim d=%d > 64 is not supported", p->d);
+  if (!p->V || !p->log_u || !p->log_v || !p->C || !p->eps) return fail("required input is NULL");
+  return 0;
+}
+
+static dfl::DenseTransportArgs transport_args(const dfl_dense_transport_params* p) {
+  dfl::DenseTransportArgs a;
+  memset(&a, 0, sizeof(a));
+  a.V = p->V; a.G = p->G; a.log_u = p->log_u; a.log_v = p->log_v; a.C = p->C; a.eps = p->eps;
+  a.x_res = p->x_res; a.mask = p->mask;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d;
+  a.o = p->o; a.T_norm = p->T_norm; a.x_centroid = p->x_res ? p->x_centroid : nullptr; a.o_avg = p->o_avg;
+  a.grad_o = p->grad_o; a.grad_T = p->grad_T; a.grad_xc = p->grad_xc;
+  a.dV = p->dV; a.dG = p->G ? p->dG : nullptr; a.dlog_u = p->dlog_u; a.dlog_v = p->dlog_v; a.dC = p->dC;
+  a.dx_res = p->x_res ? p->dx_res : nullptr;
+  return a;
+}
+
+int dfl_dense_transport_fwd(const dfl_dense_transport_params* p, void* stream) {
+  if (int rc = check_transport(p)) return rc;
+  if (!p->o || !p->T_norm || !p->o_avg) return fail("o, T_norm and o_avg are required");
+  if (p->x_res && !p->x_centroid) return fail("x_centroid is required with x_res");
+  hipError_t e = dfl::dense_transport_forward(transport_args(p), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dense transport forward launch");
+  return 0;
+}
+
+int dfl_dense_transport_bwd(const dfl_dense_transport_params* p, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  if (int rc = check_transport(p)) return rc;
+  if (!p->T_norm || !p->o_avg || !p->dV || !p->dlog_u || !p->dlog_v || !p->dC)
+    return fail("T_norm, o_avg, dV, dlog_u, dlog_v and dC are required");
+  const size_t need = dfl_dense_transport_workspace_size(p->B, p->H, p->N, p->d);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  dfl::DenseTransportArgs a = transport_args(p);
+  const size_t bhn = (size_t)p->B * p->H * p->N;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  a.goa = reinterpret_cast<float*>(ws);
+  a.dx_part = p->x_res ? reinterpret_cast<float*>(ws + (bhn * p->d * 4 + 255) / 256 * 256) : nullptr;
+  hipError_t e = dfl::dense_transport_backward(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dense transport backward launch");
   return 0;
 }
 

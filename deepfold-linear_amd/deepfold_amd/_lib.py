@@ -105,6 +105,41 @@ class A2TParams(ctypes.Structure):
     ]
 
 
+class DenseSinkhornParams(ctypes.Structure):
+    """Mirror of ``dfl_dense_sinkhorn_params``."""
+
+    _fields_ = [
+        ("C", P), ("log_mu", P), ("log_nu", P), ("eps", P),
+        ("log_u_init", P), ("log_v_init", P), ("mask", P),
+        ("B", I32), ("H", I32), ("N", I32), ("K", I32),
+        ("lam", F32), ("threshold", F32), ("check_every", I32),
+        ("log_u", P), ("log_v", P), ("history", P), ("iters_done", P),
+    ]
+
+
+class DenseSinkhornBwdParams(ctypes.Structure):
+    """Mirror of ``dfl_dense_sinkhorn_bwd_params``."""
+
+    _fields_ = [
+        ("C", P), ("eps", P), ("mask", P), ("history", P),
+        ("B", I32), ("H", I32), ("N", I32), ("K_max", I32), ("K", I32), ("lam", F32),
+        ("grad_log_u", P), ("grad_log_v", P),
+        ("dC", P), ("dlog_mu", P), ("dlog_nu", P), ("dlog_u_init", P), ("dlog_v_init", P),
+    ]
+
+
+class DenseTransportParams(ctypes.Structure):
+    """Mirror of ``dfl_dense_transport_params``."""
+
+    _fields_ = [
+        ("V", P), ("G", P), ("log_u", P), ("log_v", P), ("C", P), ("eps", P), ("x_res", P), ("mask", P),
+        ("B", I32), ("H", I32), ("N", I32), ("d", I32),
+        ("o", P), ("T_norm", P), ("x_centroid", P), ("o_avg", P),
+        ("grad_o", P), ("grad_T", P), ("grad_xc", P),
+        ("dV", P), ("dG", P), ("dlog_u", P), ("dlog_v", P), ("dC", P), ("dx_res", P),
+    ]
+
+
 DFL_ATTN_BIAS_NONE = 0
 DFL_ATTN_BIAS_BINS = 1
 DFL_ATTN_BIAS_DENSE = 2
@@ -125,6 +160,12 @@ SIGNATURES = [
     ("dfl_a2t_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
     ("dfl_a2t_fwd", I32, [ctypes.POINTER(A2TParams), P]),
     ("dfl_a2t_bwd", I32, [ctypes.POINTER(A2TParams), P, ctypes.c_size_t, P]),
+    ("dfl_dense_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
+    ("dfl_dense_sinkhorn_fwd", I32, [ctypes.POINTER(DenseSinkhornParams), P, ctypes.c_size_t, P]),
+    ("dfl_dense_sinkhorn_bwd", I32, [ctypes.POINTER(DenseSinkhornBwdParams), P, ctypes.c_size_t, P]),
+    ("dfl_dense_transport_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
+    ("dfl_dense_transport_fwd", I32, [ctypes.POINTER(DenseTransportParams), P]),
+    ("dfl_dense_transport_bwd", I32, [ctypes.POINTER(DenseTransportParams), P, ctypes.c_size_t, P]),
 ]
 
 

@@ -242,6 +242,101 @@ size_t dfl_a2t_workspace_size(int B, int H, int M, int d);
 int dfl_a2t_fwd(const dfl_a2t_params* p, void* stream);
 int dfl_a2t_bwd(const dfl_a2t_params* p, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Dense, materialised-cost Sinkhorn (src/deepfold/model/sinkhorn.py).  fp32,
+ * contiguous.  The caller allocates every output.
+ *
+ * dfl_dense_sinkhorn_fwd replaces sinkhorn_solve (sinkhorn.py:17-112): up to K
+ * iterations u = kappa (log mu - LSE_j(-C/eps + v + cb)), v = kappa (log nu -
+ * LSE_i(-C/eps + u + rb)) on C (B,H,N,N), masks as -1e9 biases, outputs log_u,
+ * log_v (B,H,N) zero at padded positions.  threshold >= 0 enables the
+ * reference's early stop (L-inf change < threshold, checked every check_every
+ * iterations); each check synchronises `stream`, as the reference's .item() does.
+ * history (4 (K+1) B H N floats) receives the potentials and LSEs of every
+ * iteration for the backward; *iters_done (host memory) the iterations executed.
+ * dfl_dense_sinkhorn_bwd is autograd through those iterations (the reference's
+ * backward): outputs dC (B,H,N,N), dlog_mu, dlog_nu (B,H,N), and optionally the
+ * initial potentials' gradients (NULL = not requested).
+ */
+typedef struct dfl_dense_sinkhorn_params {
+  const float* C;
+  const float* log_mu;
+  const float* log_nu;
+  const float* eps;
+  const float* log_u_init;
+  const float* log_v_init;
+  const float* mask;
+  int B, H, N;
+  int K;
+  float lam;
+  float threshold;
+  int check_every;
+  float* log_u;
+  float* log_v;
+  float* history;
+  int* iters_done;
+} dfl_dense_sinkhorn_params;
+
+typedef struct dfl_dense_sinkhorn_bwd_params {
+  const float* C;
+  const float* eps;
+  const float* mask;
+  const float* history;
+  int B, H, N;
+  int K_max;
+  int K;
+  float lam;
+  const float* grad_log_u;
+  const float* grad_log_v;
+  float* dC;
+  float* dlog_mu;
+  float* dlog_nu;
+  float* dlog_u_init;
+  float* dlog_v_init;
+} dfl_dense_sinkhorn_bwd_params;
+
+size_t dfl_dense_sinkhorn_workspace_size(int B, int H, int N, int K);
+int dfl_dense_sinkhorn_fwd(const dfl_dense_sinkhorn_params* p, void* workspace, size_t workspace_bytes, void* stream);
+int dfl_dense_sinkhorn_bwd(const dfl_dense_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* dfl_dense_transport_fwd replaces compute_transport_output (sinkhorn.py:115-198):
+ * T_norm = exp(ls - max)/(sum + 1e-6) (rows of padded queries zero), O = T_norm V,
+ * o = sigmoid(G) O permuted to (B,N,H*d) (G may be NULL: no gate), x_centroid =
+ * T_norm x_res (x_res may be NULL).  d <= 64.  o_avg (B,H,N,d) is saved for the
+ * backward.  dfl_dense_transport_bwd: gradients of those ops for grad_o, grad_T
+ * (gradient of T_norm, may be NULL) and grad_xc (may be NULL): dV, dG (NULL if no
+ * gate), dlog_u, dlog_v, dC and dx_res (NULL if no x_res). */
+typedef struct dfl_dense_transport_params {
+  const float* V;
+  const float* G;
+  const float* log_u;
+  const float* log_v;
+  const float* C;
+  const float* eps;
+  const float* x_res;
+  const float* mask;
+  int B, H, N, d;
+  float* o;
+  float* T_norm;
+  float* x_centroid;
+  float* o_avg;
+  const float* grad_o;
+  const float* grad_T;
+  const float* grad_xc;
+  float* dV;
+  float* dG;
+  float* dlog_u;
+  float* dlog_v;
+  float* dC;
+  float* dx_res;
+} dfl_dense_transport_params;
+
+size_t dfl_dense_transport_workspace_size(int B, int H, int N, int d);
+int dfl_dense_transport_fwd(const dfl_dense_transport_params* p, void* stream);
+int dfl_dense_transport_bwd(const dfl_dense_transport_params* p, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

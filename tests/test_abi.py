@@ -81,7 +81,10 @@ def test_struct_layout_matches_c(lib_path):
     mirrors = {"dfl_sinkhorn_fwd_params": _lib.SinkhornFwdParams,
                "dfl_sinkhorn_bwd_params": _lib.SinkhornBwdParams,
                "dfl_attn_params": _lib.AttnParams,
-               "dfl_a2t_params": _lib.A2TParams}
+               "dfl_a2t_params": _lib.A2TParams,
+               "dfl_dense_sinkhorn_params": _lib.DenseSinkhornParams,
+               "dfl_dense_sinkhorn_bwd_params": _lib.DenseSinkhornBwdParams,
+               "dfl_dense_transport_params": _lib.DenseTransportParams}
     assert set(mirrors) == set(structs)
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for sname, fields in structs.items():
@@ -108,8 +111,9 @@ def test_struct_layout_matches_c(lib_path):
 
 def test_ops_refuse_cpu_tensors():
     import torch
-    from deepfold_amd import (atom_to_token_attn, conjugate_gradient, flash_atom_attn, flash_diffusion_attn,
-                              flash_sinkhorn, flash_sinkhorn_attn, token_to_atom_attn)
+    from deepfold_amd import (atom_to_token_attn, compute_transport_output, conjugate_gradient, flash_atom_attn,
+                              flash_diffusion_attn, flash_sinkhorn, flash_sinkhorn_attn, sinkhorn_solve,
+                              token_to_atom_attn)
 
     B, H, N, d = 1, 2, 8, 4
     q = torch.randn(B, H, N, d)
@@ -124,7 +128,11 @@ def test_ops_refuse_cpu_tensors():
                                             torch.ones(B, N, dtype=torch.int32)),
                  lambda: flash_sinkhorn(q, q, q, torch.zeros(B, N, 3), torch.zeros(H, 68), None, torch.ones(H),
                                         torch.zeros(H), torch.zeros(B, H, N), torch.zeros(B, H, N)),
-                 lambda: conjugate_gradient(lambda v: v, torch.ones(4))):
+                 lambda: conjugate_gradient(lambda v: v, torch.ones(4)),
+                 lambda: sinkhorn_solve(torch.zeros(B, H, N, N), torch.zeros(B, H, N), torch.zeros(B, H, N),
+                                        torch.ones(H)),
+                 lambda: compute_transport_output(q, q, torch.zeros(B, H, N), torch.zeros(B, H, N),
+                                                  torch.zeros(B, H, N, N), torch.ones(H))):
         with pytest.raises(RuntimeError, match="GPU"):
             call()
 

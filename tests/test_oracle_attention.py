@@ -20,7 +20,14 @@ import torch
 
 from oracle import attention as ref
 
-torch.set_default_dtype(torch.float64)
+
+@pytest.fixture(autouse=True, scope="module")
+def _float64_default():
+    """float64 for this module's tensors only; the dtype is restored for the other modules."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def rnd(*shape, seed=0, scale=1.0):
