@@ -174,7 +174,7 @@ AttnWs attn_ws_layout(int B, int H, int Mq, int Nk) {
   w.dcoef = w.do_w + r256(rows * 64 * 4);
   w.kv_part = w.dcoef + r256(rows * 4);
   w.dpw_part = w.kv_part + (qs > 1 ? r256((size_t)qs * B * H * Nk * 2 * 64 * 4) : 0);
-  w.total = w.dpw_part + r256((size_t)B * H * ((Mq + 63) / 64) * 68 * 4);
+  w.total = w.dpw_part + r256((size_t)B * H * ((Mq + 31) / 32) * 68 * 4);  // per 32- or 64-query block
   return w;
 }
 
