@@ -177,17 +177,22 @@ template <int DP> struct Mfma<float, DP> {
 
 // ---------------------------------------------------------------------------
 // Lane reductions across the 4 lane groups (l/16) of a wave that hold the same
-// accumulator column.
-__device__ __forceinline__ float sum_groups(float x) {
-  x += __shfl_xor(x, 16, WAVE);
-  x += __shfl_xor(x, 32, WAVE);
-  return x;
+// accumulator column.  gfx950's v_permlane16/32_swap exchange 16-lane rows inside
+// the VALU: with x as both operands, the two results hold x[l] and x[l ^ 16]
+// (resp. x[l ^ 32]) in some order, so their sum / max is the pair reduction with
+// no LDS round trip (a __shfl_xor compiles to ds_bpermute).
+__device__ __forceinline__ float xor16_pair(float x, bool mx) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return mx ? fmaxf(a, b) : a + b;
 }
-__device__ __forceinline__ float max_groups(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16, WAVE));
-  x = fmaxf(x, __shfl_xor(x, 32, WAVE));
-  return x;
+__device__ __forceinline__ float xor32_pair(float x, bool mx) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return mx ? fmaxf(a, b) : a + b;
 }
+__device__ __forceinline__ float sum_groups(float x) { return xor32_pair(xor16_pair(x, false), false); }
+__device__ __forceinline__ float max_groups(float x) { return xor32_pair(xor16_pair(x, true), true); }
 
 // Unsigned maximum over the 64 lanes of a wave; every lane must be active.
 // Four DPP steps reduce each 16-lane row, four readlanes combine the rows.  (An

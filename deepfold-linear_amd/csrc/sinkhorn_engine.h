@@ -200,8 +200,8 @@ __device__ __forceinline__ bool gather_potential(const uint64_t* buf, int n, uin
 //                   every exponent x - shift stays within fp32 range).
 // lse2[q] receives the result for local resident row q in [0, nr*16).
 // If publish != null, the threads that finish row q also call publish(q, lse2_q)
-// before the closing barrier.  *s_reset (if non-null) is zeroed between the two
-// barriers of each chunk.  Called by the whole block.
+// before the closing barrier.  *s_reset (if non-null) is zeroed before the first
+// barrier of each chunk.  Called by the whole block.
 template <int NT, typename T, int DP, bool GENERAL, bool TRANS, bool ONLINE, typename Pub>
 __device__ __forceinline__ void lse_sweep(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
                           const float* __restrict__ w2, int n_str_tiles, int rt0, int nr, float sc,
@@ -299,8 +299,10 @@ __device__ __forceinline__ void lse_sweep(const T* __restrict__ res_lds, const T
         }
       }
     }
-    __syncthreads();
+    // the change word of the coming gather is cleared before the barrier, so no
+    // wave's post-barrier atomic can precede the clear
     if (s_reset && threadIdx.x == 0) *s_reset = 0u;
+    __syncthreads();
     if ((int)threadIdx.x < nc * 16) {
       const int q = threadIdx.x;
       const int r = q >> 4, l = q & 15;
