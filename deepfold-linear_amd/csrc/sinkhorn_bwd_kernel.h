@@ -160,6 +160,30 @@ __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np
   return true;
 }
 
+// Resident-tile assignment of the heavy passes.  With nr <= BWD_NW resident tiles,
+// each tile gets wpt = BWD_NW / nr waves that take interleaved 32-row pairs of
+// every streamed chunk (all waves busy); the part > 0 waves hand their partial
+// sums to part 0 through LDS.  With more tiles, waves own whole tiles (up to
+// MAXT each) as before.
+struct PassSplit {
+  bool split;
+  int wpt, part;
+  bool active;  // this wave has a tile in split mode
+  __device__ __forceinline__ PassSplit(int nr, int wave) {
+    split = nr <= BWD_NW;
+    wpt = split ? BWD_NW / nr : 1;
+    part = split ? wave / nr : 0;
+    active = !split || part < wpt;
+  }
+  // resident tile of slot k in batch rt0 (nr if none)
+  __device__ __forceinline__ int tile(int rt0, int k, int nr, int wave) const {
+    if (split) return (k == 0 && active) ? wave % nr : nr;
+    return rt0 + wave + BWD_NW * k;
+  }
+};
+// Floats per lane of the partial sums handed over in split mode.
+template <int DP> constexpr int pass_partial_floats() { return 4 + 4 * (DP / 16); }
+
 __device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
 constexpr int STAGE_BATCH = 4;  // 16-byte loads each thread keeps in flight while staging
@@ -307,7 +331,8 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   // ---- LDS carve-up (must match sinkhorn_bwd_lds_bytes)
   unsigned char* valid = smem;
   const int res_rows = STREAM ? loc : Np;  // rows of Q and K kept in LDS by the solve
-  const size_t region = max((size_t)2 * res_rows * DP * sizeof(T), (size_t)4 * CH * DP * sizeof(T));
+  const size_t region = max(max((size_t)2 * res_rows * DP * sizeof(T), (size_t)4 * CH * DP * sizeof(T)),
+                            (size_t)BWD_NW * WAVE * pass_partial_floats<DP>() * 4);
   T* R0 = reinterpret_cast<T*>(smem + ((Np + 15) / 16) * 16);
   float* after_region = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(R0) + region);
   float* fv = STREAM ? a.vec_ws + wg_id * (size_t)BWD_STREAM_VECS * Np : after_region;
@@ -426,16 +451,18 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     float* a2 = ct;                  // (u - logZ) in log2, rows (ct is free until the solve)
     for (int i = threadIdx.x; i < Np; i += BWD_NT) a2[i] = (i < n && valid[i]) ? uu[i] - lz[i] : NEG_BIG;
     __syncthreads();
-    for (int rt0 = 0; rt0 < nr; rt0 += bwd_maxt<DP>() * BWD_NW) {
-      // wave w owns resident tiles rt0 + w + BWD_NW*k, k < MAXT
+    const PassSplit ps(nr, wave);
+    for (int rt0 = 0; rt0 < nr; rt0 += ps.split ? nr : bwd_maxt<DP>() * BWD_NW) {
       constexpr int MAXT = bwd_maxt<DP>();
       typename M::Frag kf[MAXT], vf[MAXT];
       f32x4 cinit[MAXT], dvacc[MAXT][NC];
       float gva[MAXT], dxa[MAXT][3], xj[MAXT][3];
+      int tl[MAXT];
       int ntile = 0;
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
-        const int rt = rt0 + wave + BWD_NW * k;
+        const int rt = ps.tile(rt0, k, nr, wave);
+        tl[k] = rt;
         gva[k] = 0.f;
         dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
 #pragma unroll
@@ -458,7 +485,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
         stage_chunk_tt<T, DP>(gOT, gOt, Np, c0, CH);
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
-        for (int pr = 0; pr < npair; ++pr) {
+        for (int pr = ps.part; pr < npair; pr += ps.wpt) {
           typename M::Frag qa[2], ga[2], gl[2];
           f32x4 wa[2], Dq[2];
 #pragma unroll
@@ -473,7 +500,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int k = 0; k < MAXT; ++k) {
             if (k < ntile) {
-              const int j = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
+              const int j = (t0 + tl[k]) * 16 + (lane & 15);
               f32x4 tv[2];
 #pragma unroll
               for (int hf = 0; hf < 2; ++hf) {
@@ -507,11 +534,37 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
           }
         }
       }
+      // split mode: part > 0 waves hand their partials to part 0 (staging buffer is free)
+      if (ps.split && ps.wpt > 1) {
+        constexpr int PF = pass_partial_floats<DP>();
+        float* pp = reinterpret_cast<float*>(R0);
+        __syncthreads();
+        if (ntile > 0 && ps.part > 0) {
+          float* dst = pp + ((size_t)wave * WAVE + lane) * PF;
+          dst[0] = gva[0]; dst[1] = dxa[0][0]; dst[2] = dxa[0][1]; dst[3] = dxa[0][2];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) *reinterpret_cast<f32x4*>(dst + 4 + 4 * c) = dvacc[0][c];
+        }
+        __syncthreads();
+        if (ntile > 0 && ps.part == 0) {
+          for (int q = 1; q < ps.wpt; ++q) {
+            const float* src = pp + ((size_t)(wave + q * nr) * WAVE + lane) * PF;
+            gva[0] += src[0]; dxa[0][0] += src[1]; dxa[0][1] += src[2]; dxa[0][2] += src[3];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+              const f32x4 o = *reinterpret_cast<const f32x4*>(src + 4 + 4 * c);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) dvacc[0][c][r] += o[r];
+            }
+          }
+        }
+        if (ps.part > 0) ntile = 0;
+      }
       // epilogue for this batch of resident tiles
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
         if (k < ntile) {
-          const int tile = t0 + rt0 + wave + BWD_NW * k;
+          const int tile = t0 + tl[k];
           const int jl = tile * 16 + (lane & 15);
           const float gsum = sum_groups(gva[k]);
           const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
@@ -698,15 +751,18 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* Kc = R0;
     T* Vc = Kc + (size_t)CH * DP;
     T* KT = Vc + (size_t)CH * DP;  // [DP][CH]
-    for (int rt0 = 0; rt0 < nr; rt0 += bwd_maxt<DP>() * BWD_NW) {
+    const PassSplit ps(nr, wave);
+    for (int rt0 = 0; rt0 < nr; rt0 += ps.split ? nr : bwd_maxt<DP>() * BWD_NW) {
       constexpr int MAXT = bwd_maxt<DP>();
       typename M::Frag qf[MAXT], gf[MAXT], gfl[MAXT];
       f32x4 cinit[MAXT], dqacc[MAXT][NC];
       float lzi[MAXT], zui[MAXT], Di[MAXT], xi[MAXT][3], dci[MAXT][3], dxa[MAXT][3];
+      int tl[MAXT];
       int ntile = 0;
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
-        const int rt = rt0 + wave + BWD_NW * k;
+        const int rt = ps.tile(rt0, k, nr, wave);
+        tl[k] = rt;
         dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) dqacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -732,7 +788,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
         stage_chunk_t<T, DP>(KT, Kg, a.sn, c0, CH, n, d);
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
-        for (int pr = 0; pr < npair; ++pr) {
+        for (int pr = ps.part; pr < npair; pr += ps.wpt) {
           typename M::Frag ka[2], va[2];
           f32x4 wv[2], wl[2], wz[2];
 #pragma unroll
@@ -747,7 +803,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int k = 0; k < MAXT; ++k) {
             if (k < ntile) {
-              const int i = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
+              const int i = (t0 + tl[k]) * 16 + (lane & 15);
               f32x4 dcv[2];
 #pragma unroll
               for (int hf = 0; hf < 2; ++hf) {
@@ -797,10 +853,35 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
           }
         }
       }
+      if (ps.split && ps.wpt > 1) {
+        constexpr int PF = pass_partial_floats<DP>();
+        float* pp = reinterpret_cast<float*>(R0);
+        __syncthreads();
+        if (ntile > 0 && ps.part > 0) {
+          float* dst = pp + ((size_t)wave * WAVE + lane) * PF;
+          dst[1] = dxa[0][0]; dst[2] = dxa[0][1]; dst[3] = dxa[0][2];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) *reinterpret_cast<f32x4*>(dst + 4 + 4 * c) = dqacc[0][c];
+        }
+        __syncthreads();
+        if (ntile > 0 && ps.part == 0) {
+          for (int q = 1; q < ps.wpt; ++q) {
+            const float* src = pp + ((size_t)(wave + q * nr) * WAVE + lane) * PF;
+            dxa[0][0] += src[1]; dxa[0][1] += src[2]; dxa[0][2] += src[3];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+              const f32x4 o = *reinterpret_cast<const f32x4*>(src + 4 + 4 * c);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) dqacc[0][c][r] += o[r];
+            }
+          }
+        }
+        if (ps.part > 0) ntile = 0;
+      }
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
         if (k < ntile) {
-          const int tile = t0 + rt0 + wave + BWD_NW * k;
+          const int tile = t0 + tl[k];
           const int il = tile * 16 + (lane & 15);
           const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
           if (lane < 16 && il < n) {
@@ -834,15 +915,18 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* QT = gOl + (size_t)CH * DP;   // [DP][CH]
     float* a2s = a2;
     float* zus = zu;
-    for (int rt0 = 0; rt0 < nr; rt0 += bwd_maxt<DP>() * BWD_NW) {
+    const PassSplit ps(nr, wave);
+    for (int rt0 = 0; rt0 < nr; rt0 += ps.split ? nr : bwd_maxt<DP>() * BWD_NW) {
       constexpr int MAXT = bwd_maxt<DP>();
       typename M::Frag kf[MAXT], vf[MAXT];
       f32x4 cinit[MAXT], dkacc[MAXT][NC];
       float lcj[MAXT], zvj[MAXT], xj[MAXT][3], dxa[MAXT][3];
+      int tl[MAXT];
       int ntile = 0;
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
-        const int rt = rt0 + wave + BWD_NW * k;
+        const int rt = ps.tile(rt0, k, nr, wave);
+        tl[k] = rt;
         dxa[k][0] = dxa[k][1] = dxa[k][2] = 0.f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) dkacc[k][c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -866,7 +950,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
         stage_chunk_t<T, DP>(QT, Qg, a.sn, c0, CH, n, d);
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
-        for (int pr = 0; pr < npair; ++pr) {
+        for (int pr = ps.part; pr < npair; pr += ps.wpt) {
           typename M::Frag qa[2], ga[2], gl[2];
           f32x4 wa[2], wlz[2], wzu[2], wD[2];
 #pragma unroll
@@ -883,7 +967,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
           for (int k = 0; k < MAXT; ++k) {
             if (k < ntile) {
-              const int j = (t0 + rt0 + wave + BWD_NW * k) * 16 + (lane & 15);
+              const int j = (t0 + tl[k]) * 16 + (lane & 15);
               const bool jok = j < n && valid[j];
               f32x4 dcv[2];
 #pragma unroll
@@ -925,10 +1009,35 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
           }
         }
       }
+      if (ps.split && ps.wpt > 1) {
+        constexpr int PF = pass_partial_floats<DP>();
+        float* pp = reinterpret_cast<float*>(R0);
+        __syncthreads();
+        if (ntile > 0 && ps.part > 0) {
+          float* dst = pp + ((size_t)wave * WAVE + lane) * PF;
+          dst[1] = dxa[0][0]; dst[2] = dxa[0][1]; dst[3] = dxa[0][2];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) *reinterpret_cast<f32x4*>(dst + 4 + 4 * c) = dkacc[0][c];
+        }
+        __syncthreads();
+        if (ntile > 0 && ps.part == 0) {
+          for (int q = 1; q < ps.wpt; ++q) {
+            const float* src = pp + ((size_t)(wave + q * nr) * WAVE + lane) * PF;
+            dxa[0][0] += src[1]; dxa[0][1] += src[2]; dxa[0][2] += src[3];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+              const f32x4 o = *reinterpret_cast<const f32x4*>(src + 4 + 4 * c);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) dkacc[0][c][r] += o[r];
+            }
+          }
+        }
+        if (ps.part > 0) ntile = 0;
+      }
 #pragma unroll
       for (int k = 0; k < MAXT; ++k) {
         if (k < ntile) {
-          const int tile = t0 + rt0 + wave + BWD_NW * k;
+          const int tile = t0 + tl[k];
           const int jl = tile * 16 + (lane & 15);
           const float d0 = sum_groups(dxa[k][0]), d1 = sum_groups(dxa[k][1]), d2 = sum_groups(dxa[k][2]);
           if (lane < 16 && jl < n) {
@@ -980,7 +1089,8 @@ inline size_t sinkhorn_bwd_lds_bytes_t(int N, int DP, int elem, int G, int CH, b
   const size_t loc = bwd_local_rows(N, G);
   const size_t res_rows = stream ? loc : Np;
   size_t bytes = ((Np + 15) / 16) * 16;                                   // valid
-  bytes += std::max(2 * res_rows * DP * elem, (size_t)4 * CH * DP * elem);  // operand region
+  bytes += std::max(std::max(2 * res_rows * DP * elem, (size_t)4 * CH * DP * elem),  // operand region, also the
+                    (size_t)BWD_NW * WAVE * (4 + 4 * (DP / 16)) * 4);           // split-pass partials
   if (!stream) bytes += (size_t)BWD_STREAM_VECS * Np * 4;                 // vectors, xs, dxc
   bytes += (2 * loc + 3 * loc + 68) * 4;                                  // lres, lout, dxs, dpw
   bytes += (size_t)(stream ? BWD_STREAM_SCRATCH : BWD_SCRATCH) * 4;
