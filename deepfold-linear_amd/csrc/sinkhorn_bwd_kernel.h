@@ -227,7 +227,9 @@ __device__ __forceinline__ void stage_chunk(T* dst, const T* __restrict__ src, l
   }
 }
 
-// Transposed: dst[DP][CH] with dst[c][row] = src[r0 + row][c].
+// Transposed: dst[DP][CH + VE] with dst[c][row] = src[r0 + row][c].  The 16-byte
+// row padding keeps the 16 lanes that read one MFMA operand column run (rows c0..c0+15)
+// in different LDS banks; an unpadded 256-row stride put all of them in one bank.
 template <typename T, int DP>
 __device__ __forceinline__ void stage_chunk_t(T* dst, const T* __restrict__ src, long long sn, int r0, int CH, int n,
                                               int d) {
@@ -253,7 +255,7 @@ __device__ __forceinline__ void stage_chunk_t(T* dst, const T* __restrict__ src,
           T v[VE];
           __builtin_memcpy(v, &w[u], 16);
 #pragma unroll
-          for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * CH + row] = v[e];
+          for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * (CH + VE) + row] = v[e];
         }
       }
     }
@@ -264,11 +266,11 @@ __device__ __forceinline__ void stage_chunk_t(T* dst, const T* __restrict__ src,
     const int i = r0 + row;
     T v = from_f32<T>(0.f);
     if (i < n && col < d) v = src[(size_t)i * sn + col];
-    dst[e] = v;
+    dst[(size_t)col * (CH + VE) + row] = v;
   }
 }
 
-// Columns [r0, r0 + CH) of a prepared transposed operand src[DP][Np] into dst[DP][CH]
+// Columns [r0, r0 + CH) of a prepared transposed operand src[DP][Np] into dst[DP][CH + VE]
 // (Np and r0 are multiples of 32 and CH of 32, so rows are 16-byte aligned).
 template <typename T, int DP>
 __device__ __forceinline__ void stage_chunk_tt(T* dst, const T* __restrict__ src, int Np, int r0, int CH) {
@@ -289,8 +291,82 @@ __device__ __forceinline__ void stage_chunk_tt(T* dst, const T* __restrict__ src
     for (int u = 0; u < STAGE_BATCH; ++u) {
       const int c = c0 + u * BWD_NT;
       const int k = c / per, e = c - k * per;
-      if (c < total) *reinterpret_cast<i32x4*>(dst + (size_t)k * CH + e * VE) = v[u];
+      if (c < total) *reinterpret_cast<i32x4*>(dst + (size_t)k * (CH + VE) + e * VE) = v[u];
     }
+  }
+}
+
+// Several operands of one chunk staged together, with the loads of every job in
+// flight at once (one L2 round trip per chunk instead of one per operand).
+//   kind 0: rows [r0, r0 + CH) of src (row stride sn, rows < n, columns < d) -> dst[CH][DP]
+//   kind 1: the same rows transposed -> dst[DP][CH + VE]
+//   kind 2: columns [r0, r0 + CH) of a prepared transposed src[DP][n] -> dst[DP][CH + VE]
+// Jobs without 16-byte aligned full rows fall back to the element-wise stagers.
+struct StageJob {
+  const void* src;
+  void* dst;
+  long long sn;
+  int n, d, kind;
+};
+
+template <typename T, int DP, int NJ>
+__device__ __forceinline__ void stage_jobs(const StageJob (&J)[NJ], int r0, int CH) {
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int CPR = DP / VE;
+  constexpr int KPT = 2;  // blocks per thread and job in flight
+  typedef __attribute__((__vector_size__(16))) int i32x4;
+  bool vec[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const T* src = static_cast<const T*>(J[j].src);
+    vec[j] = J[j].kind == 2 ||
+             (J[j].d == DP && J[j].sn % VE == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0);
+    if (!vec[j]) {
+      if (J[j].kind == 0) stage_chunk<T, DP>(static_cast<T*>(J[j].dst), src, J[j].sn, r0, CH, J[j].n, J[j].d);
+      else stage_chunk_t<T, DP>(static_cast<T*>(J[j].dst), src, J[j].sn, r0, CH, J[j].n, J[j].d);
+    }
+  }
+  const int total = CH * CPR;  // 16-byte blocks per job (kind 2: DP rows of CH / VE)
+  for (int c0 = threadIdx.x; c0 < total; c0 += KPT * BWD_NT) {
+    i32x4 v[NJ][KPT];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) {
+        const int c = c0 + u * BWD_NT;
+        const T* src = static_cast<const T*>(J[j].src);
+        v[j][u] = i32x4{0, 0, 0, 0};
+        if (!vec[j] || c >= total) continue;
+        if (J[j].kind == 2) {
+          const int per = CH / VE, k = c / per, e = c - k * per;
+          if (r0 + e * VE < J[j].n) v[j][u] = *reinterpret_cast<const i32x4*>(src + (size_t)k * J[j].n + r0 + e * VE);
+        } else {
+          const int row = J[j].kind == 0 ? c / CPR : c % CH;
+          const int k = J[j].kind == 0 ? c - row * CPR : c / CH;
+          if (r0 + row < J[j].n) v[j][u] = *reinterpret_cast<const i32x4*>(src + (size_t)(r0 + row) * J[j].sn + k * VE);
+        }
+      }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) {
+        const int c = c0 + u * BWD_NT;
+        if (!vec[j] || c >= total) continue;
+        T* dst = static_cast<T*>(J[j].dst);
+        if (J[j].kind == 2) {
+          const int per = CH / VE, k = c / per, e = c - k * per;
+          *reinterpret_cast<i32x4*>(dst + (size_t)k * (CH + VE) + e * VE) = v[j][u];
+        } else if (J[j].kind == 0) {
+          const int row = c / CPR, k = c - row * CPR;
+          *reinterpret_cast<i32x4*>(dst + (size_t)row * DP + k * VE) = v[j][u];
+        } else {
+          const int row = c % CH, k = c / CH;
+          T e8[VE];
+          __builtin_memcpy(e8, &v[j][u], 16);
+#pragma unroll
+          for (int e = 0; e < VE; ++e) dst[(size_t)(k * VE + e) * (CH + VE) + row] = e8[e];
+        }
+      }
   }
 }
 
@@ -318,6 +394,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const int N = a.N, d = a.d;
   const int Np = ((N + 31) / 32) * 32;
   const int CH = a.ch;
+  constexpr int TPAD = 16 / (int)sizeof(T);  // row padding of the transposed chunk buffers
   const int loc = bwd_local_rows(N, a.G);
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
@@ -331,7 +408,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   // ---- LDS carve-up (must match sinkhorn_bwd_lds_bytes)
   unsigned char* valid = smem;
   const int res_rows = STREAM ? loc : Np;  // rows of Q and K kept in LDS by the solve
-  const size_t region = max(max((size_t)2 * res_rows * DP * sizeof(T), (size_t)4 * CH * DP * sizeof(T)),
+  const size_t region = max(max((size_t)2 * res_rows * DP * sizeof(T), (size_t)(4 * CH + TPAD) * DP * sizeof(T)),
                             (size_t)BWD_NW * WAVE * pass_partial_floats<DP>() * 4);
   T* R0 = reinterpret_cast<T*>(smem + ((Np + 15) / 16) * 16);
   float* after_region = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(R0) + region);
@@ -447,7 +524,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* Qc = R0;
     T* gOc = Qc + (size_t)CH * DP;
     T* gOl = gOc + (size_t)CH * DP;  // low halves of gO (bf16 only)
-    T* gOT = gOl + (size_t)CH * DP;  // [DP][CH]
+    T* gOT = gOl + (size_t)CH * DP;  // [DP][CH + TPAD]
     float* a2 = ct;                  // (u - logZ) in log2, rows (ct is free until the solve)
     for (int i = threadIdx.x; i < Np; i += BWD_NT) a2[i] = (i < n && valid[i]) ? uu[i] - lz[i] : NEG_BIG;
     __syncthreads();
@@ -479,10 +556,14 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       }
       for (int c0 = 0; c0 < n; c0 += CH) {
         __syncthreads();
-        stage_chunk<T, DP>(Qc, Qg, a.sn, c0, CH, n, d);
-        stage_chunk<T, DP>(gOc, gOh, DP, c0, CH, Np, DP);
-        if (M::SPLIT) stage_chunk<T, DP>(gOl, gOlo, DP, c0, CH, Np, DP);
-        stage_chunk_tt<T, DP>(gOT, gOt, Np, c0, CH);
+        if constexpr (M::SPLIT) {
+          const StageJob jobs[4] = {{Qg, Qc, a.sn, n, d, 0}, {gOh, gOc, DP, Np, DP, 0}, {gOlo, gOl, DP, Np, DP, 0},
+                                    {gOt, gOT, Np, Np, DP, 2}};
+          stage_jobs<T, DP, 4>(jobs, c0, CH);
+        } else {
+          const StageJob jobs[3] = {{Qg, Qc, a.sn, n, d, 0}, {gOh, gOc, DP, Np, DP, 0}, {gOt, gOT, Np, Np, DP, 2}};
+          stage_jobs<T, DP, 3>(jobs, c0, CH);
+        }
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
         for (int pr = ps.part; pr < npair; pr += ps.wpt) {
@@ -528,7 +609,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
               }
 #pragma unroll
               for (int c = 0; c < NC; ++c)
-                dvacc[k][c] = M::pv(tv[0], tv[1], gOT + (size_t)(c * 16 + (lane & 15)) * CH + pr * 32, lane,
+                dvacc[k][c] = M::pv(tv[0], tv[1], gOT + (size_t)(c * 16 + (lane & 15)) * (CH + TPAD) + pr * 32, lane,
                                     dvacc[k][c]);
             }
           }
@@ -750,7 +831,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   {
     T* Kc = R0;
     T* Vc = Kc + (size_t)CH * DP;
-    T* KT = Vc + (size_t)CH * DP;  // [DP][CH]
+    T* KT = Vc + (size_t)CH * DP;  // [DP][CH + TPAD]
     const PassSplit ps(nr, wave);
     for (int rt0 = 0; rt0 < nr; rt0 += ps.split ? nr : bwd_maxt<DP>() * BWD_NW) {
       constexpr int MAXT = bwd_maxt<DP>();
@@ -783,9 +864,10 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       }
       for (int c0 = 0; c0 < n; c0 += CH) {
         __syncthreads();
-        stage_chunk<T, DP>(Kc, Kg, a.sn, c0, CH, n, d);
-        stage_chunk<T, DP>(Vc, Vg, a.sn, c0, CH, n, d);
-        stage_chunk_t<T, DP>(KT, Kg, a.sn, c0, CH, n, d);
+        {
+          const StageJob jobs[3] = {{Kg, Kc, a.sn, n, d, 0}, {Vg, Vc, a.sn, n, d, 0}, {Kg, KT, a.sn, n, d, 1}};
+          stage_jobs<T, DP, 3>(jobs, c0, CH);
+        }
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
         for (int pr = ps.part; pr < npair; pr += ps.wpt) {
@@ -847,7 +929,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
               }
 #pragma unroll
               for (int c = 0; c < NC; ++c)
-                dqacc[k][c] = M::pv(dcv[0], dcv[1], KT + (size_t)(c * 16 + (lane & 15)) * CH + pr * 32, lane,
+                dqacc[k][c] = M::pv(dcv[0], dcv[1], KT + (size_t)(c * 16 + (lane & 15)) * (CH + TPAD) + pr * 32, lane,
                                     dqacc[k][c]);
             }
           }
@@ -912,7 +994,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     T* Qc = R0;
     T* gOc = Qc + (size_t)CH * DP;
     T* gOl = gOc + (size_t)CH * DP;  // low halves of gO (bf16 only)
-    T* QT = gOl + (size_t)CH * DP;   // [DP][CH]
+    T* QT = gOl + (size_t)CH * DP;   // [DP][CH + TPAD]
     float* a2s = a2;
     float* zus = zu;
     const PassSplit ps(nr, wave);
@@ -944,10 +1026,14 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       }
       for (int c0 = 0; c0 < n; c0 += CH) {
         __syncthreads();
-        stage_chunk<T, DP>(Qc, Qg, a.sn, c0, CH, n, d);
-        stage_chunk<T, DP>(gOc, gOh, DP, c0, CH, Np, DP);
-        if (M::SPLIT) stage_chunk<T, DP>(gOl, gOlo, DP, c0, CH, Np, DP);
-        stage_chunk_t<T, DP>(QT, Qg, a.sn, c0, CH, n, d);
+        if constexpr (M::SPLIT) {
+          const StageJob jobs[4] = {{Qg, Qc, a.sn, n, d, 0}, {gOh, gOc, DP, Np, DP, 0}, {gOlo, gOl, DP, Np, DP, 0},
+                                    {Qg, QT, a.sn, n, d, 1}};
+          stage_jobs<T, DP, 4>(jobs, c0, CH);
+        } else {
+          const StageJob jobs[3] = {{Qg, Qc, a.sn, n, d, 0}, {gOh, gOc, DP, Np, DP, 0}, {Qg, QT, a.sn, n, d, 1}};
+          stage_jobs<T, DP, 3>(jobs, c0, CH);
+        }
         __syncthreads();
         const int npair = (min(CH, n - c0) + 31) / 32;
         for (int pr = ps.part; pr < npair; pr += ps.wpt) {
@@ -1003,7 +1089,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
               }
 #pragma unroll
               for (int c = 0; c < NC; ++c)
-                dkacc[k][c] = M::pv(dcv[0], dcv[1], QT + (size_t)(c * 16 + (lane & 15)) * CH + pr * 32, lane,
+                dkacc[k][c] = M::pv(dcv[0], dcv[1], QT + (size_t)(c * 16 + (lane & 15)) * (CH + TPAD) + pr * 32, lane,
                                     dkacc[k][c]);
             }
           }
@@ -1089,8 +1175,10 @@ inline size_t sinkhorn_bwd_lds_bytes_t(int N, int DP, int elem, int G, int CH, b
   const size_t loc = bwd_local_rows(N, G);
   const size_t res_rows = stream ? loc : Np;
   size_t bytes = ((Np + 15) / 16) * 16;                                   // valid
-  bytes += std::max(std::max(2 * res_rows * DP * elem, (size_t)4 * CH * DP * elem),  // operand region, also the
-                    (size_t)BWD_NW * WAVE * (4 + 4 * (DP / 16)) * 4);           // split-pass partials
+  // operand region: Q and K for the solve, or four chunk buffers (the transposed one
+  // padded by 16 bytes a row), or the split-pass partials
+  bytes += std::max(std::max(2 * res_rows * DP * elem, (size_t)(4 * CH + 16 / elem) * DP * elem),
+                    (size_t)BWD_NW * WAVE * (4 + 4 * (DP / 16)) * 4);
   if (!stream) bytes += (size_t)BWD_STREAM_VECS * Np * 4;                 // vectors, xs, dxc
   bytes += (2 * loc + 3 * loc + 68) * 4;                                  // lres, lout, dxs, dpw
   bytes += (size_t)(stream ? BWD_STREAM_SCRATCH : BWD_SCRATCH) * 4;
