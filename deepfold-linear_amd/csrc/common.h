@@ -192,6 +192,15 @@ __device__ __forceinline__ float xor32_pair(float x, bool mx) {
   return mx ? fmaxf(a, b) : a + b;
 }
 __device__ __forceinline__ float sum_groups(float x) { return xor32_pair(xor16_pair(x, false), false); }
+// Sum over the 64 lanes of a wave, in every lane (DPP within 16-lane rows, then the
+// row swaps); a fixed order, so equal inputs give bit-equal sums in every wave.
+__device__ __forceinline__ float wave_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false));  // row_half_mirror
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, false));  // row_mirror
+  return sum_groups(x);
+}
 __device__ __forceinline__ float max_groups(float x) { return xor32_pair(xor16_pair(x, true), true); }
 
 // Unsigned maximum over the 64 lanes of a wave; every lane must be active.
@@ -232,48 +241,6 @@ __device__ __forceinline__ bool error_raised(const uint32_t* err, uint32_t salt)
 __device__ __forceinline__ void xch_put(uint64_t* word, float v, uint32_t tag) {
   const uint64_t w = ((uint64_t)__float_as_uint(v) << 32) | (uint64_t)tag;
   __hip_atomic_store(word, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// All threads of the block cooperatively wait for words [0, n) of `buf` to carry
-// `tag`, writing value * scale into dst[] (LDS).  Returns false (uniformly across
-// the block) if the error flag is raised or the spin limit is hit.
-template <int NT>
-__device__ __forceinline__ bool xch_gather(const uint64_t* buf, int n, uint32_t tag, float* dst, float scale,
-                           uint32_t* err, int* s_flag) {
-  const uint32_t salt = tag >> 12;
-  const int t = threadIdx.x;
-  bool ok = true;
-  for (int base = 0; base < n && ok; base += 8 * NT) {
-    uint32_t pending = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (base + t + k * NT < n) pending |= 1u << k;
-    uint32_t spins = 0;
-    while (pending) {
-      uint64_t w[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (pending & (1u << k))
-          w[k] = __hip_atomic_load(const_cast<uint64_t*>(buf + base + t + k * NT), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if ((pending & (1u << k)) && (uint32_t)w[k] == tag) {
-          dst[base + t + k * NT] = __uint_as_float((uint32_t)(w[k] >> 32)) * scale;
-          pending &= ~(1u << k);
-        }
-      }
-      if (pending) {
-        __builtin_amdgcn_s_sleep(1);  // back off: tight polling slows the publishers' stores
-        if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); ok = false; break; }
-        if ((spins & 255u) == 0u && error_raised(err, salt)) { ok = false; break; }
-      }
-    }
-  }
-  if (!ok) *s_flag = 1;
-  __syncthreads();
-  const bool all_ok = (*s_flag == 0);
-  return all_ok;
 }
 
 }  // namespace dfl

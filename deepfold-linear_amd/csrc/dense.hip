@@ -31,11 +31,6 @@ __device__ __forceinline__ float wave_max(float x) {
   for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, WAVE));
   return x;
 }
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, WAVE);
-  return x;
-}
 __device__ __forceinline__ float mask_bias(const float* mask, int b, int N, int j) {
   return mask ? (1.f - mask[(size_t)b * N + j]) * MASK_BIAS : 0.f;
 }

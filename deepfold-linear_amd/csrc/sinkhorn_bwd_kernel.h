@@ -133,31 +133,63 @@ __device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const
 }
 
 // Deterministic block-wide sum of f(i) over i in [0, n) (same order in every block).
+// red holds two slots of BWD_NW partials used alternately (flip), so one barrier
+// suffices: a slot is rewritten only after the barrier of the call in between.
 template <typename F>
-__device__ __forceinline__ float block_sum(int n, F f, float* red) {
+__device__ __forceinline__ float block_sum(int n, F f, float* red, int& flip) {
   float acc = 0.f;
   for (int i = threadIdx.x; i < n; i += BWD_NT) acc += f(i);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
-  const int wave = threadIdx.x / WAVE;
-  __syncthreads();
-  if ((threadIdx.x & (WAVE - 1)) == 0) red[wave] = acc;
+  acc = wave_sum(acc);
+  float* slot = red + flip * BWD_NW;
+  flip ^= 1;
+  if ((threadIdx.x & (WAVE - 1)) == 0) slot[threadIdx.x / WAVE] = acc;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
-  for (int w = 0; w < BWD_NW; ++w) tot += red[w];
-  __syncthreads();
+  for (int w = 0; w < BWD_NW; ++w) tot += slot[w];
   return tot;
 }
 
-// Gather a published vector into dst (scale 1), zeroing invalid entries and the tail.
+// Gather a published vector into dst: values at valid indices < n, zero elsewhere
+// (invalid entries and the tail [n, Np)); one barrier at the end.  Returns false
+// (uniformly) if the error flag is raised or a wait expires.
 __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
                                               const unsigned char* valid, uint32_t* err, int* s_flag) {
-  if (!xch_gather<BWD_NT>(buf, n, tag, dst, 1.f, err, s_flag)) return false;  // values as published
-  for (int i = threadIdx.x; i < Np; i += BWD_NT)
-    if (i >= n || !valid[i]) dst[i] = 0.f;
+  const uint32_t salt = tag >> 12;
+  const int t = threadIdx.x;
+  for (int i = n + t; i < Np; i += BWD_NT) dst[i] = 0.f;
+  bool ok = true;
+  for (int base = 0; base < n && ok; base += 8 * BWD_NT) {
+    uint32_t pending = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (base + t + k * BWD_NT < n) pending |= 1u << k;
+    uint32_t spins = 0;
+    while (pending) {
+      uint64_t w[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (pending & (1u << k))
+          w[k] = __hip_atomic_load(const_cast<uint64_t*>(buf + base + t + k * BWD_NT), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if ((pending & (1u << k)) && (uint32_t)w[k] == tag) {
+          const int i = base + t + k * BWD_NT;
+          dst[i] = valid[i] ? __uint_as_float((uint32_t)(w[k] >> 32)) : 0.f;
+          pending &= ~(1u << k);
+        }
+      }
+      if (pending) {
+        __builtin_amdgcn_s_sleep(1);  // back off: tight polling slows the publishers' stores
+        if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); ok = false; break; }
+        if ((spins & 255u) == 0u && error_raised(err, salt)) { ok = false; break; }
+      }
+    }
+  }
+  if (!ok) *s_flag = 1;
   __syncthreads();
-  return true;
+  return *s_flag == 0;
 }
 
 // Resident-tile assignment of the heavy passes.  With nr <= BWD_NW resident tiles,
@@ -373,7 +405,7 @@ __device__ __forceinline__ void stage_jobs(const StageJob (&J)[NJ], int r0, int 
 struct BwdShared {
   int flag, tmp;
   float posw[68];
-  float red[BWD_NW];
+  float red[2 * BWD_NW];
 };
 
 // Streamed rows per LDS chunk in resident mode (stream mode sizes it on the host).
@@ -760,7 +792,8 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       ctw[i] = 0.f;
     }
     __syncthreads();
-    float rr = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red);
+    int flip = 0;
+    float rr = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red, flip);
     // cg_rtol > 0: stop once ||r|| <= rtol ||b|| (utils/cg.py:63-80).  cg_rtol == 0:
     // exactly `iters` iterations; a residual that reaches zero stays zero (alpha = beta = 0).
     // rr, pAp and rr_new are bit-identical in every member, so the exit is uniform.
@@ -784,7 +817,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase);
       if (!gather_vector(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag)) return;
       // CG update, identical in every member (utils/cg.py:70-92 with x0 = 0)
-      const float pAp = block_sum(Np, [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red);
+      const float pAp = block_sum(Np, [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red, flip);
       if (early_exit && pAp == 0.f) break;
       const float alpha = (pAp != 0.f && rr != 0.f) ? rr / pAp : 0.f;
       for (int i = threadIdx.x; i < Np; i += BWD_NT) {
@@ -793,7 +826,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
         ctw[i] += alpha * ct[i];
       }
       __syncthreads();
-      const float rr_new = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red);
+      const float rr_new = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red, flip);
       const float beta = rr != 0.f ? rr_new / rr : 0.f;
       for (int i = threadIdx.x; i < Np; i += BWD_NT) cp[i] = cr[i] + beta * cp[i];
       rr = rr_new;
