@@ -460,7 +460,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   float* ctw = ct + Np;      // CG W x (rows)
   float* xs = ctw + Np;      // x coordinates [Np][3]
   float* dxc = xs + 3 * Np;  // grad x_centroid rows [Np][3]
-  float* lres = STREAM ? after_region : dxc + 3 * Np;  // per-local-row constants [loc]
+  float* lres = STREAM ? after_region : dxc + 3 * Np;  // per-local-row constants [loc] (stream mode)
   float* lout = lres + loc;      // per-local-row results [loc]
   float* dxs = lout + loc;       // dx accumulator for my stripe [loc][3]
   float* dpw = dxs + 3 * loc;    // d pos_weight histogram [68]
@@ -725,24 +725,31 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     stage_rows<T, DP>(KS, Kg, a.sn, n, d, Np);
   }
   __syncthreads();
-  // lout[q] = sum_j exp2(sc <res_q, str_j> + lres[q] + w2_j (+bias)) z_j over all
+  // lout[q] = sum_j exp2(sc <res_q, str_j> + cres[q] + w2_j (+bias)) z_j over all
   // streamed j; row = true: resident plan rows (Q) against streamed K.
-  auto wsum = [&](bool row, const float* w2, const float* z) {
+  // cres: per-resident-row constants, local index (X + r_lo for an Np-vector X).
+  // Resident mode reads them in place (LDS); stream mode keeps its vectors in the
+  // workspace, so they are first copied to LDS (lres).
+  auto wsum = [&](bool row, const float* w2, const float* z, const float* cres_in) {
+    const float* cres = cres_in;
     if constexpr (STREAM) {
+      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = cres_in[q];
+      __syncthreads();
+      cres = lres;
       if (row) {
-        if (general) stream_sweep<BWD_NT, T, DP, SW_WSUM, true, false>(QS, Kp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
-        else stream_sweep<BWD_NT, T, DP, SW_WSUM, false, false>(QS, Kp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+        if (general) stream_sweep<BWD_NT, T, DP, SW_WSUM, true, false>(QS, Kp, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+        else stream_sweep<BWD_NT, T, DP, SW_WSUM, false, false>(QS, Kp, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, nullptr, scratch, nullptr, NoPublish());
       } else {
-        if (general) stream_sweep<BWD_NT, T, DP, SW_WSUM, true, true>(KS, Qp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
-        else stream_sweep<BWD_NT, T, DP, SW_WSUM, false, true>(KS, Qp, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+        if (general) stream_sweep<BWD_NT, T, DP, SW_WSUM, true, true>(KS, Qp, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, nullptr, scratch, nullptr, NoPublish());
+        else stream_sweep<BWD_NT, T, DP, SW_WSUM, false, true>(KS, Qp, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, nullptr, scratch, nullptr, NoPublish());
       }
     } else {
       if (row) {
-        if (general) light_sweep<T, DP, true, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
-        else light_sweep<T, DP, false, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
+        if (general) light_sweep<T, DP, true, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
+        else light_sweep<T, DP, false, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
       } else {
-        if (general) light_sweep<T, DP, true, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
-        else light_sweep<T, DP, false, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, lres, bias, lout, scratch);
+        if (general) light_sweep<T, DP, true, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
+        else light_sweep<T, DP, false, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
       }
     }
   };
@@ -761,16 +768,12 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     __syncthreads();
     for (int it = 0; it < a.iters; ++it) {
       // z_u_i = kappa sum_j S_col_ij z_v_j   (resident rows: cres = u_i)
-      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = uu[r_lo + q];
-      __syncthreads();
-      wsum(true, mcl, zvv);
+      wsum(true, mcl, zvv, uu + r_lo);
       ++phase;
       for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, kappa * lout[i - r_lo], salt | phase);
       if (!gather_vector(xA, n, Np, salt | phase, zu, valid, a.err, &sh.flag)) return;
       // z_v_j = g_v_j + kappa sum_i T_ij z_u_i   (resident cols: cres = v_j)
-      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = vv[r_lo + q];
-      __syncthreads();
-      wsum(false, a2, zu);
+      wsum(false, a2, zu, vv + r_lo);
       ++phase;
       for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT)
         xch_put(xB + j, gv[j] + kappa * lout[j - r_lo], salt | phase);
@@ -803,16 +806,12 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     for (int it = 0; it < a.iters; ++it) {
       if (early_exit && (rr <= stop2 || rr == 0.f)) break;
       // t_i = sum_j W_ij p_j (my rows)
-      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = al[r_lo + q];
-      __syncthreads();
-      wsum(true, be, cp);
+      wsum(true, be, cp, al + r_lo);
       ++phase;
       for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, lout[i - r_lo], salt | phase);
       if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) return;
       // s_j = sum_i W_ij t_i (my cols)
-      for (int q = threadIdx.x; q < nr * 16; q += BWD_NT) lres[q] = be[r_lo + q];
-      __syncthreads();
-      wsum(false, al, ct);
+      wsum(false, al, ct, be + r_lo);
       ++phase;
       for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase);
       if (!gather_vector(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag)) return;
