@@ -819,13 +819,14 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       const float pAp = block_sum(Np, [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red, flip);
       if (early_exit && pAp == 0.f) break;
       const float alpha = (pAp != 0.f && rr != 0.f) ? rr / pAp : 0.f;
-      for (int i = threadIdx.x; i < Np; i += BWD_NT) {
+      // the update and ||r_new||^2 in one pass: each thread squares the entries it wrote
+      const float rr_new = block_sum(Np, [&](int i) {
         cy[i] += alpha * cp[i];
-        cr[i] -= alpha * (cp[i] - k2 * cs[i]);
+        const float ri = cr[i] - alpha * (cp[i] - k2 * cs[i]);
+        cr[i] = ri;
         ctw[i] += alpha * ct[i];
-      }
-      __syncthreads();
-      const float rr_new = block_sum(Np, [&](int i) { return cr[i] * cr[i]; }, sh.red, flip);
+        return ri * ri;
+      }, sh.red, flip);
       const float beta = rr != 0.f ? rr_new / rr : 0.f;
       for (int i = threadIdx.x; i < Np; i += BWD_NT) cp[i] = cr[i] + beta * cp[i];
       rr = rr_new;
