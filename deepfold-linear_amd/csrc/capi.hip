@@ -39,6 +39,11 @@ hipError_t dense_sinkhorn_backward(const DenseSinkBwdArgs& a, hipStream_t s);
 hipError_t dense_zero(float* p, size_t n, hipStream_t s);
 hipError_t dense_transport_forward(const DenseTransportArgs& a, hipStream_t s);
 hipError_t dense_transport_backward(const DenseTransportArgs& a, hipStream_t s);
+size_t balanced_bwd_lds_bytes(int N, int DP);
+int balanced_max_tiles(int DP);
+hipError_t launch_balanced_prep(const BalPrepArgs& p, int DP, hipStream_t stream);
+hipError_t launch_balanced_bwd(const BalBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop);
+hipError_t launch_balanced_finalize(const BalBwdArgs& a, float* dx, float* dalpha, float* dr, hipStream_t stream);
 }  // namespace dfl
 
 namespace {
@@ -231,6 +236,93 @@ dfl::A2TArgs a2t_args(const dfl_a2t_params* p) {
   return a;
 }
 
+// Storage-mode choice, workspace pointers and launches of the persistent forward
+// (shared by the UOT and the balanced entry points).  a holds inputs and outputs.
+int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, void* workspace, void* stream) {
+  const int G = group_size(a.B, a.H, a.N);
+  const int elem = bf16 ? 2 : 4;
+  const size_t lds_res = dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, false);
+  const bool stream_mode = storage == DFL_STORAGE_STREAM || (storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT);
+  const size_t lds = stream_mode ? dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, true) : lds_res;
+  if (lds > LDS_LIMIT)
+    return fail("N=%d, d=%d, %s storage needs %zu bytes of LDS per workgroup (limit %zu)", a.N, a.d,
+                stream_mode ? "stream" : "resident", lds, LDS_LIMIT);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
+  a.G = G;
+  a.salt = next_salt();
+  const bool coop = G > 1;  // members wait on each other: all must be co-resident
+  hipError_t e;
+  if (stream_mode) {
+    const StreamPtrs sp = stream_ptrs(workspace, a.B, a.H, a.N, G);
+    dfl::PadArgs pa;
+    memset(&pa, 0, sizeof(pa));
+    pa.q = a.q; pa.k = a.k; pa.v = a.v;
+    pa.sb = a.sb; pa.sh = a.sh; pa.sn = a.sn;
+    pa.x = a.x; pa.mask = a.mask;
+    pa.B = a.B; pa.H = a.H; pa.N = a.N; pa.d = a.d;
+    pa.qp = sp.qp; pa.kp = sp.kp; pa.vt = a.v ? sp.vt : nullptr; pa.xs_p = sp.xs_p;
+    e = dfl::launch_sinkhorn_pad(pa, bf16, DP, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "sinkhorn pad launch");
+    a.qp = sp.qp; a.kp = sp.kp; a.vt = sp.vt; a.xs_p = sp.xs_p;
+    e = dfl::launch_sinkhorn_fwd_stream(a, bf16, DP, lds, (hipStream_t)stream, coop);
+  } else {
+    e = dfl::launch_sinkhorn_fwd(a, bf16, DP, lds, (hipStream_t)stream, coop);
+  }
+  if (e != hipSuccess) return hip_fail(e, "sinkhorn forward launch");
+  return 0;
+}
+
+// Balanced transport workspace: the forward's (header, exchange words, stream
+// region), or the backward's prepared operands and partials if larger.
+struct BalWs {
+  size_t qp, kp, qt, kt, vp, gp, gt, dcoef, gxs, xs, dx_part, ar_part, total;
+};
+BalWs bal_ws_layout(int B, int H, int N, int d) {
+  auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t np = np32(N);
+  const int DP = head_dim_pad(d) < 0 ? 64 : head_dim_pad(d);
+  const int G = group_size(B, H, N);
+  const size_t op = r256((size_t)B * H * np * DP * 4);
+  BalWs w;
+  w.qp = r256(WS_HEADER + xch_words(B, H, N) * 8);
+  w.kp = w.qp + op;
+  w.qt = w.kp + op;
+  w.kt = w.qt + op;
+  w.vp = w.kt + op;
+  w.gp = w.vp + op;
+  w.gt = w.gp + op;
+  w.dcoef = w.gt + op;
+  w.gxs = w.dcoef + r256((size_t)B * H * np * 4);
+  w.xs = w.gxs + r256((size_t)B * H * 3 * np * 4);
+  w.dx_part = w.xs + r256((size_t)B * 3 * np * 4);
+  w.ar_part = w.dx_part + r256((size_t)B * H * N * 3 * 4);
+  w.total = w.ar_part + r256((size_t)B * H * G * 2 * 4);
+  return w;
+}
+
+// Forward workspace: the header and exchange words when (b,h) stays resident in
+// LDS, else the whole stream-mode layout of the UOT forward.
+size_t bal_fwd_need(int B, int H, int N, int d, int storage) {
+  const int DP = head_dim_pad(d) < 0 ? 64 : head_dim_pad(d);
+  const size_t lds_res = dfl::sinkhorn_fwd_lds_bytes(N, DP, 4, group_size(B, H, N), false);
+  const bool stream_mode = storage == DFL_STORAGE_STREAM || (storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT);
+  if (stream_mode) return dfl_sinkhorn_workspace_size(B, H, N);
+  return WS_HEADER + xch_words(B, H, N) * 8;
+}
+
+int check_balanced(int dtype, const void* q, const void* k, const float* x, const float* eps, const float* alpha,
+                   const float* r, int B, int H, int N, int d, int K_iter, long long sn) {
+  if (dtype != DFL_F32) return fail("balanced transport computes in fp32: dtype must be DFL_F32");
+  if (B <= 0 || H <= 0 || N <= 0 || d <= 0) return fail("B, H, N, d must be positive");
+  if (head_dim_pad(d) < 0) return fail("head dim d=%d > 64 is not supported", d);
+  if (K_iter < 1 || K_iter > 1000) return fail("K_iter=%d outside [1, 1000]", K_iter);
+  if (!q || !k || !x || !eps || !alpha || !r) return fail("required input is NULL");
+  if (sn < d) return fail("stride_n must be >= d (unit inner stride)");
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -273,14 +365,6 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
   const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
   if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
   if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_STREAM) return fail("unknown storage %d", p->storage);
-  const int G = group_size(p->B, p->H, p->N);
-  const int elem = p->dtype == DFL_BF16 ? 2 : 4;
-  const size_t lds_res = dfl::sinkhorn_fwd_lds_bytes(p->N, DP, elem, G, false);
-  const bool stream_mode = p->storage == DFL_STORAGE_STREAM || (p->storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT);
-  const size_t lds = stream_mode ? dfl::sinkhorn_fwd_lds_bytes(p->N, DP, elem, G, true) : lds_res;
-  if (lds > LDS_LIMIT)
-    return fail("N=%d, d=%d, %s storage needs %zu bytes of LDS per workgroup (limit %zu)", p->N, p->d,
-                stream_mode ? "stream" : "resident", lds, LDS_LIMIT);
 
   dfl::SinkFwdArgs a;
   memset(&a, 0, sizeof(a));
@@ -293,31 +377,7 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
   a.K_iter = p->K_iter; a.lam = p->lam; a.r0 = p->r_0;
   a.o_flat = p->o_flat; a.x_centroid = p->x_centroid; a.log_u = p->log_u; a.log_v = p->log_v;
   a.o_avg = p->o_avg; a.log_z = p->log_z; a.col_lse = p->col_lse;
-  unsigned char* ws = static_cast<unsigned char*>(workspace);
-  a.err = reinterpret_cast<uint32_t*>(ws);
-  a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
-  a.G = G;
-  a.salt = next_salt();
-  const bool coop = G > 1;  // members wait on each other: all must be co-resident
-  hipError_t e;
-  if (stream_mode) {
-    const StreamPtrs sp = stream_ptrs(workspace, p->B, p->H, p->N, G);
-    dfl::PadArgs pa;
-    memset(&pa, 0, sizeof(pa));
-    pa.q = p->q; pa.k = p->k; pa.v = p->v;
-    pa.sb = p->stride_b; pa.sh = p->stride_h; pa.sn = p->stride_n;
-    pa.x = p->x_res; pa.mask = p->mask;
-    pa.B = p->B; pa.H = p->H; pa.N = p->N; pa.d = p->d;
-    pa.qp = sp.qp; pa.kp = sp.kp; pa.vt = sp.vt; pa.xs_p = sp.xs_p;
-    e = dfl::launch_sinkhorn_pad(pa, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e, "sinkhorn pad launch");
-    a.qp = sp.qp; a.kp = sp.kp; a.vt = sp.vt; a.xs_p = sp.xs_p;
-    e = dfl::launch_sinkhorn_fwd_stream(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
-  } else {
-    e = dfl::launch_sinkhorn_fwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
-  }
-  if (e != hipSuccess) return hip_fail(e, "sinkhorn forward launch");
-  return 0;
+  return run_fwd(a, p->dtype == DFL_BF16, DP, p->storage, workspace, stream);
 }
 
 int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
@@ -611,6 +671,91 @@ int dfl_dense_transport_bwd(const dfl_dense_transport_params* p, void* workspace
   a.dx_part = p->x_res ? reinterpret_cast<float*>(ws + (bhn * p->d * 4 + 255) / 256 * 256) : nullptr;
   hipError_t e = dfl::dense_transport_backward(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "dense transport backward launch");
+  return 0;
+}
+
+size_t dfl_balanced_workspace_size(int B, int H, int N, int d, int backward) {
+  if (B <= 0 || H <= 0 || N <= 0 || d <= 0) return 0;
+  const size_t f = bal_fwd_need(B, H, N, d, DFL_STORAGE_AUTO);
+  if (!backward) return f;
+  const size_t b = bal_ws_layout(B, H, N, d).total;
+  return f > b ? f : b;
+}
+
+int dfl_balanced_fwd(const dfl_balanced_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!p) return fail("params is NULL");
+  if (int rc = check_balanced(p->dtype, p->q, p->k, p->x_res, p->eps, p->alpha_h, p->r_h, p->B, p->H, p->N, p->d,
+                              p->K_iter, p->stride_n))
+    return rc;
+  if (!p->x_centroid || !p->log_u || !p->log_v || !p->log_z || !p->hist) return fail("output pointer is NULL");
+  if (p->h_centroid && !p->v) return fail("h_centroid needs v");
+  if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_STREAM) return fail("unknown storage %d", p->storage);
+  const size_t need = bal_fwd_need(p->B, p->H, p->N, p->d, p->storage);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  dfl::SinkFwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = p->q; a.k = p->k; a.v = p->h_centroid ? p->v : nullptr;
+  a.sb = p->stride_b; a.sh = p->stride_h; a.sn = p->stride_n;
+  a.x = p->x_res; a.eps = p->eps; a.mask = p->mask;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d;
+  a.K_iter = p->K_iter; a.lam = 1.f; a.r0 = 1.f;
+  a.x_centroid = p->x_centroid; a.o_avg = p->h_centroid;
+  a.log_u = p->log_u; a.log_v = p->log_v; a.log_z = p->log_z;
+  a.balanced = 1; a.alpha = p->alpha_h; a.r_h = p->r_h; a.hist = p->hist;
+  return run_fwd(a, false, head_dim_pad(p->d), p->storage, workspace, stream);
+}
+
+int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!p) return fail("params is NULL");
+  if (int rc = check_balanced(p->dtype, p->q, p->k, p->x_res, p->eps, p->alpha_h, p->r_h, p->B, p->H, p->N, p->d,
+                              p->K_iter, p->stride_n))
+    return rc;
+  if (!p->x_centroid || !p->hist) return fail("x_centroid and hist are required");
+  if (p->grad_hc && (!p->v || !p->h_centroid)) return fail("grad_hc needs v and h_centroid");
+  if (!p->dq || !p->dk || !p->dx_res || !p->dalpha_h || !p->dr_h) return fail("output pointer is NULL");
+  const size_t need = bal_ws_layout(p->B, p->H, p->N, p->d).total;
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  const int DP = head_dim_pad(p->d);
+  const int G = group_size(p->B, p->H, p->N);
+  const int max_nr = ((p->N + 15) / 16 + G - 1) / G;
+  if (max_nr > dfl::balanced_max_tiles(DP))
+    return fail("balanced backward: N=%d over %d workgroups per (b,h) exceeds %d tiles of 16 rows each", p->N, G,
+                dfl::balanced_max_tiles(DP));
+  const size_t lds = dfl::balanced_bwd_lds_bytes(p->N, DP);
+  if (lds > LDS_LIMIT)
+    return fail("balanced backward: N=%d needs %zu bytes of LDS per workgroup (limit %zu)", p->N, lds, LDS_LIMIT);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const BalWs L = bal_ws_layout(p->B, p->H, p->N, p->d);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
+  const bool has_h = p->grad_hc != nullptr;
+  dfl::BalPrepArgs pr;
+  memset(&pr, 0, sizeof(pr));
+  pr.q = static_cast<const float*>(p->q); pr.k = static_cast<const float*>(p->k);
+  pr.v = static_cast<const float*>(p->v);
+  pr.sb = p->stride_b; pr.sh = p->stride_h; pr.sn = p->stride_n;
+  pr.x = p->x_res; pr.mask = p->mask; pr.xc = p->x_centroid; pr.hc = p->h_centroid;
+  pr.gxc = p->grad_xc; pr.ghc = p->grad_hc;
+  pr.B = p->B; pr.H = p->H; pr.N = p->N; pr.d = p->d;
+  pr.qp = F(L.qp); pr.kp = F(L.kp); pr.qt = F(L.qt); pr.kt = F(L.kt);
+  pr.vp = has_h ? F(L.vp) : nullptr; pr.gp = has_h ? F(L.gp) : nullptr; pr.gt = has_h ? F(L.gt) : nullptr;
+  pr.dcoef = F(L.dcoef); pr.gxs = F(L.gxs); pr.xs = F(L.xs);
+  hipError_t e = dfl::launch_balanced_prep(pr, DP, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "balanced backward prep launch");
+  dfl::BalBwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d; a.K = p->K_iter;
+  a.eps = p->eps; a.alpha = p->alpha_h; a.r_h = p->r_h; a.mask = p->mask; a.hist = p->hist;
+  a.qp = pr.qp; a.kp = pr.kp; a.qt = pr.qt; a.kt = pr.kt; a.vp = pr.vp; a.gp = pr.gp; a.gt = pr.gt;
+  a.dcoef = pr.dcoef; a.gxs = pr.gxs; a.xs = pr.xs; a.has_h = has_h ? 1 : 0;
+  a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dx_part = F(L.dx_part); a.ar_part = F(L.ar_part);
+  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
+  a.G = G;
+  a.salt = next_salt();
+  e = dfl::launch_balanced_bwd(a, DP, lds, (hipStream_t)stream, G > 1);
+  if (e != hipSuccess) return hip_fail(e, "balanced backward launch");
+  e = dfl::launch_balanced_finalize(a, p->dx_res, p->dalpha_h, p->dr_h, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "balanced backward finalize launch");
   return 0;
 }
 

@@ -45,6 +45,14 @@ struct SinkFwdArgs {
   const void* kp;     // [B*H][Np][DP]
   const void* vt;     // [B*H][DP][Np]
   const float* xs_p;  // [B][Np][3]
+  // Balanced transport mode (flash_sinkhorn_transport.py:253-282, 289-320): column
+  // update first, kappa = 1, uniform marginals -log(n_valid) per sample, cost
+  // (1 - w_h)(1 - q.k) + w_h d/(r + d) with w_h = sigmoid(alpha_h), r = max(|r_h|, 0.1).
+  // log_mu / log_nu / g / o_flat / col_lse are unused (may be null); v may be null.
+  int balanced;
+  const float* alpha;  // (H,)
+  const float* r_h;    // (H,)
+  float* hist;         // (K_iter, 2, B*H, N): v after the column update, u after the row update
 };
 
 // Backward (flash_sinkhorn_attn.py:246-667 semantics, plus analytic mode / CG).
@@ -100,6 +108,55 @@ struct SinkBwdArgs {
   const void* qp;  // [B*H][Np][DP] zero-padded copies (sinkhorn_pad_kernel)
   const void* kp;
   float* vec_ws;   // per-workgroup vectors, BWD_STREAM_VECS * Np floats each
+};
+
+// Unrolled backward of the balanced transport (flash_sinkhorn_transport.py:322-373,
+// 448-516).  fp32 operands; every prepared array is per (b,h) with Np rows, zero
+// on masked rows, rows >= N and columns >= d.
+struct BalBwdArgs {
+  int B, H, N, d, K;
+  const float* eps;    // (H,)
+  const float* alpha;  // (H,)
+  const float* r_h;    // (H,)
+  const float* mask;   // (B,N) or null
+  const float* hist;   // (K, 2, B*H, N) forward potentials (natural log)
+  const float* qp;     // [B*H][Np][DP]
+  const float* kp;
+  const float* qt;     // [B*H][DP][Np]
+  const float* kt;
+  const float* vp;     // [B*H][Np][DP]  V            (h centroid only)
+  const float* gp;     // [B*H][Np][DP]  grad h_c     (h centroid only)
+  const float* gt;     // [B*H][DP][Np]  grad h_c transposed
+  const float* dcoef;  // [B*H][Np]      D_i = dxc_i.xc_i + dhc_i.hc_i
+  const float* gxs;    // [B*H][3][Np]   grad x_c, coordinate-major
+  const float* xs;     // [B][3][Np]     coordinates, coordinate-major
+  int has_h;           // grad h_c given
+  float* dq;           // (B,H,N,d)
+  float* dk;
+  float* dv;           // (B,H,N,d) or null
+  float* dx_part;      // (B,H,N,3) per-head partials
+  float* ar_part;      // (B*H*G, 2) per-workgroup d alpha, d r partials
+  uint64_t* xch;       // B*H*2*Np exchange words
+  uint32_t* err;
+  int G;
+  uint32_t salt;
+};
+
+struct BalPrepArgs {
+  const float* q;  // (B,H,N,d) fp32, element strides sb/sh/sn, unit inner stride
+  const float* k;
+  const float* v;  // or null
+  long long sb, sh, sn;
+  const float* x;      // (B,N,3)
+  const float* mask;   // (B,N) or null
+  const float* xc;     // (B,H,N,3) forward x centroid
+  const float* hc;     // (B,H,N,d) forward h centroid (null without grad_hc)
+  const float* gxc;    // (B,H,N,3) or null
+  const float* ghc;    // (B,H,N,d) or null
+  int B, H, N, d;
+  float* qp; float* kp; float* qt; float* kt;
+  float* vp; float* gp; float* gt;  // null without grad_hc
+  float* dcoef; float* gxs; float* xs;
 };
 
 // Zero-padded operand copies for stream mode, written by sinkhorn_pad_kernel.

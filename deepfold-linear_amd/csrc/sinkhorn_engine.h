@@ -42,7 +42,7 @@ struct Bias {
     }
     if (xs) {
       const float dx = xs[3 * i] - xs[3 * j], dy = xs[3 * i + 1] - xs[3 * j + 1], dz = xs[3 * i + 2] - xs[3 * j + 2];
-      const float dist = sqrtf(dx * dx + dy * dy + dz * dz);
+      const float dist = fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-8f);
       b += geo_scale * dist / (r0 + dist);
     }
     return b;
@@ -571,7 +571,7 @@ __global__ void __launch_bounds__(256) sinkhorn_pad_kernel(PadArgs p) {
   if (ok && c < d) {
     qv = reinterpret_cast<const T*>(p.q)[off];
     kv = reinterpret_cast<const T*>(p.k)[off];
-    vv = reinterpret_cast<const T*>(p.v)[off];
+    if (p.v) vv = reinterpret_cast<const T*>(p.v)[off];
   }
   reinterpret_cast<T*>(p.qp)[row * DP + c] = qv;
   reinterpret_cast<T*>(p.kp)[row * DP + c] = kv;

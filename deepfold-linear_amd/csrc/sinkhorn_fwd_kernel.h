@@ -21,6 +21,15 @@
 //             (sinkhorn_pad_kernel), which stay L2-resident.  Used when the
 //             resident layout does not fit in 160 KB of LDS (long sequences).
 //
+// Balanced mode (SinkFwdArgs::balanced) restates the balanced transport of
+// flash_sinkhorn_transport.py:253-282 with the same machinery: column update
+// first, kappa = 1, log marginals -log(n_valid) of the sample, logit
+// (1 - w_h)(q.k)/eps - w_h d/(r + d)/eps (the constant (1 - w_h)/eps of the cost
+// 1 - q.k shifts every column potential equally and leaves the plan unchanged),
+// and the potentials of every half-iteration written to a history for the
+// unrolled backward.  The last update is a row update, so the plan's rows sum to
+// 1/n exactly and the output pass normalises by the row LSE of that update.
+//
 // All logits are handled in log2 units (x * log2 e) so that exp2 maps onto
 // v_exp_f32 directly.
 #pragma once
@@ -79,7 +88,7 @@ template <typename T, int DP>
 __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int h, int tile, int n,
                                                const unsigned char* valid, const float* lse2_t, const float* mx2_t,
                                                const float* vecU, const float* vecV, const f32x4* oacc, float xc0,
-                                               float xc1, float xc2, const T* Gg, int lane) {
+                                               float xc1, float xc2, const T* Gg, int lane, bool bal) {
   constexpr int NC = DP / 16;
   const int N = a.N, d = a.d;
   const int g = lane >> 4;
@@ -91,7 +100,7 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
   xc2 = sum_groups(xc2);
   // T_norm = p / (1 + 1e-6 * 2^(max - lse))  <=>  reference T / (sum T + 1e-6), T = e^(s - max)
   if (lane < 16 && irow < n && valid[irow]) {
-    const float den = 1.f + 1e-6f * fast_exp2(mx2_t[lane] - l2);
+    const float den = bal ? 1.f : 1.f + 1e-6f * fast_exp2(mx2_t[lane] - l2);
     const size_t o = (bh * N + irow) * 3;
     a.x_centroid[o + 0] = xc0 / den;
     a.x_centroid[o + 1] = xc1 / den;
@@ -104,8 +113,9 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
     const size_t o = (bh * N + irow) * 3;
     a.x_centroid[o + 0] = a.x_centroid[o + 1] = a.x_centroid[o + 2] = 0.f;
     a.log_u[bh * N + irow] = a.log_z[bh * N + irow] = a.log_v[bh * N + irow] = 0.f;
-    a.col_lse[bh * N + irow] = 0.f;
+    if (a.col_lse) a.col_lse[bh * N + irow] = 0.f;
   }
+  if (!a.o_avg) return;  // no V: coordinate centroid only
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = tile * 16 + 4 * g + r;
@@ -115,20 +125,22 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
         const int col = c * 16 + (lane & 15);
         if (col < d) {
           a.o_avg[(bh * N + row) * d + col] = 0.f;
-          a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = 0.f;
+          if (a.o_flat) a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = 0.f;
         }
       }
     }
     if (row < n && valid[row]) {
-      const float den = 1.f + 1e-6f * fast_exp2(mx2_t[4 * g + r] - lse2_t[4 * g + r]);
+      const float den = bal ? 1.f : 1.f + 1e-6f * fast_exp2(mx2_t[4 * g + r] - lse2_t[4 * g + r]);
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int col = c * 16 + (lane & 15);
         if (col < d) {
           const float o = oacc[c][r] / den;
           a.o_avg[(bh * N + row) * d + col] = o;
-          const float sg = Gg ? 1.f / (1.f + __expf(-to_f32(Gg[(size_t)row * a.sn + col]))) : 1.f;
-          a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = sg * o;
+          if (a.o_flat) {
+            const float sg = Gg ? 1.f / (1.f + __expf(-to_f32(Gg[(size_t)row * a.sn + col]))) : 1.f;
+            a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = sg * o;
+          }
         }
       }
     }
@@ -140,13 +152,16 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_flag, s_tmp;
   __shared__ unsigned s_du, s_dv;
+  __shared__ int s_cnt;
   __shared__ float s_posw[68];
   int grp, member;
   if (!group_of(a.B * a.H, a.G, grp, member)) return;  // surplus workgroup of the XCD-aligned grid
   const int b = grp / a.H, h = grp % a.H;
   const int N = a.N, d = a.d;
   const int Np = ((N + 31) / 32) * 32;
-  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; }
+  const bool bal = a.balanced != 0;
+  const bool has_v = a.v != nullptr && a.o_avg != nullptr;
+  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; s_cnt = 0; }
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
@@ -179,15 +194,15 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     const size_t bh0 = (size_t)b * a.H + h;
     for (int i = n_tiles * 16 + member; i < N; i += a.G) {
       for (int c = threadIdx.x; c < d; c += FWD_NT) {
-        a.o_avg[(bh0 * N + i) * d + c] = 0.f;
-        a.o_flat[((size_t)b * N + i) * (size_t)(a.H * d) + (size_t)h * d + c] = 0.f;
+        if (a.o_avg) a.o_avg[(bh0 * N + i) * d + c] = 0.f;
+        if (a.o_flat) a.o_flat[((size_t)b * N + i) * (size_t)(a.H * d) + (size_t)h * d + c] = 0.f;
       }
       if (threadIdx.x < 3) a.x_centroid[(bh0 * N + i) * 3 + threadIdx.x] = 0.f;
       if (threadIdx.x == 0) {
         a.log_u[bh0 * N + i] = 0.f;
         a.log_v[bh0 * N + i] = 0.f;
         a.log_z[bh0 * N + i] = 0.f;
-        a.col_lse[bh0 * N + i] = 0.f;
+        if (a.col_lse) a.col_lse[bh0 * N + i] = 0.f;
       }
     }
   }
@@ -212,19 +227,28 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   }
 
   const float eps = a.eps[h];
-  const float kappa = a.lam / (a.lam + eps);
-  const float sc = LOG2E / (sqrtf((float)d) * eps);
+  const float w_bal = bal ? 1.f / (1.f + __expf(-a.alpha[h])) : 0.f;
+  const float kappa = bal ? 1.f : a.lam / (a.lam + eps);
+  const float sc = bal ? LOG2E * (1.f - w_bal) / eps : LOG2E / (sqrtf((float)d) * eps);
+  float lmarg = 0.f;  // balanced: log(1 / n_valid) of this sample
+  if (bal) {
+    int c = 0;
+    for (int i = threadIdx.x; i < n; i += FWD_NT) c += valid[i];
+    atomicAdd(&s_cnt, c);
+    __syncthreads();
+    lmarg = -logf((float)max(s_cnt, 1));
+  }
   for (int q = threadIdx.x; q < nr * 16; q += FWD_NT) {
     const int i = r_lo + q;
-    lmu_l[q] = i < n ? a.log_mu[bh * N + i] : 0.f;
-    lnu_l[q] = i < n ? a.log_nu[bh * N + i] : 0.f;
+    lmu_l[q] = i < n ? (bal ? lmarg : a.log_mu[bh * N + i]) : 0.f;
+    lnu_l[q] = i < n ? (bal ? lmarg : a.log_nu[bh * N + i]) : 0.f;
   }
   for (int i = threadIdx.x; i < Np; i += FWD_NT) {
     const bool ok = i < n && valid[i];
     vecU[i] = ok ? (a.u_init ? a.u_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
     vecV[i] = ok ? (a.v_init ? a.v_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
   }
-  const float w_h = a.w_dist ? a.w_dist[h] : 0.f;
+  const float w_h = bal ? w_bal : (a.w_dist ? a.w_dist[h] : 0.f);
   const bool use_geo = (a.x != nullptr) && (w_h != 0.f);
   const bool use_pos = (a.bins != nullptr) && (a.pos_w != nullptr);
   if (use_pos)
@@ -242,7 +266,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   bias.posw = s_posw;
   bias.xs = use_geo ? xsrc : nullptr;
   bias.geo_scale = -LOG2E * w_h / eps;
-  bias.r0 = a.r0;
+  bias.r0 = bal ? fmaxf(fabsf(a.r_h[h]), 0.1f) : a.r0;
   bias.N = N;
   const bool general = use_pos || use_geo;
 
@@ -278,20 +302,27 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
 
-  for (int it = 0; it < a.K_iter; ++it) {
-    // ---- row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j)) for my rows
+  // ---- row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j)) for my rows
+  auto row_update = [&](int it) -> bool {
     ++phase;
     {
       const uint32_t tag = salt | phase;
       const bool online = it == 0 || __uint_as_float(s_dv) > FIXED_SHIFT_MAX_DELTA;
       auto pub = [&](int q, float l2) {
         const int i = r_lo + q;
-        if (i < n) xch_put(xu + i, kappa * (lmu_l[q] - l2 * LN2), tag);
+        if (i < n) {
+          const float u = kappa * (lmu_l[q] - l2 * LN2);
+          xch_put(xu + i, u, tag);
+          if (bal) a.hist[((size_t)(2 * it + 1) * a.B * a.H + bh) * N + i] = valid[i] ? u : 0.f;
+        }
       };
       sweep(true, online, lse_r, nullptr, &s_du, pub);
-      if (!gather_potential<FWD_NT>(xu, n, tag, vecU, valid, a.err, &s_flag, &s_du)) return;
+      if (!gather_potential<FWD_NT>(xu, n, tag, vecU, valid, a.err, &s_flag, &s_du)) return false;
     }
-    // ---- column update: v_j = kappa (log nu_j - LSE_i(L_ij + u_i)) for my columns
+    return true;
+  };
+  // ---- column update: v_j = kappa (log nu_j - LSE_i(L_ij + u_i)) for my columns
+  auto col_update = [&](int it) -> bool {
     ++phase;
     {
       const uint32_t tag = salt | phase;
@@ -300,15 +331,25 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       auto pub = [&](int q, float l2) {
         const int j = r_lo + q;
         if (j < n) {
-          xch_put(xv + j, kappa * (lnu_l[q] - l2 * LN2), tag);
-          if (last && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
+          const float v = kappa * (lnu_l[q] - l2 * LN2);
+          xch_put(xv + j, v, tag);
+          if (last && valid[j] && a.col_lse) a.col_lse[bh * N + j] = l2 * LN2;
+          if (bal) a.hist[((size_t)(2 * it) * a.B * a.H + bh) * N + j] = valid[j] ? v : 0.f;
         }
       };
       sweep(false, online, lse_c, nullptr, &s_dv, pub);
-      if (!gather_potential<FWD_NT>(xv, n, tag, vecV, valid, a.err, &s_flag, &s_dv)) return;
+      if (!gather_potential<FWD_NT>(xv, n, tag, vecV, valid, a.err, &s_flag, &s_dv)) return false;
+    }
+    return true;
+  };
+  for (int it = 0; it < a.K_iter; ++it) {
+    if (bal) {
+      if (!col_update(it) || !row_update(it)) return;
+    } else {
+      if (!row_update(it) || !col_update(it)) return;
     }
   }
-  if (a.K_iter == 0) {
+  if (a.K_iter == 0 && a.col_lse) {
     auto pub = [&](int q, float l2) {
       const int j = r_lo + q;
       if (j < n && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
@@ -316,8 +357,9 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     sweep(false, true, lse_c, nullptr, nullptr, pub);
   }
 
-  // ---- final row LSE with the last v: exact log Z and the row maximum
-  sweep(true, true, lse_r, mx2, nullptr, NoPublish());
+  // ---- final row LSE with the last v: exact log Z and the row maximum.  In
+  // balanced mode the last update was a row update whose LSE is that value.
+  if (!bal) sweep(true, true, lse_r, mx2, nullptr, NoPublish());
   const float* lse2 = lse_r;
 
   // ---- transport output for my rows: O_avg = T_norm V, x_c = T_norm x.
@@ -330,7 +372,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     // V^T replaces Q in LDS; resident Q fragments are read from global memory.
     T* VT = QS;  // [DP][Np]
     __syncthreads();
-    stage_rows_t<T, DP>(VT, Vg, a.sn, n, d, Np);
+    if (has_v) stage_rows_t<T, DP>(VT, Vg, a.sn, n, d, Np);
     __syncthreads();
     const int n_pairs = (n_tiles + 1) / 2;
     for (int rt = wave; rt < nr; rt += FWD_NW) {
@@ -369,12 +411,14 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
             }
           }
         }
+        if (has_v) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-          oacc[c] = M::pv_split(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
+          for (int c = 0; c < NC; ++c)
+            oacc[c] = M::pv_split(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
+        }
       }
       fwd_write_tile<T, DP>(a, b, h, tile, n, valid, lse2 + qloc, mx2 + qloc, vecU, vecV, oacc, xc0, xc1, xc2, Gg,
-                            lane);
+                            lane, bal);
     }
   } else {
     // Stream mode: K and V^T pass through LDS in chunks of FWD_OCH streamed rows
@@ -404,7 +448,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       for (int c0 = 0; c0 < n_tiles * 16; c0 += FWD_OCH) {
         __syncthreads();
         stage_rows<T, DP>(KC, Kp + (size_t)c0 * DP, DP, min(FWD_OCH, Np - c0), DP, FWD_OCH);
-        for (int e = threadIdx.x; e < DP * (FWD_OCH / VE); e += FWD_NT) {
+        for (int e = threadIdx.x; has_v && e < DP * (FWD_OCH / VE); e += FWD_NT) {
           const int c = e / (FWD_OCH / VE), jv = e - c * (FWD_OCH / VE);
           i32x4 v = {0, 0, 0, 0};
           if (c0 + jv * VE < Np) v = *reinterpret_cast<const i32x4*>(Vt + (size_t)c * Np + c0 + jv * VE);
@@ -446,10 +490,12 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
                   xc[k][2] = __builtin_fmaf(pv, xsrc[3 * jj + 2], xc[k][2]);
                 }
               }
+              if (has_v) {
 #pragma unroll
-              for (int c = 0; c < NC; ++c)
-                oacc[k][c] = M::pv_split(p[0], p[1], VC + (size_t)(c * 16 + (lane & 15)) * FWD_OCH + sp * 32, lane,
-                                         oacc[k][c]);
+                for (int c = 0; c < NC; ++c)
+                  oacc[k][c] = M::pv_split(p[0], p[1], VC + (size_t)(c * 16 + (lane & 15)) * FWD_OCH + sp * 32,
+                                           lane, oacc[k][c]);
+              }
             }
           }
         }
@@ -459,7 +505,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
         const int rt = rb0 + wave + FWD_NW * k;
         if (rt < nr)
           fwd_write_tile<T, DP>(a, b, h, t0 + rt, n, valid, lse2 + rt * 16, mx2 + rt * 16, vecU, vecV, oacc[k],
-                                xc[k][0], xc[k][1], xc[k][2], Gg, lane);
+                                xc[k][0], xc[k][1], xc[k][2], Gg, lane, bal);
       }
     }
   }

@@ -11,6 +11,8 @@ from .cross_attn_kernel import atom_to_token_attn, token_to_atom_attn  # noqa: F
 from .flash_atom_attn import flash_atom_attn  # noqa: F401
 from .flash_diffusion_attn import flash_diffusion_attn  # noqa: F401
 from .flash_sinkhorn_attn import FlashSinkhornAttn, flash_sinkhorn_attn  # noqa: F401
+from .flash_sinkhorn_transport import (  # noqa: F401
+    BalancedSinkhornDualFn, BalancedSinkhornFn, balanced_sinkhorn_transport, balanced_sinkhorn_transport_dual)
 from .sinkhorn import compute_transport_output, sinkhorn_solve  # noqa: F401
 from .sinkhorn_kernel import FlashSinkhornFunction, flash_sinkhorn  # noqa: F401
 

@@ -140,6 +140,34 @@ class DenseTransportParams(ctypes.Structure):
     ]
 
 
+class BalancedFwdParams(ctypes.Structure):
+    """Mirror of ``dfl_balanced_fwd_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("q", P), ("k", P), ("v", P),
+        ("stride_b", I64), ("stride_h", I64), ("stride_n", I64),
+        ("x_res", P), ("eps", P), ("alpha_h", P), ("r_h", P), ("mask", P),
+        ("B", I32), ("H", I32), ("N", I32), ("d", I32), ("K_iter", I32),
+        ("x_centroid", P), ("h_centroid", P), ("log_u", P), ("log_v", P), ("log_z", P), ("hist", P),
+        ("storage", I32),
+    ]
+
+
+class BalancedBwdParams(ctypes.Structure):
+    """Mirror of ``dfl_balanced_bwd_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("q", P), ("k", P), ("v", P),
+        ("stride_b", I64), ("stride_h", I64), ("stride_n", I64),
+        ("x_res", P), ("eps", P), ("alpha_h", P), ("r_h", P), ("mask", P),
+        ("B", I32), ("H", I32), ("N", I32), ("d", I32), ("K_iter", I32),
+        ("x_centroid", P), ("h_centroid", P), ("hist", P), ("grad_xc", P), ("grad_hc", P),
+        ("dq", P), ("dk", P), ("dv", P), ("dx_res", P), ("dalpha_h", P), ("dr_h", P),
+    ]
+
+
 DFL_ATTN_BIAS_NONE = 0
 DFL_ATTN_BIAS_BINS = 1
 DFL_ATTN_BIAS_DENSE = 2
@@ -166,6 +194,9 @@ SIGNATURES = [
     ("dfl_dense_transport_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
     ("dfl_dense_transport_fwd", I32, [ctypes.POINTER(DenseTransportParams), P]),
     ("dfl_dense_transport_bwd", I32, [ctypes.POINTER(DenseTransportParams), P, ctypes.c_size_t, P]),
+    ("dfl_balanced_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32, I32]),
+    ("dfl_balanced_fwd", I32, [ctypes.POINTER(BalancedFwdParams), P, ctypes.c_size_t, P]),
+    ("dfl_balanced_bwd", I32, [ctypes.POINTER(BalancedBwdParams), P, ctypes.c_size_t, P]),
 ]
 
 

@@ -1,0 +1,172 @@
+"""Balanced Sinkhorn transport: the coordinate (and feature) centroid of TokenOTBlock.
+
+Drop-in for ``deepfold.model.kernels.flash_sinkhorn_transport`` of
+vv137/deepfold-linear (src/deepfold/model/kernels/flash_sinkhorn_transport.py):
+``balanced_sinkhorn_transport`` (:376), ``balanced_sinkhorn_transport_dual`` (:519)
+and their autograd Functions ``BalancedSinkhornFn`` (:287) and
+``BalancedSinkhornDualFn`` (:403), with the same argument order, defaults and
+returns.  Both directions run as HIP kernels for gfx950 through the C ABI
+(``dfl_balanced_fwd`` / ``dfl_balanced_bwd`` in include/dfl_amd.h): the forward is
+the persistent flash-Sinkhorn kernel in its balanced mode (column update first,
+kappa = 1, plan never materialised) and the backward is the exact gradient of the
+K unrolled iterations, as the reference's.  There is no CPU path: CPU tensors raise.
+
+Semantics follow the reference's CPU form ``_sinkhorn_cpu`` (:253-282), which its
+tests compare against: per-sample log marginal -log(n_valid) (the reference's
+Triton path averages it over the batch, :294), geometry distance max(|x_i - x_j|,
+1e-8), padded tokens excluded from the plan with zero outputs, and the gradient
+of r_h through |r_h| clamped at 0.1 as autograd gives it.  Compute is fp32, as
+the reference casts its inputs with ``.float()`` (:291).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+def _f32c(t):
+    return None if t is None else t.detach().to(torch.float32).contiguous()
+
+
+def _run_forward(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask):
+    dev = _lib.require_gpu(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, mask)
+    if Q_s.dim() != 4:
+        raise ValueError(f"Q_s must be (B, H, N, d), got shape {tuple(Q_s.shape)}")
+    B, H, N, d = Q_s.shape
+    if K_s.shape != Q_s.shape:
+        raise ValueError("K_s must have the shape of Q_s")
+    if V_h is not None and V_h.shape != Q_s.shape:
+        raise ValueError("V_h must have the shape of Q_s (B, H, N, d)")
+    K_iter = int(K_iter)
+    Qf, Kf, Vf = _f32c(Q_s), _f32c(K_s), _f32c(V_h)
+    xf = _f32c(x_res)
+    ef, af, rf = _f32c(eps), _f32c(alpha_h), _f32c(r_h)
+    mf = None if mask is None else mask.detach().to(torch.float32).contiguous()
+    f32 = dict(device=dev, dtype=torch.float32)
+    xc = torch.empty(B, H, N, 3, **f32)
+    hc = torch.empty(B, H, N, d, **f32) if Vf is not None else None
+    lu = torch.empty(B, H, N, **f32)
+    lv = torch.empty(B, H, N, **f32)
+    lz = torch.empty(B, H, N, **f32)
+    hist = torch.zeros(max(K_iter, 1), 2, B, H, N, **f32)
+    lib = _lib.load()
+    ws = _lib.workspace(dev, lib.dfl_balanced_workspace_size(B, H, N, d, 0), "balanced")
+    st = Qf.stride()
+    p = _lib.BalancedFwdParams(
+        _lib.DFL_F32, Qf.data_ptr(), Kf.data_ptr(), _lib.ptr(Vf), st[0], st[1], st[2],
+        xf.data_ptr(), ef.data_ptr(), af.data_ptr(), rf.data_ptr(), _lib.ptr(mf),
+        B, H, N, d, K_iter,
+        xc.data_ptr(), _lib.ptr(hc), lu.data_ptr(), lv.data_ptr(), lz.data_ptr(), hist.data_ptr(),
+        _lib.DFL_STORAGE_AUTO)
+    rc = _lib.timed_launch("balanced_fwd", dev, lambda: lib.dfl_balanced_fwd(
+        ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
+    _lib.check(rc, "dfl_balanced_fwd")
+    if _lib.debug_checks():
+        _lib.check_workspace(ws, "dfl_balanced_fwd")
+    return (Qf, Kf, Vf, xf, ef, af, rf, mf, xc, hc, hist)
+
+
+def _run_backward(saved, K_iter, grad_xc, grad_hc):
+    Qf, Kf, Vf, xf, ef, af, rf, mf, xc, hc, hist = saved
+    dev = Qf.device
+    B, H, N, d = Qf.shape
+    gx = _f32c(grad_xc)
+    gh = _f32c(grad_hc) if Vf is not None else None
+    f32 = dict(device=dev, dtype=torch.float32)
+    dq = torch.empty(B, H, N, d, **f32)
+    dk = torch.empty(B, H, N, d, **f32)
+    dv = torch.empty(B, H, N, d, **f32) if Vf is not None else None
+    dx = torch.empty(B, N, 3, **f32)
+    da = torch.empty(H, **f32)
+    dr = torch.empty(H, **f32)
+    lib = _lib.load()
+    ws = _lib.workspace(dev, lib.dfl_balanced_workspace_size(B, H, N, d, 1), "balanced")
+    st = Qf.stride()
+    p = _lib.BalancedBwdParams(
+        _lib.DFL_F32, Qf.data_ptr(), Kf.data_ptr(), _lib.ptr(Vf), st[0], st[1], st[2],
+        xf.data_ptr(), ef.data_ptr(), af.data_ptr(), rf.data_ptr(), _lib.ptr(mf),
+        B, H, N, d, int(K_iter),
+        xc.data_ptr(), _lib.ptr(hc), hist.data_ptr(), _lib.ptr(gx), _lib.ptr(gh),
+        dq.data_ptr(), dk.data_ptr(), _lib.ptr(dv), dx.data_ptr(), da.data_ptr(), dr.data_ptr())
+    rc = _lib.timed_launch("balanced_bwd", dev, lambda: lib.dfl_balanced_bwd(
+        ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
+    _lib.check(rc, "dfl_balanced_bwd")
+    if _lib.debug_checks():
+        _lib.check_workspace(ws, "dfl_balanced_bwd")
+    return dq, dk, dv, dx, da, dr
+
+
+def _cast(t, like):
+    return None if t is None else t.to(like.dtype)
+
+
+class BalancedSinkhornFn(torch.autograd.Function):
+    """flash_sinkhorn_transport.py:287-373: returns x_centroid (B,H,N,3)."""
+
+    @staticmethod
+    def forward(ctx, Q_s, K_s, x_res, eps, alpha_h, r_h, K_iter, mask):
+        saved = _run_forward(Q_s, K_s, x_res, None, eps, alpha_h, r_h, K_iter, mask)
+        ctx.saved = saved
+        ctx.K_iter = int(K_iter)
+        ctx.dtypes = (Q_s, K_s, x_res, alpha_h, r_h)
+        return saved[8].to(Q_s.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_xc):
+        Q_s, K_s, x_res, alpha_h, r_h = ctx.dtypes
+        dq, dk, _, dx, da, dr = _run_backward(ctx.saved, ctx.K_iter, grad_xc, None)
+        ctx.saved = None
+        return (_cast(dq, Q_s), _cast(dk, K_s), _cast(dx, x_res), None, _cast(da, alpha_h), _cast(dr, r_h),
+                None, None)
+
+
+class BalancedSinkhornDualFn(torch.autograd.Function):
+    """flash_sinkhorn_transport.py:403-516: returns (x_centroid, h_centroid)."""
+
+    @staticmethod
+    def forward(ctx, Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask):
+        saved = _run_forward(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask)
+        ctx.saved = saved
+        ctx.K_iter = int(K_iter)
+        ctx.dtypes = (Q_s, K_s, x_res, V_h, alpha_h, r_h)
+        return saved[8].to(Q_s.dtype), saved[9].to(Q_s.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_xc, grad_hc):
+        Q_s, K_s, x_res, V_h, alpha_h, r_h = ctx.dtypes
+        dq, dk, dv, dx, da, dr = _run_backward(ctx.saved, ctx.K_iter, grad_xc, grad_hc)
+        ctx.saved = None
+        return (_cast(dq, Q_s), _cast(dk, K_s), _cast(dx, x_res), _cast(dv, V_h), None, _cast(da, alpha_h),
+                _cast(dr, r_h), None, None)
+
+
+def balanced_sinkhorn_transport(
+    Q_s: torch.Tensor, K_s: torch.Tensor, x_res: torch.Tensor,
+    eps: torch.Tensor, alpha_h: torch.Tensor, r_h: torch.Tensor,
+    K_iter: int = 20, mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Balanced Sinkhorn transport; returns the coordinate centroid (B, H, N, 3)
+    (flash_sinkhorn_transport.py:376-400)."""
+    cdtype = Q_s.dtype if Q_s.dtype == torch.float64 else torch.float32
+    Q_s = Q_s.to(cdtype)
+    K_s = K_s.to(cdtype)
+    return BalancedSinkhornFn.apply(Q_s, K_s, x_res, eps, alpha_h, r_h, K_iter, mask)
+
+
+def balanced_sinkhorn_transport_dual(
+    Q_s: torch.Tensor, K_s: torch.Tensor, x_res: torch.Tensor,
+    V_h: torch.Tensor,
+    eps: torch.Tensor, alpha_h: torch.Tensor, r_h: torch.Tensor,
+    K_iter: int = 20, mask: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Balanced Sinkhorn transport; returns (x_centroid (B,H,N,3), h_centroid
+    (B,H,N,D_V)) from one plan (flash_sinkhorn_transport.py:519-545)."""
+    cdtype = Q_s.dtype if Q_s.dtype == torch.float64 else torch.float32
+    Q_s = Q_s.to(cdtype)
+    K_s = K_s.to(cdtype)
+    V_f = V_h.to(cdtype)
+    return BalancedSinkhornDualFn.apply(Q_s, K_s, x_res, V_f, eps, alpha_h, r_h, K_iter, mask)

@@ -337,6 +337,86 @@ int dfl_dense_transport_fwd(const dfl_dense_transport_params* p, void* stream);
 int dfl_dense_transport_bwd(const dfl_dense_transport_params* p, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Balanced Sinkhorn transport (the coordinate / feature centroid of TokenOTBlock).
+ * Replaces BalancedSinkhornFn and BalancedSinkhornDualFn
+ * (src/deepfold/model/kernels/flash_sinkhorn_transport.py:287-373, 403-516; CPU
+ * form _sinkhorn_cpu :253-282).  Per (b,h), on the valid tokens of the sample:
+ *   C_ij = (1 - w_h)(1 - q_i.k_j) + w_h d_ij / (r + d_ij),  w_h = sigmoid(alpha_h),
+ *   r = max(|r_h|, 0.1), d_ij = max(|x_i - x_j|, 1e-8), L = -C / eps_h;
+ *   K_iter iterations of  v = lm - LSE_i(L + u),  u = lm - LSE_j(L + v)  (column
+ *   update first, u starts at 0, lm = -log n_valid);
+ *   P = exp(u + L + v - lm) (rows sum to 1);  x_centroid = P x,  h_centroid = P V.
+ * Inputs are fp32 (the reference casts to fp32 first).  q, k and v share the
+ * element strides stride_b/h/n (unit inner stride); v has the head dim d and may be
+ * NULL (coordinate centroid only, as balanced_sinkhorn_transport).  x_res (B,N,3)
+ * contiguous is required; mask (B,N) may be NULL.  Padded tokens produce zero
+ * outputs.  K_iter must be >= 1.
+ * The forward writes x_centroid (B,H,N,3), h_centroid (B,H,N,d) (if v given),
+ * log_u, log_v, log_z (B,H,N) and hist (K_iter,2,B,H,N): v after the column update
+ * and u after the row update of every iteration, which the backward needs (the
+ * reference saves the same history).
+ * The backward (exact gradient of the K unrolled iterations) takes the forward's
+ * inputs, its x_centroid / h_centroid / hist and grad_xc (B,H,N,3), grad_hc
+ * (B,H,N,d) (either may be NULL), and writes dq, dk (B,H,N,d), dx_res (B,N,3),
+ * dv (B,H,N,d) (may be NULL), dalpha_h and dr_h (H,).  eps receives no gradient,
+ * as in the reference.  dfl_balanced_workspace_size(..., backward = 0) is the
+ * forward's workspace (O(B*H*N) exchange words while a (b,h) fits in LDS);
+ * backward = 1 gives the size that serves both directions (it adds O(B*H*N*d)
+ * prepared operands).  The rules of dfl_sinkhorn_fwd's workspace apply.
+ */
+typedef struct dfl_balanced_fwd_params {
+  int dtype; /* DFL_F32 */
+  const void* q;
+  const void* k;
+  const void* v;
+  long long stride_b, stride_h, stride_n;
+  const float* x_res;
+  const float* eps;
+  const float* alpha_h;
+  const float* r_h;
+  const float* mask;
+  int B, H, N, d;
+  int K_iter;
+  float* x_centroid;
+  float* h_centroid;
+  float* log_u;
+  float* log_v;
+  float* log_z;
+  float* hist;
+  int storage;
+} dfl_balanced_fwd_params;
+
+typedef struct dfl_balanced_bwd_params {
+  int dtype; /* DFL_F32 */
+  const void* q;
+  const void* k;
+  const void* v;
+  long long stride_b, stride_h, stride_n;
+  const float* x_res;
+  const float* eps;
+  const float* alpha_h;
+  const float* r_h;
+  const float* mask;
+  int B, H, N, d;
+  int K_iter;
+  const float* x_centroid;
+  const float* h_centroid;
+  const float* hist;
+  const float* grad_xc;
+  const float* grad_hc;
+  float* dq;
+  float* dk;
+  float* dv;
+  float* dx_res;
+  float* dalpha_h;
+  float* dr_h;
+} dfl_balanced_bwd_params;
+
+size_t dfl_balanced_workspace_size(int B, int H, int N, int d, int backward);
+int dfl_balanced_fwd(const dfl_balanced_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

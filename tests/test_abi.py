@@ -84,7 +84,9 @@ def test_struct_layout_matches_c(lib_path):
                "dfl_a2t_params": _lib.A2TParams,
                "dfl_dense_sinkhorn_params": _lib.DenseSinkhornParams,
                "dfl_dense_sinkhorn_bwd_params": _lib.DenseSinkhornBwdParams,
-               "dfl_dense_transport_params": _lib.DenseTransportParams}
+               "dfl_dense_transport_params": _lib.DenseTransportParams,
+               "dfl_balanced_fwd_params": _lib.BalancedFwdParams,
+               "dfl_balanced_bwd_params": _lib.BalancedBwdParams}
     assert set(mirrors) == set(structs)
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for sname, fields in structs.items():
@@ -111,9 +113,9 @@ def test_struct_layout_matches_c(lib_path):
 
 def test_ops_refuse_cpu_tensors():
     import torch
-    from deepfold_amd import (atom_to_token_attn, compute_transport_output, conjugate_gradient, flash_atom_attn,
-                              flash_diffusion_attn, flash_sinkhorn, flash_sinkhorn_attn, sinkhorn_solve,
-                              token_to_atom_attn)
+    from deepfold_amd import (atom_to_token_attn, balanced_sinkhorn_transport, balanced_sinkhorn_transport_dual,
+                              compute_transport_output, conjugate_gradient, flash_atom_attn, flash_diffusion_attn,
+                              flash_sinkhorn, flash_sinkhorn_attn, sinkhorn_solve, token_to_atom_attn)
 
     B, H, N, d = 1, 2, 8, 4
     q = torch.randn(B, H, N, d)
@@ -132,7 +134,11 @@ def test_ops_refuse_cpu_tensors():
                  lambda: sinkhorn_solve(torch.zeros(B, H, N, N), torch.zeros(B, H, N), torch.zeros(B, H, N),
                                         torch.ones(H)),
                  lambda: compute_transport_output(q, q, torch.zeros(B, H, N), torch.zeros(B, H, N),
-                                                  torch.zeros(B, H, N, N), torch.ones(H))):
+                                                  torch.zeros(B, H, N, N), torch.ones(H)),
+                 lambda: balanced_sinkhorn_transport(q, q, torch.zeros(B, N, 3), torch.ones(H), torch.zeros(H),
+                                                     torch.ones(H)),
+                 lambda: balanced_sinkhorn_transport_dual(q, q, torch.zeros(B, N, 3), q, torch.ones(H),
+                                                          torch.zeros(H), torch.ones(H))):
         with pytest.raises(RuntimeError, match="GPU"):
             call()
 
