@@ -11,12 +11,15 @@ One "step" = one forward (flash_sinkhorn_attn) + one backward (autograd) of the
 layer, inputs resident in HBM.  Prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-                    [--workload cfg2|cfg5|cfg3|cfg4]
+                    [--workload cfg2|cfg5|cfg3|cfg4|balanced]
     python bench.py --rocpd-summary RESULTS.db    (CPU only: kernel table of a rocprofv3 run)
 
 Opt-in workloads: cfg5 = BASELINE configs[4] (B=1, H=16, N=4096, d=64, bf16,
 Dirichlet(5) marginals, eps=0.25, K=100, 30 CG steps; stream storage mode);
-cfg3 / cfg4 = the attention rows (configs[2] and [3]).
+cfg3 / cfg4 = the attention rows (configs[2] and [3]); balanced = the balanced
+Sinkhorn transport of TokenOTBlock (balanced_sinkhorn_transport_dual fwd+bwd at
+the trunk shape B=1, H=16, N=256, d=32, fp32, K=20; the timing configuration of
+the reference's tests/test_dual_transport.py).
 """
 
 from __future__ import annotations
@@ -36,6 +39,7 @@ PEAK_MFMA_BF16 = 2.5e15
 PEAK_HBM = 8.0e12
 # v_exp_f32 rate used by BASELINE.md's exp roof (quarter-rate estimate).
 PEAK_EXP_NOMINAL = 9.8e12
+PEAK_MFMA_F32 = 157.3e12
 
 SINKHORN = {
     "cfg2": dict(B=2, H=8, N=768, d=32, eps=0.5, K_iter=50, n_cg=20, seed=1002, ragged=True, dirichlet=False,
@@ -369,13 +373,125 @@ def bench_attention(args, which):
     print(json.dumps(out), flush=True)
 
 
+def balanced_workload(dev):
+    """TokenOTBlock's balanced transport (trunk_block.py:164-186): Q_s, K_s
+    L2-normalised, V_s, x_res, the trunk's eps buffer (0.5/1/2/4 per quarter of
+    the heads), alpha_h = -1 and r_h = 10 (their initial values), no padding,
+    K_ITER = 20; seed 1006."""
+    import torch
+    import torch.nn.functional as F
+
+    B, H, N, d, K = 1, 16, 256, 32, 20
+    g = torch.Generator().manual_seed(1006)
+    cpu = dict(Q=F.normalize(torch.randn(B, H, N, d, generator=g), dim=-1),
+               K=F.normalize(torch.randn(B, H, N, d, generator=g), dim=-1),
+               V=torch.randn(B, H, N, d, generator=g), x=torch.randn(B, N, 3, generator=g) * 3.0,
+               eps=torch.tensor([0.5] * 4 + [1.0] * 4 + [2.0] * 4 + [4.0] * 4),
+               alpha=torch.full((H,), -1.0), r=torch.full((H,), 10.0), mask=torch.ones(B, N),
+               gx=torch.randn(B, H, N, 3, generator=g), gh=torch.randn(B, H, N, d, generator=g))
+    t = {k: v.to(dev) for k, v in cpu.items()}
+    cfg = dict(B=B, H=H, N=N, d=d, K_iter=K)
+    return cfg, cpu, t
+
+
+def balanced_counts(cfg):
+    """Algorithmic work of one fwd+bwd (no padding: E = H N^2 per sample).
+    Forward: 2K LSE sweeps (QK^T, 2d flops / element) + output sweep (QK^T and
+    P V, 4d).  Backward: 2K+1 sweeps of cost recompute (2d) and one gradient
+    product (2d), plus the centroid sweeps' dhc.V (2d each) and P^T dhc (2d).
+    Exponentials: forward 2K+1, backward 4K+1 per element."""
+    E = cfg["B"] * cfg["H"] * cfg["N"] ** 2
+    d, K = cfg["d"], cfg["K_iter"]
+    f_fwd = E * d * (4 * K + 4)
+    f_bwd = E * d * (8 * K + 10)
+    return E, f_fwd, f_bwd, E * (2 * K + 1), E * (4 * K + 1)
+
+
+def balanced_cpu_baseline(cpu, cfg, reps=3):
+    """The oracle's restatement of the reference CPU path (_sinkhorn_cpu under
+    autograd, flash_sinkhorn_transport.py:253-282, 397-399) in float32 torch on
+    all host threads: forward + backward of the same workload, median of `reps`."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import balanced_transport as bt
+
+    threads = torch.get_num_threads()
+    times = []
+    for _ in range(reps + 1):
+        leaves = {k: cpu[k].clone().requires_grad_(True) for k in ("Q", "K", "x", "V", "alpha", "r")}
+        t0 = time.perf_counter()
+        xc, hc = bt.sinkhorn_cpu(leaves["Q"], leaves["K"], leaves["x"], cpu["eps"], leaves["alpha"], leaves["r"],
+                                 cpu["mask"], cfg["N"], cfg["K_iter"], V_h=leaves["V"])
+        ((xc * cpu["gx"]).sum() + (hc * cpu["gh"]).sum()).backward()
+        times.append(time.perf_counter() - t0)
+    times = sorted(times[1:])
+    return dict(value=round(times[len(times) // 2] * 1e3, 2), unit="ms/step", cores=threads, kind="port",
+                sample=f"oracle restatement of _sinkhorn_cpu (float32 torch autograd, {threads} threads), full "
+                       f"workload, median of {reps} after one warm-up")
+
+
+def bench_balanced(args):
+    import torch
+    from deepfold_amd import _lib, balanced_sinkhorn_transport_dual
+
+    dev = torch.device("cuda:0")
+    cfg, cpu, t = balanced_workload(dev)
+
+    def step():
+        q, k, x, v, a, r = (t[n].detach().requires_grad_(True) for n in ("Q", "K", "x", "V", "alpha", "r"))
+        xc, hc = balanced_sinkhorn_transport_dual(q, k, x, v, t["eps"], a, r, K_iter=cfg["K_iter"], mask=t["mask"])
+        torch.autograd.backward((xc, hc), (t["gx"], t["gh"]))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.launch_timings = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = {}
+    for name, s_, e_ in _lib.launch_timings:
+        per.setdefault(name, []).append(s_.elapsed_time(e_))
+    _lib.launch_timings = None
+    avg = {k: sum(v) / len(v) for k, v in per.items()}
+    ms = wall * 1e3 / args.steps
+    E, f_fwd, f_bwd, x_fwd, x_bwd = balanced_counts(cfg)
+    dom = max(avg, key=avg.get)
+    f_dom = f_fwd if dom == "balanced_fwd" else f_bwd
+    x_dom = x_fwd if dom == "balanced_fwd" else x_bwd
+    achieved = f_dom / (avg[dom] * 1e-3)
+    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_F32, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
+    out = {
+        "metric": "balanced Sinkhorn transport (dual) fwd+bwd ms/step @B1,H16,N256,d32 fp32 K20",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seed 1006): Q,K L2-normalised N(0,1), V, x*3, upstream grads N(0,1)",
+        "config": {"workload": "TokenOTBlock balanced transport, balanced_sinkhorn_transport_dual fwd+bwd",
+                   "B": cfg["B"], "H": cfg["H"], "N": cfg["N"], "d": cfg["d"], "K_iter": cfg["K_iter"],
+                   "valid_plan_elements": E},
+        "kernel_ms": {k: round(v, 4) for k, v in avg.items()},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
+                     "peak": PEAK_MFMA_F32 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_F32, 5),
+                     "traffic": profiled_traffic(dom, "balanced_tokenot_bench.md")},
+        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_NOMINAL,
+                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
+                         "step_t_roof_ms": t_roof * 1e3, "step_frac": t_roof * 1e3 / ms},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = balanced_cpu_baseline(cpu, cfg)
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg5", "cfg3", "cfg4"],
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg5", "cfg3", "cfg4", "balanced"],
                     help="cfg2 (default): the headline flash-Sinkhorn layer; cfg5: the N=4096 layer; "
                          "cfg3 / cfg4: attention rows")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -409,6 +525,8 @@ def main():
         return
     if args.workload in SINKHORN:
         bench_sinkhorn(args, args.workload)
+    elif args.workload == "balanced":
+        bench_balanced(args)
     else:
         bench_attention(args, args.workload)
 
