@@ -44,6 +44,11 @@ int balanced_max_tiles(int DP);
 hipError_t launch_balanced_prep(const BalPrepArgs& p, int DP, hipStream_t stream);
 hipError_t launch_balanced_bwd(const BalBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop);
 hipError_t launch_balanced_finalize(const BalBwdArgs& a, float* dx, float* dalpha, float* dr, hipStream_t stream);
+size_t unrolled_bwd_lds_bytes(int N);
+int unrolled_max_tiles(int DP);
+hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipStream_t stream);
+hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop);
+hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream);
 }  // namespace dfl
 
 namespace {
@@ -312,6 +317,35 @@ size_t bal_fwd_need(int B, int H, int N, int d, int storage) {
   return WS_HEADER + xch_words(B, H, N) * 8;
 }
 
+// Unrolled UOT backward workspace: header, exchange words, fp32 operand copies
+// (Q, K, V, gO rows; Q, K, gO transposed), vectors and partials.
+struct UnrWs {
+  size_t qp, kp, qt, kt, vp, gp, gt, dcoef, gxs, xs, dx_part, dpw_part, dw_part, total;
+};
+UnrWs unr_ws_layout(int B, int H, int N, int d) {
+  auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t np = np32(N);
+  const int DP = head_dim_pad(d) < 0 ? 64 : head_dim_pad(d);
+  const int G = group_size(B, H, N);
+  const size_t op = r256((size_t)B * H * np * DP * 4);
+  UnrWs w;
+  w.qp = r256(WS_HEADER + xch_words(B, H, N) * 8);
+  w.kp = w.qp + op;
+  w.qt = w.kp + op;
+  w.kt = w.qt + op;
+  w.vp = w.kt + op;
+  w.gp = w.vp + op;
+  w.gt = w.gp + op;
+  w.dcoef = w.gt + op;
+  w.gxs = w.dcoef + r256((size_t)B * H * np * 4);
+  w.xs = w.gxs + r256((size_t)B * H * 3 * np * 4);
+  w.dx_part = w.xs + r256((size_t)B * 3 * np * 4);
+  w.dpw_part = w.dx_part + r256((size_t)B * H * N * 3 * 4);
+  w.dw_part = w.dpw_part + r256((size_t)B * H * G * 68 * 4);
+  w.total = w.dw_part + r256((size_t)B * H * G * 4);
+  return w;
+}
+
 int check_balanced(int dtype, const void* q, const void* k, const float* x, const float* eps, const float* alpha,
                    const float* r, int B, int H, int N, int d, int K_iter, long long sn) {
   if (dtype != DFL_F32) return fail("balanced transport computes in fp32: dtype must be DFL_F32");
@@ -377,6 +411,7 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
   a.K_iter = p->K_iter; a.lam = p->lam; a.r0 = p->r_0;
   a.o_flat = p->o_flat; a.x_centroid = p->x_centroid; a.log_u = p->log_u; a.log_v = p->log_v;
   a.o_avg = p->o_avg; a.log_z = p->log_z; a.col_lse = p->col_lse;
+  a.hist = p->hist;
   return run_fwd(a, p->dtype == DFL_BF16, DP, p->storage, workspace, stream);
 }
 
@@ -756,6 +791,74 @@ int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t w
   if (e != hipSuccess) return hip_fail(e, "balanced backward launch");
   e = dfl::launch_balanced_finalize(a, p->dx_res, p->dalpha_h, p->dr_h, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "balanced backward finalize launch");
+  return 0;
+}
+
+size_t dfl_sinkhorn_unrolled_workspace_size(int B, int H, int N, int d) {
+  if (B <= 0 || H <= 0 || N <= 0 || d <= 0) return 0;
+  return unr_ws_layout(B, H, N, d).total;
+}
+
+int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_BF16 && p->dtype != DFL_F32) return fail("dtype must be DFL_BF16 or DFL_F32");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0 || p->d <= 0) return fail("B, H, N, d must be positive");
+  const int DP = head_dim_pad(p->d);
+  if (DP < 0) return fail("head dim d=%d > 64 is not supported", p->d);
+  if (p->K_iter < 1 || p->K_iter > 1000) return fail("K_iter=%d outside [1, 1000]", p->K_iter);
+  if (!p->q || !p->k || !p->v || !p->eps || !p->log_mu || !p->log_nu || !p->o_avg || !p->x_centroid || !p->log_u ||
+      !p->log_z || !p->hist || !p->grad_o)
+    return fail("required input is NULL");
+  if (!p->dq || !p->dk || !p->dv || !p->dlog_mu || !p->dlog_nu || (p->g && !p->dg))
+    return fail("output pointer is NULL");
+  if (p->stride_n < p->d) return fail("stride_n must be >= d (unit inner stride)");
+  if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
+  const UnrWs L = unr_ws_layout(p->B, p->H, p->N, p->d);
+  if (!workspace || workspace_bytes < L.total) return fail("workspace too small: need %zu bytes", L.total);
+  const int G = group_size(p->B, p->H, p->N);
+  const int max_nr = ((p->N + 15) / 16 + G - 1) / G;
+  if (max_nr > dfl::unrolled_max_tiles(DP))
+    return fail("unrolled backward: N=%d over %d workgroups per (b,h) exceeds %d tiles of 16 rows each", p->N, G,
+                dfl::unrolled_max_tiles(DP));
+  const size_t lds = dfl::unrolled_bwd_lds_bytes(p->N);
+  if (lds > LDS_LIMIT)
+    return fail("unrolled backward: N=%d needs %zu bytes of LDS per workgroup (limit %zu)", p->N, lds, LDS_LIMIT);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
+  dfl::UnrPrepArgs pr;
+  memset(&pr, 0, sizeof(pr));
+  pr.q = p->q; pr.k = p->k; pr.v = p->v; pr.g = p->g;
+  pr.sb = p->stride_b; pr.sh = p->stride_h; pr.sn = p->stride_n;
+  pr.x = p->x_res; pr.mask = p->mask; pr.o_avg = p->o_avg; pr.xc = p->x_centroid;
+  pr.grad_o = p->grad_o; pr.grad_xc = p->grad_xc;
+  pr.B = p->B; pr.H = p->H; pr.N = p->N; pr.d = p->d;
+  pr.qp = F(L.qp); pr.kp = F(L.kp); pr.qt = F(L.qt); pr.kt = F(L.kt);
+  pr.vp = F(L.vp); pr.gp = F(L.gp); pr.gt = F(L.gt);
+  pr.dcoef = F(L.dcoef); pr.gxs = F(L.gxs); pr.xs = F(L.xs); pr.dg = p->dg;
+  hipError_t e = dfl::launch_unrolled_prep(pr, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "unrolled backward prep launch");
+  dfl::UnrBwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d; a.K = p->K_iter;
+  a.eps = p->eps; a.lam = p->lam; a.r0 = p->r_0; a.mask = p->mask; a.hist = p->hist;
+  a.log_mu = p->log_mu; a.log_nu = p->log_nu; a.log_u = p->log_u; a.log_z = p->log_z; a.v_init = p->log_v_init;
+  a.bins = p->pos_bins; a.pos_w = p->pos_weight; a.w_dist = p->w_dist;
+  a.has_geo = (p->x_res && p->w_dist) ? 1 : 0;
+  a.qp = pr.qp; a.kp = pr.kp; a.qt = pr.qt; a.kt = pr.kt; a.vp = pr.vp; a.gp = pr.gp; a.gt = pr.gt;
+  a.dcoef = pr.dcoef; a.gxs = pr.gxs; a.xs = pr.xs;
+  a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dlog_mu = p->dlog_mu; a.dlog_nu = p->dlog_nu;
+  a.dv_init = p->dlog_v_init;
+  a.dx_part = F(L.dx_part); a.dpw_part = F(L.dpw_part); a.dw_part = F(L.dw_part);
+  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
+  a.G = G;
+  a.salt = next_salt();
+  e = dfl::launch_unrolled_bwd(a, DP, lds, (hipStream_t)stream, G > 1);
+  if (e != hipSuccess) return hip_fail(e, "unrolled backward launch");
+  e = dfl::launch_unrolled_finalize(a, p->x_res ? p->dx_res : nullptr, p->dpos_weight, p->dw_dist,
+                                    (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "unrolled backward finalize launch");
   return 0;
 }
 

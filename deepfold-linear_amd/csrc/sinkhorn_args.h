@@ -53,6 +53,7 @@ struct SinkFwdArgs {
   const float* alpha;  // (H,)
   const float* r_h;    // (H,)
   float* hist;         // (K_iter, 2, B*H, N): v after the column update, u after the row update
+                       // (both modes; null = not recorded)
 };
 
 // Backward (flash_sinkhorn_attn.py:246-667 semantics, plus analytic mode / CG).
@@ -140,6 +141,66 @@ struct BalBwdArgs {
   uint32_t* err;
   int G;
   uint32_t salt;
+};
+
+// Unrolled backward of the UOT flash-Sinkhorn (the reference's GPU-path backward,
+// sinkhorn_kernel.py:2085-2382): prepared fp32 operands as for the balanced one.
+struct UnrBwdArgs {
+  int B, H, N, d, K;
+  const float* eps;      // (H,)
+  float lam, r0;
+  const float* mask;     // (B,N) or null
+  const float* hist;     // (K, 2, B*H, N): v after the column update, u after the row update
+  const float* log_mu;   // (B,H,N)
+  const float* log_nu;
+  const float* log_u;    // (B,H,N) forward outputs: final u and LSE_j(u + L + v)
+  const float* log_z;
+  const float* v_init;   // (B,H,N) or null (zeros)
+  const int* bins;       // (B,N,N) or null
+  const float* pos_w;    // (H,68) or null
+  const float* w_dist;   // (H,) or null
+  int has_geo;           // geometry term present (x given and w_dist given)
+  const float* qp;       // [B*H][Np][DP] fp32 copies, zero on masked rows / padding
+  const float* kp;
+  const float* qt;       // [B*H][DP][Np]
+  const float* kt;
+  const float* vp;       // V rows
+  const float* gp;       // gO rows (gO = sigma(G) dO)
+  const float* gt;       // gO transposed
+  const float* dcoef;    // [B*H][Np] D_i = gO_i.O_i + dxc_i.xc_i
+  const float* gxs;      // [B*H][3][Np] grad x_c
+  const float* xs;       // [B][3][Np] coordinates
+  float* dq;             // (B,H,N,d) fp32
+  float* dk;
+  float* dv;
+  float* dlog_mu;        // (B,H,N)
+  float* dlog_nu;
+  float* dv_init;        // (B,H,N) or null
+  float* dx_part;        // (B,H,N,3)
+  float* dpw_part;       // (B*H*G, 68)
+  float* dw_part;        // (B*H*G)
+  uint64_t* xch;
+  uint32_t* err;
+  int G;
+  uint32_t salt;
+};
+
+struct UnrPrepArgs {
+  const void* q;  // (B,H,N,d) bf16 or fp32, element strides sb/sh/sn
+  const void* k;
+  const void* v;
+  const void* g;  // gate logits or null
+  long long sb, sh, sn;
+  const float* x;        // (B,N,3) or null
+  const float* mask;     // (B,N) or null
+  const float* o_avg;    // (B,H,N,d) forward output
+  const float* xc;       // (B,H,N,3) forward output
+  const float* grad_o;   // (B,N,H*d) fp32
+  const float* grad_xc;  // (B,H,N,3) or null
+  int B, H, N, d;
+  float* qp; float* kp; float* qt; float* kt; float* vp; float* gp; float* gt;
+  float* dcoef; float* gxs; float* xs;
+  float* dg;             // (B,H,N,d) or null (no gate)
 };
 
 struct BalPrepArgs {

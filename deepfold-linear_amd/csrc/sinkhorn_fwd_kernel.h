@@ -313,7 +313,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
         if (i < n) {
           const float u = kappa * (lmu_l[q] - l2 * LN2);
           xch_put(xu + i, u, tag);
-          if (bal) a.hist[((size_t)(2 * it + 1) * a.B * a.H + bh) * N + i] = valid[i] ? u : 0.f;
+          if (a.hist) a.hist[((size_t)(2 * it + 1) * a.B * a.H + bh) * N + i] = valid[i] ? u : 0.f;
         }
       };
       sweep(true, online, lse_r, nullptr, &s_du, pub);
@@ -334,7 +334,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
           const float v = kappa * (lnu_l[q] - l2 * LN2);
           xch_put(xv + j, v, tag);
           if (last && valid[j] && a.col_lse) a.col_lse[bh * N + j] = l2 * LN2;
-          if (bal) a.hist[((size_t)(2 * it) * a.B * a.H + bh) * N + j] = valid[j] ? v : 0.f;
+          if (a.hist) a.hist[((size_t)(2 * it) * a.B * a.H + bh) * N + j] = valid[j] ? v : 0.f;
         }
       };
       sweep(false, online, lse_c, nullptr, &s_dv, pub);

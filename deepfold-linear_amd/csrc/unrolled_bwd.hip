@@ -1,0 +1,603 @@
+// Unrolled backward of the UOT flash-Sinkhorn on gfx950 (persistent per-(b,h)
+// workgroup groups, fp32 sweeps).
+//
+// Restates the GPU-path backward of vv137/deepfold-linear's FlashSinkhornFunction
+// (src/deepfold/model/kernels/sinkhorn_kernel.py:2085-2382; its dense autograd
+// check is tests/test_triton_fallback_consistency.py:312-430): the exact gradient
+// through the K executed iterations of
+//   u^k_i = kappa (lmu_i - LSE_j(L_ij + v^{k-1}_j))   (v^{-1} = v_init or 0)   row update
+//   v^k_j = kappa (lnu_j - LSE_i(L_ij + u^k_i))                              column update
+//   P_ij  = exp(L_ij + v^{K-1}_j - LSE_j(L_ij + v^{K-1}_j))  (row softmax; u cancels)
+//   O = P V (gated by sigma(G) outside), xc = P x,
+//   L = -C / eps,  C = -q.k / sqrt(d) + pw_h[bins] + w_dist d / (r0 + d),
+// on the valid tokens of each sample.  With the plans of each half-iteration
+//   s^{R,k} = exp(L + v^{k-1}_j + u^k_i / kappa - lmu_i)   (rows sum to 1)
+//   s^{C,k} = exp(L + u^k_i + v^k_j / kappa - lnu_j)       (columns sum to 1)
+// and D_i = gO_i.O_i + dxc_i.xc_i, W0 = -P (gO_i.V_j + dxc_i.x_j - D_i):
+//   gl_v^{K-1} = -sum_i W0_ij,                 gl_u^k = -kappa s^{C,k} gl_v^k,
+//   gl_v^{k-1} = -kappa (s^{R,k})^T gl_u^k,     d lmu = kappa sum_k gl_u^k, d lnu = kappa sum_k gl_v^k,
+//   eps dC = W0 + kappa sum_k [ s^{C,k} diag(gl_v^k) + diag(gl_u^k) s^{R,k} ],
+//   d v_init = gl_v^{-1}.
+// As in the balanced backward (balanced_bwd.hip), each term is produced once in a
+// row-owned sweep (dQ, row ends of dx, d pos_weight, d w_dist) and once in a
+// column-owned sweep (dK, column ends of dx).  Sweep order:
+//   CS_cent: P, W0 -> gl_v^{K-1}, dV, P^T dxc
+//   RS(k), k = K-1..0: s^{C,k} gl_v^k (+ diag(gl_u^{k+1}) s^{R,k+1} for k < K-1, W0 for k = K-1) -> gl_u^k
+//   CS(k), k = K-1..0: diag(gl_u^k) s^{R,k} + s^{C,k} diag(gl_v^k) -> gl_v^{k-1}
+//   RS(-1): diag(gl_u^0) s^{R,0}
+// 2K + 2 sweeps, at most two exponentials per element each.
+#include <type_traits>
+
+#include "sinkhorn_bwd_kernel.h"
+
+namespace dfl {
+
+constexpr int UNR_NT = 512;
+constexpr int UNR_NW = UNR_NT / WAVE;
+template <int DP> constexpr int unr_maxt() { return DP <= 32 ? 2 : 1; }
+constexpr int UNR_MAXT_ANY = 2;
+
+__host__ __device__ inline int unr_wpt(int nr) { return nr >= UNR_NW ? 1 : UNR_NW / nr; }
+
+// Prep: one thread per (b, h, i, c), c < DP.  fp32 copies of Q, K, V, gO and gO^T,
+// D, grad x_c, coordinates; dG = sigma(1 - sigma) O dO (flash_sinkhorn_attn.py:278-292).
+template <typename T, int DP>
+__global__ void __launch_bounds__(256) unrolled_prep_kernel(UnrPrepArgs p) {
+  const int N = p.N, d = p.d;
+  const int Np = ((N + 31) / 32) * 32;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t row = e / DP;
+  const int c = (int)(e % DP);
+  const int bh = (int)(row / Np), i = (int)(row % Np);
+  if (bh >= p.B * p.H) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const bool ok = i < N && (p.mask ? p.mask[(size_t)b * N + i] > 0.5f : true);
+  const size_t off = (size_t)b * p.sb + (size_t)h * p.sh + (size_t)i * p.sn + c;
+  float qv = 0.f, kv = 0.f, vv = 0.f, go = 0.f, oa = 0.f;
+  if (ok && c < d) {
+    qv = to_f32(reinterpret_cast<const T*>(p.q)[off]);
+    kv = to_f32(reinterpret_cast<const T*>(p.k)[off]);
+    vv = to_f32(reinterpret_cast<const T*>(p.v)[off]);
+    const float dO = p.grad_o[((size_t)b * N + i) * p.H * d + (size_t)h * d + c];
+    oa = p.o_avg[((size_t)bh * N + i) * d + c];
+    float s = 1.f;
+    if (p.g) {
+      s = 1.f / (1.f + __expf(-to_f32(reinterpret_cast<const T*>(p.g)[off])));
+      p.dg[((size_t)bh * N + i) * d + c] = s * (1.f - s) * oa * dO;
+    }
+    go = s * dO;
+  } else if (p.g && i < N && c < d) {
+    p.dg[((size_t)bh * N + i) * d + c] = 0.f;
+  }
+  p.qp[row * DP + c] = qv;
+  p.kp[row * DP + c] = kv;
+  p.vp[row * DP + c] = vv;
+  p.gp[row * DP + c] = go;
+  p.qt[((size_t)bh * DP + c) * Np + i] = qv;
+  p.kt[((size_t)bh * DP + c) * Np + i] = kv;
+  p.gt[((size_t)bh * DP + c) * Np + i] = go;
+  float part = go * oa;
+#pragma unroll
+  for (int o = DP / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, WAVE);
+  if (c < 3) p.gxs[((size_t)bh * 3 + c) * Np + i] = (ok && p.grad_xc) ? p.grad_xc[((size_t)bh * N + i) * 3 + c] : 0.f;
+  if (c < 3 && h == 0) p.xs[((size_t)b * 3 + c) * Np + i] = (p.x && i < N) ? p.x[((size_t)b * N + i) * 3 + c] : 0.f;
+  if (c == 0) {
+    if (ok && p.grad_xc)
+      for (int t = 0; t < 3; ++t) part += p.grad_xc[((size_t)bh * N + i) * 3 + t] * p.xc[((size_t)bh * N + i) * 3 + t];
+    p.dcoef[(size_t)bh * Np + i] = ok ? part : 0.f;
+  }
+}
+
+// Finalize: dx = sum_h dx_part; d pos_weight, d w_dist = sums of the workgroup partials.
+__global__ void __launch_bounds__(256) unrolled_finalize_kernel(UnrBwdArgs a, float* dx, float* dpw, float* dw) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int nx = a.B * a.N * 3;
+  if (dx && e < nx) {
+    const int b = e / (a.N * 3), r = e % (a.N * 3);
+    float s = 0.f;
+    for (int h = 0; h < a.H; ++h) s += a.dx_part[((size_t)b * a.H + h) * a.N * 3 + r];
+    dx[e] = s;
+  }
+  if (dpw && e < a.H * 68) {
+    const int h = e / 68, k = e % 68;
+    float s = 0.f;
+    for (int b = 0; b < a.B; ++b)
+      for (int m = 0; m < a.G; ++m) s += a.dpw_part[(((size_t)b * a.H + h) * a.G + m) * 68 + k];
+    dpw[e] = s;
+  }
+  if (dw && e < a.H) {
+    float s = 0.f;
+    for (int b = 0; b < a.B; ++b)
+      for (int m = 0; m < a.G; ++m) s += a.dw_part[((size_t)b * a.H + e) * a.G + m];
+    dw[e] = s;
+  }
+}
+
+template <int DP>
+__global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
+  using M = Mfma<float, DP>;
+  constexpr int NC = DP / 16;
+  constexpr int NW = UNR_NW;
+  constexpr int MAXT = unr_maxt<DP>();
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_flag, s_tmp;
+  __shared__ float s_pw[68];   // pos_weight of this head (natural units)
+  __shared__ float s_dpw[68];  // d pos_weight partial of this workgroup (times eps)
+  int grp, member;
+  if (!group_of(a.B * a.H, a.G, grp, member)) return;
+  const int b = grp / a.H, h = grp % a.H;
+  const int N = a.N, d = a.d, K = a.K;
+  const int Np = ((N + 31) / 32) * 32;
+  const int BH = a.B * a.H;
+  const size_t bh = (size_t)grp;
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, g = lane >> 4;
+  if (tid == 0) s_flag = 0;
+  if (tid < 68) {
+    s_pw[tid] = a.pos_w ? a.pos_w[h * 68 + tid] : 0.f;
+    s_dpw[tid] = 0.f;
+  }
+  if (blockIdx.x == 0 && tid == 0)
+    __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- LDS carve-up (must match unrolled_bwd_lds_bytes)
+  unsigned char* valid = smem;
+  float* xs0 = reinterpret_cast<float*>(smem + ((Np + 15) / 16) * 16);
+  float* xs1 = xs0 + Np;
+  float* xs2 = xs1 + Np;
+  float* gx0 = xs2 + Np;
+  float* gx1 = gx0 + Np;
+  float* gx2 = gx1 + Np;
+  float* dcf = gx2 + Np;
+  float* GLU = dcf + Np;
+  float* GLV = GLU + Np;
+  float* STA = GLV + Np;  // streamed exponent terms of term 1 (or of P in CS_cent)
+  float* STB = STA + Np;  // streamed exponent terms of term 2 (or of P in RS(K-1))
+  float* sred = STB + Np;                        // [NW][MAXT][16]
+  float* spart = sred + NW * UNR_MAXT_ANY * 16;  // [NW][16*64] part hand-over
+  float* sscal = spart + NW * 16 * 64;           // [NW][2]
+
+  const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &s_tmp);
+  const int n_tiles = (n + 15) / 16;
+  int t0, t1;
+  stripe(n_tiles, member, a.G, t0, t1);
+  const int nr = t1 - t0;
+  for (int i = n_tiles * 16 + member; i < N; i += a.G) {
+    for (int c = tid; c < d; c += UNR_NT) {
+      a.dq[(bh * N + i) * d + c] = 0.f;
+      a.dk[(bh * N + i) * d + c] = 0.f;
+      a.dv[(bh * N + i) * d + c] = 0.f;
+    }
+    if (tid < 3) a.dx_part[(bh * N + i) * 3 + tid] = 0.f;
+    if (tid == 0) {
+      a.dlog_mu[bh * N + i] = 0.f;
+      a.dlog_nu[bh * N + i] = 0.f;
+      if (a.dv_init) a.dv_init[bh * N + i] = 0.f;
+    }
+  }
+  if (n == 0 || nr <= 0) {
+    if (tid < 68) a.dpw_part[(bh * a.G + member) * 68 + tid] = 0.f;
+    if (tid == 0) a.dw_part[bh * a.G + member] = 0.f;
+    return;  // owns nothing; no other member waits on it
+  }
+  for (int i = tid; i < Np; i += UNR_NT) {
+    xs0[i] = a.xs[((size_t)b * 3 + 0) * Np + i];
+    xs1[i] = a.xs[((size_t)b * 3 + 1) * Np + i];
+    xs2[i] = a.xs[((size_t)b * 3 + 2) * Np + i];
+    gx0[i] = a.gxs[(bh * 3 + 0) * Np + i];
+    gx1[i] = a.gxs[(bh * 3 + 1) * Np + i];
+    gx2[i] = a.gxs[(bh * 3 + 2) * Np + i];
+    dcf[i] = a.dcoef[bh * Np + i];
+    GLU[i] = 0.f;
+    GLV[i] = 0.f;
+  }
+  __syncthreads();
+  const float eps = a.eps[h];
+  const float kappa = a.lam / (a.lam + eps);
+  const float ik = 1.f / kappa;
+  const float sc = LOG2E / (sqrtf((float)d) * eps);
+  const float bsc = -LOG2E / eps;  // bias (pw + w d/(r0 + d)) -> log2 logit
+  const float wd = a.w_dist ? a.w_dist[h] : 0.f;
+  const bool geo = a.has_geo != 0 && wd != 0.f;
+  const bool use_bins = a.bins != nullptr;
+  const int* bins_b = use_bins ? a.bins + (size_t)b * N * N : nullptr;
+  const float r0 = a.r0;
+  const int r_lo = t0 * 16;
+  const float* hist = a.hist;
+  const size_t bhN = bh * N;
+  auto Un = [&](int k, int i) { return hist[((size_t)(2 * k + 1) * BH + bh) * N + i]; };  // natural
+  auto Vn = [&](int k, int j) {
+    if (k >= 0) return hist[((size_t)(2 * k) * BH + bh) * N + j];
+    return a.v_init ? a.v_init[bhN + j] : 0.f;
+  };
+
+  const int wpt = unr_wpt(nr);
+  const int nts = NW / wpt;
+  const int ts = wave / wpt, part = wave % wpt;
+  const int n_pairs = (n_tiles + 1) / 2;
+  const float* qp = a.qp + bh * Np * DP;
+  const float* kp = a.kp + bh * Np * DP;
+  const float* qt = a.qt + bh * DP * Np;
+  const float* kt = a.kt + bh * DP * Np;
+  const float* vp = a.vp + bh * Np * DP;
+  const float* gp = a.gp + bh * Np * DP;
+  const float* gt = a.gt + bh * DP * Np;
+
+  f32x4 dQa[MAXT][NC], dKa[MAXT][NC];
+  float gbx[MAXT], gby[MAXT], gbz[MAXT], xt0[MAXT], xt1[MAXT], xt2[MAXT], dmu[MAXT], dnu[MAXT];
+#pragma unroll
+  for (int s = 0; s < MAXT; ++s) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) dQa[s][c] = dKa[s][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    gbx[s] = gby[s] = gbz[s] = xt0[s] = xt1[s] = xt2[s] = dmu[s] = dnu[s] = 0.f;
+  }
+  float s_w = 0.f;  // sum W * cg (d w_dist, row-owned sweeps)
+
+  uint64_t* xgu = a.xch + bh * 2 * (size_t)Np;
+  uint64_t* xgv = xgu + Np;
+  const uint32_t salt = a.salt << 12;
+  uint32_t phase = 0;
+
+  auto write_rows = [&](f32x4 (&acc)[MAXT][NC], float* out, float scale) {
+    __syncthreads();
+    if (wpt > 1 && part > 0 && ts < nr) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) spart[(size_t)wave * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)] = acc[0][c][r];
+    }
+    __syncthreads();
+    if (part == 0) {
+#pragma unroll
+      for (int s = 0; s < MAXT; ++s) {
+        const int rt = ts + nts * s;
+        if (rt >= nr) continue;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float v = acc[s][c][r];
+            for (int p = 1; p < wpt; ++p) v += spart[(size_t)(wave + p) * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)];
+            const int row = (t0 + rt) * 16 + 4 * g + r, col = c * 16 + (lane & 15);
+            if (row < N && col < d) out[(bh * N + row) * d + col] = (row < n && valid[row]) ? scale * v : 0.f;
+          }
+      }
+    }
+  };
+
+  // Reduction of a per-(tile slot, lane) value over lane groups and parts into
+  // `dst_fn(local row q, value)` for q < nr*16 (called by the owning threads).
+  auto combine_rows = [&](const float (&val)[MAXT], auto dst_fn) {
+#pragma unroll
+    for (int s = 0; s < MAXT; ++s) {
+      const float r = sum_groups(val[s]);
+      if (lane < 16) sred[(wave * MAXT + s) * 16 + lane] = r;
+    }
+    __syncthreads();
+    for (int q = tid; q < nr * 16; q += UNR_NT) {
+      const int rt = q >> 4, l16 = q & 15;
+      const int s = rt / nts, tsl = rt % nts;
+      float v = 0.f;
+      for (int p = 0; p < wpt; ++p) v += sred[((tsl * wpt + p) * MAXT + s) * 16 + l16];
+      dst_fn(q, v);
+    }
+  };
+
+  // One sweep.  ROW: resident rows i (streamed j), else resident columns j
+  // (streamed i).  CENT: the centroid sweep of that orientation.  Index k as in
+  // the header comment (CS_cent uses k = K).
+  auto sweep = [&](auto row_tag, auto cent_tag, int k) -> bool {
+    constexpr bool ROW = decltype(row_tag)::value;
+    constexpr bool CENT = decltype(cent_tag)::value;
+    const bool use_c = ROW ? k >= 0 : !CENT;     // term 1 (recurrence term)
+    const bool term2 = ROW ? k <= K - 2 : !CENT;  // term 2 (mirror term)
+    const bool publish = ROW ? k >= 0 : (CENT || k >= 1);
+    __syncthreads();  // readers of STA / STB and of the gathered vectors are done
+    for (int i = tid; i < Np; i += UNR_NT) {
+      float sa = NEG_BIG, sb = NEG_BIG;
+      if (i < n && valid[i]) {
+        if (ROW) {  // streamed columns j
+          if (use_c) sa = (Vn(k, i) * ik - a.log_nu[bhN + i]) * LOG2E;  // s^{C,k}
+          if (term2 || CENT) sb = Vn(k, i) * LOG2E;                       // s^{R,k+1} or P
+        } else {    // streamed rows i
+          if (CENT) sa = (a.log_u[bhN + i] - a.log_z[bhN + i]) * LOG2E;   // P
+          else {
+            sa = (Un(k, i) * ik - a.log_mu[bhN + i]) * LOG2E;             // s^{R,k}
+            sb = Un(k, i) * LOG2E;                                         // s^{C,k}
+          }
+        }
+      }
+      STA[i] = sa;
+      STB[i] = sb;
+    }
+    __syncthreads();
+    const float* STC = ROW ? GLV : GLU;  // streamed recurrence coefficients
+    const float* Sop = ROW ? kp : qp;
+    const float* Sot = ROW ? kt : qt;
+    const float* Rop = ROW ? qp : kp;
+
+    typename M::Frag bf[MAXT], cbf[MAXT];
+    float ra[MAXT], rb[MAXT], dd[MAXT], xr0[MAXT], xr1[MAXT], xr2[MAXT], Dr[MAXT], gr0[MAXT], gr1[MAXT], gr2[MAXT];
+    float red[MAXT];
+    f32x4 gVa[MAXT][NC];
+#pragma unroll
+    for (int s = 0; s < MAXT; ++s) {
+      const int rt = ts + nts * s;
+      const int ri = (t0 + min(rt, nr - 1)) * 16 + (lane & 15);
+      const bool ok = rt < nr && ri < n && valid[ri];
+      M::load(bf[s], Rop + (size_t)ri * DP, lane);
+      if (CENT) M::load(cbf[s], (ROW ? gp : vp) + (size_t)ri * DP, lane);
+      ra[s] = rb[s] = NEG_BIG;
+      dd[s] = 0.f;
+      if (ok) {
+        if (ROW) {  // resident rows i
+          if (use_c) ra[s] = Un(k, ri) * LOG2E;                                             // s^{C,k}
+          if (CENT) rb[s] = (a.log_u[bhN + ri] - a.log_z[bhN + ri]) * LOG2E;                // P
+          else if (term2) rb[s] = (Un(k + 1, ri) * ik - a.log_mu[bhN + ri]) * LOG2E;        // s^{R,k+1}
+          if (term2) dd[s] = kappa * GLU[ri];
+        } else {    // resident columns j
+          if (CENT) ra[s] = Vn(K - 1, ri) * LOG2E;                                          // P
+          else {
+            ra[s] = Vn(k - 1, ri) * LOG2E;                                                  // s^{R,k}
+            rb[s] = (Vn(k, ri) * ik - a.log_nu[bhN + ri]) * LOG2E;                          // s^{C,k}
+            dd[s] = kappa * GLV[ri];
+          }
+        }
+      }
+      xr0[s] = xs0[ri];
+      xr1[s] = xs1[ri];
+      xr2[s] = xs2[ri];
+      Dr[s] = gr0[s] = gr1[s] = gr2[s] = 0.f;
+      if (CENT && ROW) {
+        Dr[s] = dcf[ri];
+        gr0[s] = gx0[ri];
+        gr1[s] = gx1[ri];
+        gr2[s] = gx2[ri];
+      }
+      red[s] = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) gVa[s][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (ts < nts) {
+      for (int sp = part; sp < n_pairs; sp += wpt) {
+#pragma unroll
+        for (int s = 0; s < MAXT; ++s) {
+          const int rt = ts + nts * s;
+          if (rt >= nr) continue;
+          const int ri = (t0 + rt) * 16 + (lane & 15);
+          f32x4 wop[2], pop[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int st = 2 * sp + hh;
+            const int o = st * 16 + 4 * g;
+            typename M::Frag af;
+            M::load(af, Sop + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            f32x4 t = zero;
+            if (CENT) {
+              typename M::Frag cf;
+              M::load(cf, (ROW ? vp : gp) + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+              t = M::qk(cf, cbf[s], zero);
+            }
+            const f32x4 x = M::qk(af, bf[s], zero);
+            const f32x4 sa = *reinterpret_cast<const f32x4*>(STA + o);
+            const f32x4 sb = *reinterpret_cast<const f32x4*>(STB + o);
+            const f32x4 scf = use_c ? *reinterpret_cast<const f32x4*>(STC + o) : zero;
+            const f32x4 sx0 = *reinterpret_cast<const f32x4*>(xs0 + o);
+            const f32x4 sx1 = *reinterpret_cast<const f32x4*>(xs1 + o);
+            const f32x4 sx2 = *reinterpret_cast<const f32x4*>(xs2 + o);
+            f32x4 sg0 = zero, sg1 = zero, sg2 = zero, sD = zero;
+            if (CENT && !ROW) {
+              sg0 = *reinterpret_cast<const f32x4*>(gx0 + o);
+              sg1 = *reinterpret_cast<const f32x4*>(gx1 + o);
+              sg2 = *reinterpret_cast<const f32x4*>(gx2 + o);
+              sD = *reinterpret_cast<const f32x4*>(dcf + o);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int sj = min(o + e, N - 1);  // streamed index (clamped for the bins read)
+              const int ii = ROW ? min(ri, N - 1) : sj, jj = ROW ? sj : min(ri, N - 1);
+              float bias = 0.f, cg = 0.f, dist = 1.f;
+              const float dx = xr0[s] - sx0[e], dy = xr1[s] - sx1[e], dz = xr2[s] - sx2[e];
+              if (geo) {
+                dist = fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-8f);
+                cg = dist / (r0 + dist);
+                bias = wd * cg;
+              }
+              int bin = -1;
+              if (use_bins) {
+                bin = bins_b[(size_t)ii * N + jj];
+                if ((unsigned)bin < 68u) bias += s_pw[bin];
+                else bin = -1;
+              }
+              const float lg = __builtin_fmaf(x[e], sc, bsc * bias);
+              const float e1 = (use_c || (CENT && !ROW)) ? fast_exp2(lg + sa[e] + ra[s]) : 0.f;
+              const float e2 = (term2 || (CENT && ROW)) ? fast_exp2(lg + sb[e] + rb[s]) : 0.f;
+              float W = 0.f;
+              if (use_c) {
+                const float t1 = kappa * e1 * scf[e];
+                W = t1;
+                red[s] -= t1;
+              }
+              if (term2) W = __builtin_fmaf(e2, dd[s], W);
+              if (CENT) {
+                const float P = ROW ? e2 : e1;
+                float dT = t[e];
+                if (ROW) dT += gr0[s] * sx0[e] + gr1[s] * sx1[e] + gr2[s] * sx2[e];
+                else dT += sg0[e] * xr0[s] + sg1[e] * xr1[s] + sg2[e] * xr2[s];
+                const float qv = P * (dT - (ROW ? Dr[s] : sD[e]));
+                W -= qv;
+                if (!ROW) {
+                  red[s] += qv;
+                  xt0[s] = __builtin_fmaf(P, sg0[e], xt0[s]);
+                  xt1[s] = __builtin_fmaf(P, sg1[e], xt1[s]);
+                  xt2[s] = __builtin_fmaf(P, sg2[e], xt2[s]);
+                  pop[hh][e] = P;
+                }
+              }
+              wop[hh][e] = W;
+              if (geo) {
+                const float om = 1.f - cg;
+                const float f = W * om * om / dist;
+                gbx[s] = __builtin_fmaf(f, dx, gbx[s]);
+                gby[s] = __builtin_fmaf(f, dy, gby[s]);
+                gbz[s] = __builtin_fmaf(f, dz, gbz[s]);
+                if (ROW) s_w = __builtin_fmaf(W, cg, s_w);
+              }
+              if (ROW && bin >= 0 && W != 0.f) atomicAdd(&s_dpw[bin], W);
+            }
+          }
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const float* vt_row = Sot + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32;
+            if (ROW) dQa[s][c] = M::pv(wop[0], wop[1], vt_row, lane, dQa[s][c]);
+            else dKa[s][c] = M::pv(wop[0], wop[1], vt_row, lane, dKa[s][c]);
+            if (CENT && !ROW)
+              gVa[s][c] = M::pv(pop[0], pop[1], gt + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, gVa[s][c]);
+          }
+        }
+      }
+    }
+    // recurrence output (gl_u^k for RS, gl_v^{k-1} or g_v for CS) of my rows
+    uint64_t* buf = ROW ? xgu : xgv;
+    ++phase;
+    const uint32_t tag = salt | phase;
+    combine_rows(red, [&](int q, float v) {
+      const int i = r_lo + q;
+      if (i >= n) return;
+      const bool ok = valid[i];
+      if (publish) xch_put(buf + i, v, tag);
+      if (!ok) return;
+      if (ROW) {
+        if (k >= 0) a.dlog_mu[bhN + i] = (k == K - 1 ? 0.f : a.dlog_mu[bhN + i]) + kappa * v;
+      } else if (CENT || k >= 1) {
+        a.dlog_nu[bhN + i] = (CENT ? 0.f : a.dlog_nu[bhN + i]) + kappa * v;
+      } else if (a.dv_init) {
+        a.dv_init[bhN + i] = v;
+      }
+    });
+    if (publish) {
+      if (!gather_vector(buf, n, Np, tag, ROW ? GLU : GLV, valid, a.err, &s_flag)) return false;
+    } else {
+      __syncthreads();
+    }
+    if (CENT && !ROW) write_rows(gVa, a.dv, 1.f);
+    return true;
+  };
+
+  using TRUE_ = std::integral_constant<bool, true>;
+  using FALSE_ = std::integral_constant<bool, false>;
+  if (!sweep(FALSE_{}, TRUE_{}, K)) return;
+  if (!sweep(TRUE_{}, TRUE_{}, K - 1)) return;
+  if (!sweep(FALSE_{}, FALSE_{}, K - 1)) return;
+  for (int k = K - 2; k >= 0; --k) {
+    if (!sweep(TRUE_{}, FALSE_{}, k)) return;
+    if (!sweep(FALSE_{}, FALSE_{}, k)) return;
+  }
+  if (!sweep(TRUE_{}, FALSE_{}, -1)) return;
+
+  // ---- outputs of my stripe
+  const float fs = -1.f / (sqrtf((float)d) * eps);
+  write_rows(dQa, a.dq, fs);
+  write_rows(dKa, a.dk, fs);
+  // invalid rows of the stripe: zero marginal gradients
+  for (int q = tid; q < nr * 16; q += UNR_NT) {
+    const int i = r_lo + q;
+    if (i < N && !(i < n && valid[i])) {
+      a.dlog_mu[bhN + i] = 0.f;
+      a.dlog_nu[bhN + i] = 0.f;
+      if (a.dv_init) a.dv_init[bhN + i] = 0.f;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < MAXT; ++s) {
+    const float v[6] = {sum_groups(gbx[s]), sum_groups(gby[s]), sum_groups(gbz[s]),
+                        sum_groups(xt0[s]), sum_groups(xt1[s]), sum_groups(xt2[s])};
+    if (lane < 16)
+      for (int t = 0; t < 6; ++t) spart[((size_t)(wave * MAXT + s) * 16 + lane) * 6 + t] = v[t];
+  }
+  {
+    const float sw = wave_sum(s_w);
+    if (lane == 0) sscal[wave] = sw;
+  }
+  __syncthreads();
+  const float gs = geo ? wd / (eps * r0) : 0.f;
+  for (int q = tid; q < nr * 16; q += UNR_NT) {
+    const int rt = q >> 4, l16 = q & 15;
+    const int s = rt / nts, tsl = rt % nts;
+    float v[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < wpt; ++p)
+      for (int t = 0; t < 6; ++t) v[t] += spart[((size_t)((tsl * wpt + p) * MAXT + s) * 16 + l16) * 6 + t];
+    const int i = r_lo + q;
+    if (i < N) {
+      const bool ok = i < n && valid[i];
+      for (int t = 0; t < 3; ++t) a.dx_part[(bh * N + i) * 3 + t] = ok ? gs * v[t] + v[3 + t] : 0.f;
+    }
+  }
+  if (tid < 68) a.dpw_part[(bh * a.G + member) * 68 + tid] = s_dpw[tid] / eps;
+  if (tid == 0) {
+    float sw = 0.f;
+    for (int wv = 0; wv < NW; ++wv) sw += sscal[wv];
+    a.dw_part[bh * a.G + member] = sw / eps;
+  }
+}
+
+size_t unrolled_bwd_lds_bytes(int N) {
+  const size_t Np = ((N + 31) / 32) * 32;
+  size_t bytes = ((Np + 15) / 16) * 16;
+  bytes += 11 * Np * 4;                              // coordinates, grad x_c, D, gathered vectors, STA, STB
+  bytes += (size_t)UNR_NW * UNR_MAXT_ANY * 16 * 4;   // recurrence partials
+  bytes += (size_t)UNR_NW * 16 * 64 * 4;             // part hand-over (>= the dx hand-over)
+  bytes += UNR_NW * 4;
+  return bytes;
+}
+
+int unrolled_max_tiles(int DP) { return (DP <= 32 ? unr_maxt<32>() : unr_maxt<64>()) * UNR_NW; }
+
+template <typename T, int DP>
+static hipError_t launch_unr_prep_t(const UnrPrepArgs& p, hipStream_t stream) {
+  const size_t Np = ((p.N + 31) / 32) * 32;
+  const size_t total = (size_t)p.B * p.H * Np * DP;  // multiple of 1024
+  hipLaunchKernelGGL((unrolled_prep_kernel<T, DP>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipStream_t stream) {
+  if (bf16_in) {
+    if (DP == 32) return launch_unr_prep_t<bf16, 32>(p, stream);
+    if (DP == 64) return launch_unr_prep_t<bf16, 64>(p, stream);
+  } else {
+    if (DP == 32) return launch_unr_prep_t<float, 32>(p, stream);
+    if (DP == 64) return launch_unr_prep_t<float, 64>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int DP>
+static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
+  auto kern = unrolled_bwd_kernel<DP>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid(grid_blocks(a.B * a.H, a.G)), block(UNR_NT);
+  UnrBwdArgs copy = a;
+  if (coop) {
+    void* args[] = {&copy};
+    return hipLaunchCooperativeKernel((const void*)kern, grid, block, args, (unsigned)lds, stream);
+  }
+  hipLaunchKernelGGL(kern, grid, block, lds, stream, copy);
+  return hipGetLastError();
+}
+
+hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop) {
+  if (DP == 32) return launch_unr_t<32>(a, lds, stream, coop);
+  if (DP == 64) return launch_unr_t<64>(a, lds, stream, coop);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream) {
+  const int total = std::max(a.B * a.N * 3, a.H * 68);
+  hipLaunchKernelGGL(unrolled_finalize_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, a, dx, dpw, dw);
+  return hipGetLastError();
+}
+
+}  // namespace dfl

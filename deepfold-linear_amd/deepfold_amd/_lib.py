@@ -49,7 +49,24 @@ class SinkhornFwdParams(ctypes.Structure):
         ("K_iter", I32), ("lam", F32), ("r_0", F32),
         ("o_flat", P), ("x_centroid", P), ("log_u", P), ("log_v", P),
         ("o_avg", P), ("log_z", P), ("col_lse", P),
-        ("storage", I32),
+        ("storage", I32), ("hist", P),
+    ]
+
+
+class SinkhornUnrolledBwdParams(ctypes.Structure):
+    """Mirror of ``dfl_sinkhorn_unrolled_bwd_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("q", P), ("k", P), ("v", P), ("g", P),
+        ("stride_b", I64), ("stride_h", I64), ("stride_n", I64),
+        ("x_res", P), ("pos_weight", P), ("pos_bins", P),
+        ("eps", P), ("w_dist", P), ("log_mu", P), ("log_nu", P), ("log_v_init", P), ("mask", P),
+        ("B", I32), ("H", I32), ("N", I32), ("d", I32), ("K_iter", I32), ("lam", F32), ("r_0", F32),
+        ("o_avg", P), ("x_centroid", P), ("log_u", P), ("log_z", P), ("hist", P),
+        ("grad_o", P), ("grad_xc", P),
+        ("dq", P), ("dk", P), ("dv", P), ("dg", P), ("dlog_mu", P), ("dlog_nu", P), ("dlog_v_init", P),
+        ("dx_res", P), ("dpos_weight", P), ("dw_dist", P),
     ]
 
 
@@ -182,6 +199,8 @@ SIGNATURES = [
     ("dfl_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
     ("dfl_sinkhorn_fwd", I32, [ctypes.POINTER(SinkhornFwdParams), P, ctypes.c_size_t, P]),
     ("dfl_sinkhorn_bwd", I32, [ctypes.POINTER(SinkhornBwdParams), P, ctypes.c_size_t, P]),
+    ("dfl_sinkhorn_unrolled_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
+    ("dfl_sinkhorn_unrolled_bwd", I32, [ctypes.POINTER(SinkhornUnrolledBwdParams), P, ctypes.c_size_t, P]),
     ("dfl_attn_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32, I32]),
     ("dfl_attn_fwd", I32, [ctypes.POINTER(AttnParams), P]),
     ("dfl_attn_bwd", I32, [ctypes.POINTER(AttnParams), P, ctypes.c_size_t, P]),

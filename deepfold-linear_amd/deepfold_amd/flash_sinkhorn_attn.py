@@ -13,8 +13,12 @@ Keyword-only extensions (defaults reproduce the reference):
   flash_sinkhorn_attn.py:471-542) or ``"cg"`` (conjugate gradient on the
   symmetric form of the same linear system).
 * ``ift_iters``: sweeps / CG steps; ``None`` means ``K_iter`` (reference: K_back = K_iter).
-* ``ift_mode``: ``"reference"`` (the reference's signs) or ``"analytic"`` (the true
-  implicit adjoint; differs in the sign of the z_v*S_col term of dC and of d log_mu).
+* ``ift_mode``: ``"reference"`` (the reference's signs), ``"analytic"`` (the true
+  implicit adjoint; differs in the sign of the z_v*S_col term of dC and of d log_mu)
+  or ``"unrolled"``: the exact gradient through the K executed iterations, as the
+  reference's GPU path (FlashSinkhornFunction.backward, sinkhorn_kernel.py:2085-2382)
+  computes it; the forward then also records the potentials of every
+  half-iteration (2*K*B*H*N floats) and ``ift_solver`` / ``ift_iters`` are unused.
 * ``cg_rtol``: CG stops early once ||r|| <= cg_rtol ||b|| (0: run all steps).
 * ``storage``: ``"auto"`` (default), ``"resident"`` or ``"stream"``: where the
   kernels keep Q, K and the length-N vectors.  Resident keeps a whole (b,h) in
@@ -95,6 +99,12 @@ class FlashSinkhornAttn(torch.autograd.Function):
         o_avg = torch.empty(B, H, N, d, **f32)
         log_z = torch.empty(B, H, N, **f32)
         col_lse = torch.empty(B, H, N, **f32)
+        mode = opts[2] if len(opts) > 2 and opts[2] is not None else "reference"
+        hist = None
+        if mode == "unrolled":
+            if int(K_iter) < 1:
+                raise ValueError("ift_mode='unrolled' needs K_iter >= 1")
+            hist = torch.zeros(int(K_iter), 2, B, H, N, **f32)
         lib = _lib.load()
         nbytes = lib.dfl_sinkhorn_workspace_size(B, H, N)
         ws = _lib.workspace(dev, nbytes)
@@ -108,7 +118,7 @@ class FlashSinkhornAttn(torch.autograd.Function):
             _lib.ptr(lu0), _lib.ptr(lv0), _lib.ptr(m),
             B, H, N, d, int(K_iter), float(lam), float(r_0),
             o_flat.data_ptr(), x_c.data_ptr(), log_u.data_ptr(), log_v.data_ptr(),
-            o_avg.data_ptr(), log_z.data_ptr(), col_lse.data_ptr(), _STORAGE[storage])
+            o_avg.data_ptr(), log_z.data_ptr(), col_lse.data_ptr(), _STORAGE[storage], _lib.ptr(hist))
         rc = _lib.timed_launch("sinkhorn_fwd", dev, lambda: lib.dfl_sinkhorn_fwd(
             ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
         _lib.check(rc, "dfl_sinkhorn_fwd")
@@ -116,13 +126,13 @@ class FlashSinkhornAttn(torch.autograd.Function):
             _lib.check_workspace(ws, "dfl_sinkhorn_fwd")
         solver = opts[0] if len(opts) > 0 and opts[0] is not None else "fixed_point"
         iters = opts[1] if len(opts) > 1 and opts[1] is not None else int(K_iter)
-        mode = opts[2] if len(opts) > 2 and opts[2] is not None else "reference"
         rtol = float(opts[3]) if len(opts) > 3 and opts[3] is not None else 0.0
         if solver not in _SOLVERS:
             raise ValueError(f"ift_solver must be one of {sorted(_SOLVERS)}, got {solver!r}")
-        if mode not in _MODES:
-            raise ValueError(f"ift_mode must be one of {sorted(_MODES)}, got {mode!r}")
+        if mode not in _MODES and mode != "unrolled":
+            raise ValueError(f"ift_mode must be one of {sorted(_MODES) + ['unrolled']}, got {mode!r}")
         ctx.save_for_backward(q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c)
+        ctx.unrolled = (hist, lmu, lnu, lv0, int(K_iter)) if mode == "unrolled" else None
         ctx.meta = (B, H, N, d, dt, float(lam), float(r_0), solver, int(iters), mode, rtol, len(opts),
                     Q_ln.dtype, G is not None, storage)
         ctx.set_materialize_grads(False)
@@ -152,6 +162,8 @@ class FlashSinkhornAttn(torch.autograd.Function):
         dx = torch.empty(B, N, 3, **f32) if need_dx else None
         dpw = torch.empty(H, 68, **f32) if need_dpw else None
         dw = torch.empty(H, **f32) if need_dw else None
+        if ctx.unrolled is not None:
+            return FlashSinkhornAttn._backward_unrolled(ctx, go, gxc, dq, dk, dv, dg, dlmu, dlnu, dx, dpw, dw)
         lib = _lib.load()
         ws = _lib.workspace(dev, lib.dfl_sinkhorn_workspace_size(B, H, N))
         sb, sh, sn, _ = q.stride()
@@ -176,6 +188,39 @@ class FlashSinkhornAttn(torch.autograd.Function):
             _lib.check_workspace(ws, "dfl_sinkhorn_bwd")
         return ((dq, dk, dv, dg if has_g else None, dx, dpw, None, None, dw,
                  dlmu, dlnu, None, None, None, None, None, None) + (None,) * n_opts)
+
+
+    @staticmethod
+    def _backward_unrolled(ctx, go, gxc, dq, dk, dv, dg, dlmu, dlnu, dx, dpw, dw):
+        (q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c) = ctx.saved_tensors
+        (B, H, N, d, dt, lam, r_0, solver, iters, mode, rtol, n_opts, in_dtype, has_g, storage) = ctx.meta
+        hist, lmu, lnu, lv0, K_iter = ctx.unrolled
+        dev = q.device
+        dlv0 = torch.empty(B, H, N, device=dev, dtype=torch.float32) if (lv0 is not None and
+                                                                         ctx.needs_input_grad[15]) else None
+        lib = _lib.load()
+        ws = _lib.workspace(dev, lib.dfl_sinkhorn_unrolled_workspace_size(B, H, N, d))
+        sb, sh, sn, _ = q.stride()
+        p = _lib.SinkhornUnrolledBwdParams(
+            _lib.DFL_BF16 if dt == torch.bfloat16 else _lib.DFL_F32,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(g),
+            sb, sh, sn,
+            _lib.ptr(x), _lib.ptr(pw), _lib.ptr(bins),
+            eps_t.data_ptr(), _lib.ptr(wd), lmu.data_ptr(), lnu.data_ptr(), _lib.ptr(lv0), _lib.ptr(m),
+            B, H, N, d, K_iter, lam, r_0,
+            o_avg.data_ptr(), x_c.data_ptr(), log_u.data_ptr(), log_z.data_ptr(), hist.data_ptr(),
+            go.data_ptr(), _lib.ptr(gxc),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _lib.ptr(dg) if has_g else None,
+            dlmu.data_ptr(), dlnu.data_ptr(), _lib.ptr(dlv0),
+            _lib.ptr(dx), _lib.ptr(dpw), _lib.ptr(dw))
+        rc = _lib.timed_launch("sinkhorn_unrolled_bwd", dev, lambda: lib.dfl_sinkhorn_unrolled_bwd(
+            ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
+        _lib.check(rc, "dfl_sinkhorn_unrolled_bwd")
+        if _lib.debug_checks():
+            _lib.check_workspace(ws, "dfl_sinkhorn_unrolled_bwd")
+        ctx.unrolled = None
+        return ((dq, dk, dv, dg if has_g else None, dx, dpw, None, None, dw,
+                 dlmu, dlnu, None, None, None, None, dlv0, None) + (None,) * n_opts)
 
 
 def flash_sinkhorn_attn(

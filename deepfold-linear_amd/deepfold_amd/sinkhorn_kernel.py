@@ -3,14 +3,16 @@
 Drop-in for ``flash_sinkhorn`` / ``FlashSinkhornFunction`` of vv137/deepfold-linear
 (src/deepfold/model/kernels/sinkhorn_kernel.py:1921-2468): same arguments,
 defaults, unbatched handling and return tuple (O_avg (B,H,N,d) before any gate,
-x_centroid (B,H,N,3), log_u, log_v (B,H,N)).  It runs the same HIP forward and
-IFT backward as ``flash_sinkhorn_attn`` with no gate.
+x_centroid (B,H,N,3), log_u, log_v (B,H,N)).  It runs the same HIP forward as
+``flash_sinkhorn_attn`` with no gate, and by default the same gradient as the
+reference's GPU path: the exact gradient through the K executed iterations
+(``ift_mode="unrolled"``, sinkhorn_kernel.py:2085-2382).
 
 Differences from the reference's Triton path, which cannot run on this
 hardware:
-* Gradients come from the implicit (IFT) adjoint -- the reference-mode signs by
-  default, CG or fixed point.  The Triton backward unrolls the K iterations
-  (sinkhorn_kernel.py:2085-2382); the two agree as K grows.
+* ``ift_mode`` may select the implicit (IFT) adjoint instead ("reference" or
+  "analytic", CG or fixed point), as for ``flash_sinkhorn_attn``; it agrees with
+  the unrolled gradient as K grows.
 * The geometry term uses the exact distance, as the reference's CPU fallback
   does.  The Triton kernel uses sqrt(sum dx^2 + 1e-8), which differs on the
   diagonal by at most w_dist * 1e-4 / r_0.
@@ -46,7 +48,7 @@ class FlashSinkhornFunction:
               log_u_init, log_v_init, BLOCK, mask_bias):
         mask = None if mask_bias is None else (mask_bias > -0.5e9).to(torch.float32)
         return _ungated(Q_ln, K_ln, V, x_res, pos_weight, pos_bins, eps, w_dist, log_mu, log_nu, K_iter, lam, r_0,
-                        log_u_init, log_v_init, mask, ())
+                        log_u_init, log_v_init, mask, ("fixed_point", None, "unrolled", 0.0))
 
 
 def flash_sinkhorn(
@@ -70,10 +72,11 @@ def flash_sinkhorn(
     *,
     ift_solver: str = "fixed_point",
     ift_iters: int | None = None,
-    ift_mode: str = "reference",
+    ift_mode: str = "unrolled",
     cg_rtol: float = 0.0,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Flash-Sinkhorn with IFT backward (sinkhorn_kernel.py:2385-2468).
+    """Flash-Sinkhorn (sinkhorn_kernel.py:2385-2468); gradients through the unrolled
+    iterations by default, as the reference's, or the IFT adjoint (``ift_mode``).
 
     Accepts unbatched (H,N,d) or batched (B,H,N,d) inputs; unbatched results are
     squeezed.  Returns (O_avg (B,H,N,d), x_centroid (B,H,N,3), log_u, log_v (B,H,N)).

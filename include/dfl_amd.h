@@ -60,6 +60,9 @@ int dfl_workspace_error(const void* workspace, void* stream);
  * RESIDENT keeps all of them in LDS (fails with an argument error if they do not
  * fit); STREAM keeps only each workgroup's stripe in LDS and streams the rest
  * through L2 (long sequences, e.g. N = 4096, d = 64).  Results agree to rounding.
+ * hist (K_iter,2,B,H,N) may be NULL; if given, the forward also writes v after the
+ * column update and u after the row update of every iteration (natural log), which
+ * dfl_sinkhorn_unrolled_bwd needs.
  */
 enum dfl_storage { DFL_STORAGE_AUTO = 0, DFL_STORAGE_RESIDENT = 1, DFL_STORAGE_STREAM = 2 };
 
@@ -92,6 +95,7 @@ typedef struct dfl_sinkhorn_fwd_params {
   float* log_z;
   float* col_lse;
   int storage;
+  float* hist;
 } dfl_sinkhorn_fwd_params;
 
 size_t dfl_sinkhorn_workspace_size(int B, int H, int N);
@@ -157,6 +161,65 @@ typedef struct dfl_sinkhorn_bwd_params {
 } dfl_sinkhorn_bwd_params;
 
 int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Flash-Sinkhorn unrolled backward: the exact gradient through the K_iter executed
+ * iterations, as the reference's GPU path computes it (FlashSinkhornFunction.backward,
+ * sinkhorn_kernel.py:2085-2382; autograd through the dense iteration in its
+ * tests/test_triton_fallback_consistency.py:312-430), instead of the implicit adjoint.
+ * Inputs: the forward's inputs (q, k, v, g, strides, x_res, pos_weight, pos_bins, eps,
+ * w_dist, log_mu, log_nu, log_v_init, mask, B, H, N, d, K_iter >= 1, lam, r_0) and
+ * outputs (o_avg, x_centroid, log_u, log_z, and hist, which the forward must have
+ * written), grad_o (B,N,H*d) fp32 and grad_xc (B,H,N,3) (may be NULL).  Outputs
+ * (fp32, fully written): dq, dk, dv, dg (dg may be NULL without g) (B,H,N,d),
+ * dlog_mu, dlog_nu (B,H,N); optional (NULL = not requested): dlog_v_init (B,H,N),
+ * dx_res (B,N,3), dpos_weight (H,68), dw_dist (H,).  Padded tokens are excluded, as
+ * in dfl_sinkhorn_bwd.  The sweeps run in fp32 for either dtype.  Workspace:
+ * dfl_sinkhorn_unrolled_workspace_size(B, H, N, d) bytes; the forward's workspace
+ * rules apply (a workspace that served the forward may serve this call if large enough).
+ */
+typedef struct dfl_sinkhorn_unrolled_bwd_params {
+  int dtype;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  long long stride_b, stride_h, stride_n;
+  const float* x_res;
+  const float* pos_weight;
+  const int* pos_bins;
+  const float* eps;
+  const float* w_dist;
+  const float* log_mu;
+  const float* log_nu;
+  const float* log_v_init;
+  const float* mask;
+  int B, H, N, d;
+  int K_iter;
+  float lam;
+  float r_0;
+  const float* o_avg;
+  const float* x_centroid;
+  const float* log_u;
+  const float* log_z;
+  const float* hist;
+  const float* grad_o;
+  const float* grad_xc;
+  float* dq;
+  float* dk;
+  float* dv;
+  float* dg;
+  float* dlog_mu;
+  float* dlog_nu;
+  float* dlog_v_init;
+  float* dx_res;
+  float* dpos_weight;
+  float* dw_dist;
+} dfl_sinkhorn_unrolled_bwd_params;
+
+size_t dfl_sinkhorn_unrolled_workspace_size(int B, int H, int N, int d);
+int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /* ---------------------------------------------------------------------------
  * Softmax attention: O = softmax(scale * Q K^T + bias, key mask) V, rows of

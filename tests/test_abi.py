@@ -79,6 +79,7 @@ def test_struct_layout_matches_c(lib_path):
 
     structs = header_structs()
     mirrors = {"dfl_sinkhorn_fwd_params": _lib.SinkhornFwdParams,
+               "dfl_sinkhorn_unrolled_bwd_params": _lib.SinkhornUnrolledBwdParams,
                "dfl_sinkhorn_bwd_params": _lib.SinkhornBwdParams,
                "dfl_attn_params": _lib.AttnParams,
                "dfl_a2t_params": _lib.A2TParams,

@@ -2,8 +2,9 @@
 
 * ``flash_sinkhorn`` / ``FlashSinkhornFunction.apply`` (sinkhorn_kernel.py:1921-2468):
   ungated O_avg, x_centroid and potentials against the oracle forward (gate
-  logits +30, sigma = 1 - 1e-13), gradients against the oracle's reference-mode
-  IFT backward; the additive mask_bias form; unbatched inputs.
+  logits +30, sigma = 1 - 1e-13), gradients of ``ift_mode="reference"`` against
+  the oracle's reference-mode IFT backward (the default unrolled gradient is
+  tests/test_gpu_unrolled.py's); the additive mask_bias form; unbatched inputs.
 * ``conjugate_gradient`` / ``CGInfo`` (utils/cg.py:28-97): the solution against
   torch.linalg.solve, and the iteration count / residual record against the
   oracle's restatement of the reference steps.
@@ -41,7 +42,7 @@ def test_flash_sinkhorn_forward_backward(dtype, tol):
         leaves[k] = leaves[k].detach().requires_grad_(True)
     O, xc, lu, lv = flash_sinkhorn(leaves["Q"], leaves["K"], leaves["V"], leaves["x_res"], leaves["pos_weight"],
                                    leaves["pos_bins"], leaves["eps"], leaves["w_dist"], leaves["log_mu"],
-                                   leaves["log_nu"], K_iter=K)
+                                   leaves["log_nu"], K_iter=K, ift_mode="reference")
     assert O.shape == (B, H, N, d)
     g = torch.Generator().manual_seed(502)
     gO = torch.randn(B, H, N, d, generator=g)

@@ -1,0 +1,125 @@
+"""GPU parity of the unrolled flash-Sinkhorn backward (``ift_mode="unrolled"``,
+the default of ``flash_sinkhorn``) against autograd through the dense float64
+iteration: oracle/sinkhorn_dense_ref.py (sinkhorn_solve + compute_transport_output)
+on the flash cost built here, which is what the reference's
+tests/test_triton_fallback_consistency.py:312-430 checks its Triton unrolled
+backward against (at 5e-3; the bar here is 1e-4 in fp32, 2e-2 in bf16).
+
+Cases: the reference test's shapes (B1 H2 N16 d32 K3; B2 masked), a gated
+ragged batch with position bins, geometry and a warm start, bf16 inputs at
+d = 64, and a longer sequence whose members own several tiles.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_rel
+from oracle import sinkhorn_dense_ref as dref
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _inputs(B, H, N, d, seed, eps, lens=None, warm=False):
+    g = torch.Generator().manual_seed(seed)
+    t = dict(Q=torch.randn(B, H, N, d, generator=g) / d ** 0.5 * 2, K=torch.randn(B, H, N, d, generator=g) / d ** 0.5,
+             V=torch.randn(B, H, N, d, generator=g), G=torch.randn(B, H, N, d, generator=g),
+             x=torch.randn(B, N, 3, generator=g) * 3, pw=torch.randn(H, 68, generator=g) * 0.3,
+             wd=torch.rand(H, generator=g),
+             lmu=torch.log_softmax(torch.randn(B, H, N, generator=g), -1),
+             lnu=torch.log_softmax(torch.randn(B, H, N, generator=g), -1))
+    bins = torch.randint(0, 68, (B, N, N), generator=g, dtype=torch.int32)
+    if warm:
+        t["v0"] = 0.3 * torch.randn(B, H, N, generator=g)
+    mask = None
+    if lens is not None:
+        mask = torch.zeros(B, N)
+        for b, n in enumerate(lens):
+            mask[b, :n] = 1
+    wo = torch.randn(B, N, H * d, generator=g)
+    wx = torch.randn(B, H, N, 3, generator=g)
+    return t, bins, torch.tensor(eps, dtype=torch.float32), mask, wo, wx
+
+
+def _oracle(t, bins, eps, mask, wo, wx, K, r0=10.0, lam=1.0):
+    L = {k: v.double().clone().requires_grad_(True) for k, v in t.items()}
+    B, H, N, d = L["Q"].shape
+    dist = (L["x"][:, :, None] - L["x"][:, None, :]).norm(dim=-1).clamp(min=1e-8)
+    C = (-(L["Q"] @ L["K"].transpose(-1, -2)) / d ** 0.5 + L["pw"][:, bins.long()].permute(1, 0, 2, 3)
+         + L["wd"][None, :, None, None] * (dist / (r0 + dist))[:, None])
+    m = None if mask is None else mask.double()
+    lu, lv = dref.sinkhorn_solve(C, L["lmu"], L["lnu"], eps.double(), lam=lam, K=K, log_v_init=L.get("v0"), mask=m)
+    o, _, xc = dref.compute_transport_output(L["V"], L["G"], lu, lv, C, eps.double(), L["x"], m)
+    ((o * wo.double()).sum() + (xc * wx.double()).sum()).backward()
+    return {"o": o, "xc": xc, "lu": lu, "lv": lv}, {k: v.grad for k, v in L.items()}
+
+
+def _gpu(t, bins, eps, mask, wo, wx, K, dtype, r0=10.0, lam=1.0):
+    from deepfold_amd import flash_sinkhorn_attn
+
+    L = {k: v.to(DEV) for k, v in t.items()}
+    for k in ("Q", "K", "V", "G"):
+        L[k] = L[k].to(dtype)
+    L = {k: v.detach().requires_grad_(True) for k, v in L.items()}
+    o, xc, lu, lv = flash_sinkhorn_attn(L["Q"], L["K"], L["V"], L["G"], L["x"], L["pw"], bins.to(DEV), eps.to(DEV),
+                                        L["wd"], L["lmu"], L["lnu"], K_iter=K, lam=lam, r_0=r0,
+                                        log_v_init=L.get("v0"), mask=None if mask is None else mask.to(DEV),
+                                        ift_mode="unrolled")
+    ((o * wo.to(DEV)).sum() + (xc * wx.to(DEV)).sum()).backward()
+    return {"o": o, "xc": xc, "lu": lu, "lv": lv}, {k: v.grad for k, v in L.items()}
+
+
+CASES = [
+    # B, H, N, d, K, eps, lens, warm, dtype, tol
+    (1, 2, 16, 32, 3, [0.5, 1.0], None, False, torch.float32, 1e-4),          # reference test_backward_unbatched
+    (2, 2, 16, 32, 3, [0.5, 1.0], [16, 11], False, torch.float32, 1e-4),      # reference batched masked
+    (2, 3, 70, 32, 7, [0.5, 1.0, 2.0], [70, 41], False, torch.float32, 1e-4),  # gate, bins, geometry, ragged
+    # warm start at K = 3: d log_v_init decays geometrically with K (about 1e-12 at K = 7,
+    # below fp32 rounding of the other gradients), so it is compared where it is measurable
+    (2, 3, 70, 32, 3, [0.5, 1.0, 2.0], [70, 41], True, torch.float32, 1e-4),
+    (1, 2, 48, 64, 5, [0.7, 1.3], None, False, torch.bfloat16, 2e-2),
+    (1, 2, 300, 32, 4, [0.5, 1.0], [290], False, torch.float32, 1e-4),        # several tiles per member
+]
+
+
+@pytest.mark.parametrize("B,H,N,d,K,eps,lens,warm,dtype,tol", CASES)
+def test_unrolled_matches_dense_autograd(B, H, N, d, K, eps, lens, warm, dtype, tol):
+    print(f"case B{B} H{H} N{N} d{d} K{K} {dtype}", flush=True)
+    t, bins, e, mask, wo, wx = _inputs(B, H, N, d, seed=N * 7 + K, eps=eps, lens=lens, warm=warm)
+    if dtype == torch.bfloat16:  # the oracle sees the rounded values
+        for k in ("Q", "K", "V", "G"):
+            t[k] = t[k].to(torch.bfloat16).float()
+    vr, gr = _oracle(t, bins, e, mask, wo, wx, K)
+    vg, gg = _gpu(t, bins, e, mask, wo, wx, K, dtype)
+    for k in ("o", "xc", "lu", "lv"):
+        assert_close_rel(vg[k].detach().float().cpu().numpy(), vr[k].detach().numpy(), tol, k)
+    for k, want in gr.items():
+        got = gg[k]
+        assert got is not None, k
+        got = got.float().cpu().numpy()
+        assert np.isfinite(got).all(), k
+        assert_close_rel(got, want.numpy(), tol, f"grad {k}")
+
+
+def test_flash_sinkhorn_defaults_to_unrolled():
+    """flash_sinkhorn (sinkhorn_kernel.py:2385) differentiates through the iterations
+    by default, as the reference's; FlashSinkhornFunction.apply likewise."""
+    from deepfold_amd import FlashSinkhornFunction, flash_sinkhorn
+
+    B, H, N, d, K = 1, 2, 24, 32, 4
+    t, bins, e, _, _, wx = _inputs(B, H, N, d, seed=5, eps=[0.5, 1.0])
+    g = torch.Generator().manual_seed(6)
+    wO = torch.randn(B, H, N, d, generator=g)
+    t["G"] = torch.full_like(t["G"], 30.0)  # sigma = 1 - 9e-14: the gated oracle is the ungated op
+    vr, gr = _oracle(t, bins, e, None, wO.permute(0, 2, 1, 3).reshape(B, N, H * d), wx, K)
+    for fn in ("flash_sinkhorn", "apply"):
+        L = {k: v.to(DEV).detach().requires_grad_(True) for k, v in t.items() if k != "G"}
+        args = (L["Q"], L["K"], L["V"], L["x"], L["pw"], bins.to(DEV), e.to(DEV), L["wd"], L["lmu"], L["lnu"])
+        if fn == "flash_sinkhorn":
+            O, xc, _, _ = flash_sinkhorn(*args, K_iter=K)
+        else:
+            O, xc, _, _ = FlashSinkhornFunction.apply(*args, K, 1.0, 10.0, None, None, 64, None)
+        ((O * wO.to(DEV)).sum() + (xc * wx.to(DEV)).sum()).backward()
+        for k in ("Q", "K", "V", "x", "pw", "wd", "lmu", "lnu"):
+            assert_close_rel(L[k].grad.cpu().numpy(), gr[k].numpy(), 1e-4, f"{fn} grad {k}")
