@@ -46,6 +46,10 @@ SINKHORN = {
                  workload="BASELINE configs[1]: flash-Sinkhorn fwd + IFT(CG) bwd"),
     "cfg5": dict(B=1, H=16, N=4096, d=64, eps=0.25, K_iter=100, n_cg=30, seed=1005, ragged=False, dirichlet=True,
                  workload="BASELINE configs[4]: large-scale flash-Sinkhorn fwd + IFT(CG) bwd (stream storage)"),
+    "cfg2-unrolled": dict(B=2, H=8, N=768, d=32, eps=0.5, K_iter=50, n_cg=0, seed=1002, ragged=True,
+                          dirichlet=False, unrolled=True,
+                          workload="BASELINE configs[1] inputs, fwd + unrolled bwd (the reference GPU path's "
+                                   "gradient through the 50 iterations)"),
 }
 
 
@@ -90,9 +94,14 @@ def step(cfg, t):
     from deepfold_amd import flash_sinkhorn_attn
 
     q, k, v, g = (t[n].detach().requires_grad_(True) for n in ("Q", "K", "V", "G"))
-    o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], t["w_dist"],
-                                        t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
-                                        ift_solver="cg", ift_iters=cfg["n_cg"])
+    if cfg.get("unrolled"):
+        o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], t["w_dist"],
+                                            t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
+                                            ift_mode="unrolled")
+    else:
+        o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], t["w_dist"],
+                                            t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
+                                            ift_solver="cg", ift_iters=cfg["n_cg"])
     o.backward(t["dO"])
     return q.grad
 
@@ -105,9 +114,15 @@ def algorithmic_counts(cfg, lengths):
     H, d, K, ncg = cfg["H"], cfg["d"], cfg["K_iter"], cfg["n_cg"]
     E = sum(H * n * n for n in lengths)
     f_fwd = E * d * (4 * K + 4)
-    f_bwd = E * d * (14 + 2 * ncg)
     x_fwd = E * (2 * K + 1)
-    x_bwd = E * (ncg + 2)
+    if cfg.get("unrolled"):
+        # 2K + 2 sweeps of cost recompute (2d) and one gradient product (2d), plus the
+        # centroid sweeps' gO.V (2d each) and P^T gO (2d); two exponentials a sweep
+        f_bwd = E * d * (8 * K + 16)
+        x_bwd = E * (4 * K + 3)
+    else:
+        f_bwd = E * d * (14 + 2 * ncg)
+        x_bwd = E * (ncg + 2)
     return E, f_fwd, f_bwd, x_fwd, x_bwd
 
 
@@ -194,6 +209,43 @@ def cpu_baseline(cfg, cpu, budget_s=12.0):
     return dict(value=round(value * 1e3, 1), unit="ms/layer", cores=1, kind="port", sample=sample)
 
 
+def unrolled_cpu_baseline(cfg, cpu, budget_s=12.0):
+    """Autograd through the dense iteration (the oracle's restatement of
+    sinkhorn.py:17-198, the CPU form of the unrolled gradient), float32 torch on
+    all host threads, one (b, h) head at a time on its valid tokens, cycling over
+    the layer's heads for about budget_s and scaled to the layer by valid elements."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import sinkhorn_dense_ref as dref
+
+    B, H, d, K = cfg["B"], cfg["H"], cfg["d"], cfg["K_iter"]
+    lengths = cpu["lengths"]
+    spent, heads = 0.0, []
+    for b, h in [(b, h) for h in range(H) for b in range(B)]:
+        n = lengths[b]
+        sl = lambda t: t[b:b + 1, h:h + 1, :n].float().clone().requires_grad_(True)
+        q, k, v = sl(cpu["Q"]), sl(cpu["K"]), sl(cpu["V"])
+        g = cpu["G"][b:b + 1, h:h + 1, :n].float()
+        go = cpu["dO"].reshape(B, -1, H, d)[b:b + 1, :n, h, :]
+        t0 = time.perf_counter()
+        C = -(q @ k.transpose(-1, -2)) / math.sqrt(d)
+        lu, lv = dref.sinkhorn_solve(C, cpu["log_mu"][b:b + 1, h:h + 1, :n], cpu["log_nu"][b:b + 1, h:h + 1, :n],
+                                     cpu["eps"][h:h + 1], K=K)
+        o, _, _ = dref.compute_transport_output(v, g, lu, lv, C, cpu["eps"][h:h + 1])
+        (o * go).sum().backward()
+        spent += time.perf_counter() - t0
+        heads.append((b, h))
+        if spent > budget_s:
+            break
+    e_all = sum(H * n * n for n in lengths)
+    e_smp = sum(lengths[b] ** 2 for b, _ in heads)
+    th = torch.get_num_threads()
+    return dict(value=round(spent * e_all / e_smp * 1e3, 1), unit="ms/layer", cores=th, kind="port",
+                sample=f"autograd through the dense oracle iteration (float32 torch, {th} threads), K={K}, "
+                       f"{len(heads)} (b,h) heads ({spent:.1f} s), scaled to the layer by valid plan elements")
+
+
 def bench_sinkhorn(args, name):
     import torch
     from deepfold_amd import _lib
@@ -227,9 +279,11 @@ def bench_sinkhorn(args, name):
     x_dom = x_fwd if dom == "sinkhorn_fwd" else x_bwd
     achieved = f_dom / (avg[dom] * 1e-3)
     traffic = profiled_traffic(dom, "sinkhorn_cfg2_bench.md" if name == "cfg2" else f"sinkhorn_{name}_bench.md")
+    peak = PEAK_MFMA_F32 if cfg.get("unrolled") and dom != "sinkhorn_fwd" else PEAK_MFMA_BF16
     t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
     metric = ("flash-Sinkhorn fwd+IFT-bwd ms/layer @B2,H8,N768,d32 bf16; % of MFMA/HBM roof" if name == "cfg2"
-              else f"flash-Sinkhorn fwd+IFT-bwd ms/layer @B{cfg['B']},H{cfg['H']},N{cfg['N']},d{cfg['d']} bf16")
+              else f"flash-Sinkhorn fwd+{'unrolled' if cfg.get('unrolled') else 'IFT'}-bwd ms/layer "
+                   f"@B{cfg['B']},H{cfg['H']},N{cfg['N']},d{cfg['d']} bf16")
     out = {
         "metric": metric,
         "value": round(ms_per_step, 4),
@@ -250,14 +304,14 @@ def bench_sinkhorn(args, name):
                    "valid_plan_elements": E},
         "kernel_ms": {k: round(v, 4) for k, v in avg.items()},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
-                     "peak": PEAK_MFMA_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_BF16, 5),
+                     "peak": peak / 1e12, "unit": "TFLOP/s", "frac": round(achieved / peak, 5),
                      "traffic": traffic},
         "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_NOMINAL,
                          "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
                          "layer_t_roof_ms": t_roof * 1e3, "layer_frac": t_roof * 1e3 / ms_per_step},
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(cfg, cpu)
+        out["cpu_baseline"] = unrolled_cpu_baseline(cfg, cpu) if cfg.get("unrolled") else cpu_baseline(cfg, cpu)
     print(json.dumps(out), flush=True)
 
 
@@ -491,7 +545,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg5", "cfg3", "cfg4", "balanced"],
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg5", "cfg2-unrolled", "cfg3", "cfg4", "balanced"],
                     help="cfg2 (default): the headline flash-Sinkhorn layer; cfg5: the N=4096 layer; "
                          "cfg3 / cfg4: attention rows")
     ap.add_argument("--calibrate-copy", action="store_true",

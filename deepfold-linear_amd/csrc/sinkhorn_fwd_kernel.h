@@ -113,9 +113,9 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
     const size_t o = (bh * N + irow) * 3;
     a.x_centroid[o + 0] = a.x_centroid[o + 1] = a.x_centroid[o + 2] = 0.f;
     a.log_u[bh * N + irow] = a.log_z[bh * N + irow] = a.log_v[bh * N + irow] = 0.f;
-    if (a.col_lse) a.col_lse[bh * N + irow] = 0.f;
+    if (!bal) a.col_lse[bh * N + irow] = 0.f;
   }
-  if (!a.o_avg) return;  // no V: coordinate centroid only
+  if (bal && !a.o_avg) return;  // balanced mode without V: coordinate centroid only
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = tile * 16 + 4 * g + r;
@@ -125,7 +125,7 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
         const int col = c * 16 + (lane & 15);
         if (col < d) {
           a.o_avg[(bh * N + row) * d + col] = 0.f;
-          if (a.o_flat) a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = 0.f;
+          if (!bal) a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = 0.f;
         }
       }
     }
@@ -137,7 +137,7 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
         if (col < d) {
           const float o = oacc[c][r] / den;
           a.o_avg[(bh * N + row) * d + col] = o;
-          if (a.o_flat) {
+          if (!bal) {
             const float sg = Gg ? 1.f / (1.f + __expf(-to_f32(Gg[(size_t)row * a.sn + col]))) : 1.f;
             a.o_flat[((size_t)b * N + row) * (size_t)(a.H * d) + (size_t)h * d + col] = sg * o;
           }
@@ -147,8 +147,16 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
   }
 }
 
-template <typename T, int DP, bool STREAM>
+// MODE (compile time, so the plain UOT instantiation carries none of the other
+// modes' code): FWD_UOT, FWD_UOT_HIST (also records the potentials history for the
+// unrolled backward) or FWD_BALANCED (balanced transport, history recorded).  The
+// host picks FWD_BALANCED exactly when a.balanced != 0 and FWD_UOT_HIST when a.hist
+// is given.
+enum FwdMode : int { FWD_UOT = 0, FWD_UOT_HIST = 1, FWD_BALANCED = 2 };
+template <typename T, int DP, bool STREAM, int MODE>
 __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
+  constexpr bool BAL = MODE == FWD_BALANCED;
+  constexpr bool HIST = MODE != FWD_UOT;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_flag, s_tmp;
   __shared__ unsigned s_du, s_dv;
@@ -159,8 +167,8 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const int b = grp / a.H, h = grp % a.H;
   const int N = a.N, d = a.d;
   const int Np = ((N + 31) / 32) * 32;
-  const bool bal = a.balanced != 0;
-  const bool has_v = a.v != nullptr && a.o_avg != nullptr;
+  constexpr bool bal = BAL;
+  const bool has_v = !BAL || (a.v != nullptr && a.o_avg != nullptr);  // UOT mode always has V
   if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; s_cnt = 0; }
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -194,15 +202,15 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     const size_t bh0 = (size_t)b * a.H + h;
     for (int i = n_tiles * 16 + member; i < N; i += a.G) {
       for (int c = threadIdx.x; c < d; c += FWD_NT) {
-        if (a.o_avg) a.o_avg[(bh0 * N + i) * d + c] = 0.f;
-        if (a.o_flat) a.o_flat[((size_t)b * N + i) * (size_t)(a.H * d) + (size_t)h * d + c] = 0.f;
+        if (has_v) a.o_avg[(bh0 * N + i) * d + c] = 0.f;
+        if (!BAL) a.o_flat[((size_t)b * N + i) * (size_t)(a.H * d) + (size_t)h * d + c] = 0.f;
       }
       if (threadIdx.x < 3) a.x_centroid[(bh0 * N + i) * 3 + threadIdx.x] = 0.f;
       if (threadIdx.x == 0) {
         a.log_u[bh0 * N + i] = 0.f;
         a.log_v[bh0 * N + i] = 0.f;
         a.log_z[bh0 * N + i] = 0.f;
-        if (a.col_lse) a.col_lse[bh0 * N + i] = 0.f;
+        if (!BAL) a.col_lse[bh0 * N + i] = 0.f;
       }
     }
   }
@@ -302,6 +310,18 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
 
+  // History for the unrolled backward: this member's stripe of the vector just
+  // exchanged, copied from its own words (exact published values), outside the sweep.
+  auto record = [&](const uint64_t* words, int slot) {
+    for (int q = threadIdx.x; q < nr * 16; q += FWD_NT) {
+      const int i = r_lo + q;
+      if (i < n) {
+        const uint64_t w = __hip_atomic_load(const_cast<uint64_t*>(words + i), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        a.hist[((size_t)slot * a.B * a.H + bh) * N + i] = valid[i] ? __uint_as_float((uint32_t)(w >> 32)) : 0.f;
+      }
+    }
+  };
   // ---- row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j)) for my rows
   auto row_update = [&](int it) -> bool {
     ++phase;
@@ -310,14 +330,11 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       const bool online = it == 0 || __uint_as_float(s_dv) > FIXED_SHIFT_MAX_DELTA;
       auto pub = [&](int q, float l2) {
         const int i = r_lo + q;
-        if (i < n) {
-          const float u = kappa * (lmu_l[q] - l2 * LN2);
-          xch_put(xu + i, u, tag);
-          if (a.hist) a.hist[((size_t)(2 * it + 1) * a.B * a.H + bh) * N + i] = valid[i] ? u : 0.f;
-        }
+        if (i < n) xch_put(xu + i, kappa * (lmu_l[q] - l2 * LN2), tag);
       };
       sweep(true, online, lse_r, nullptr, &s_du, pub);
       if (!gather_potential<FWD_NT>(xu, n, tag, vecU, valid, a.err, &s_flag, &s_du)) return false;
+      if constexpr (HIST) record(xu, 2 * it + 1);
     }
     return true;
   };
@@ -331,25 +348,27 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       auto pub = [&](int q, float l2) {
         const int j = r_lo + q;
         if (j < n) {
-          const float v = kappa * (lnu_l[q] - l2 * LN2);
-          xch_put(xv + j, v, tag);
-          if (last && valid[j] && a.col_lse) a.col_lse[bh * N + j] = l2 * LN2;
-          if (a.hist) a.hist[((size_t)(2 * it) * a.B * a.H + bh) * N + j] = valid[j] ? v : 0.f;
+          xch_put(xv + j, kappa * (lnu_l[q] - l2 * LN2), tag);
+          if (!BAL && last && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
         }
       };
       sweep(false, online, lse_c, nullptr, &s_dv, pub);
       if (!gather_potential<FWD_NT>(xv, n, tag, vecV, valid, a.err, &s_flag, &s_dv)) return false;
+      if constexpr (HIST) record(xv, 2 * it);
     }
     return true;
   };
+  // The UOT order is row then column, the balanced order column then row.  One call
+  // site per update in each instantiation: with two, the compiler outlines them
+  // into calls with a stack frame.
   for (int it = 0; it < a.K_iter; ++it) {
-    if (bal) {
+    if constexpr (BAL) {
       if (!col_update(it) || !row_update(it)) return;
     } else {
       if (!row_update(it) || !col_update(it)) return;
     }
   }
-  if (a.K_iter == 0 && a.col_lse) {
+  if (a.K_iter == 0 && !BAL) {
     auto pub = [&](int q, float l2) {
       const int j = r_lo + q;
       if (j < n && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
@@ -530,9 +549,9 @@ inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stre
   return bytes;
 }
 
-template <typename T, int DP, bool STREAM>
+template <typename T, int DP, bool STREAM, int MODE>
 static hipError_t launch_fwd_t(const SinkFwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  auto kern = sinkhorn_fwd_kernel<T, DP, STREAM>;
+  auto kern = sinkhorn_fwd_kernel<T, DP, STREAM, MODE>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(FWD_NT);
@@ -547,12 +566,28 @@ static hipError_t launch_fwd_t(const SinkFwdArgs& a, size_t lds, hipStream_t str
 
 template <bool STREAM>
 hipError_t launch_fwd_mode(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+  if (a.balanced) {  // the balanced transport computes in fp32 only
+    if (bf16_in || !a.hist) return hipErrorInvalidValue;
+    if (DP == 32) return launch_fwd_t<float, 32, STREAM, FWD_BALANCED>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<float, 64, STREAM, FWD_BALANCED>(a, lds, stream, coop);
+    return hipErrorInvalidValue;
+  }
+  if (a.hist) {
+    if (bf16_in) {
+      if (DP == 32) return launch_fwd_t<bf16, 32, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
+      if (DP == 64) return launch_fwd_t<bf16, 64, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
+    } else {
+      if (DP == 32) return launch_fwd_t<float, 32, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
+      if (DP == 64) return launch_fwd_t<float, 64, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
+    }
+    return hipErrorInvalidValue;
+  }
   if (bf16_in) {
-    if (DP == 32) return launch_fwd_t<bf16, 32, STREAM>(a, lds, stream, coop);
-    if (DP == 64) return launch_fwd_t<bf16, 64, STREAM>(a, lds, stream, coop);
+    if (DP == 32) return launch_fwd_t<bf16, 32, STREAM, FWD_UOT>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<bf16, 64, STREAM, FWD_UOT>(a, lds, stream, coop);
   } else {
-    if (DP == 32) return launch_fwd_t<float, 32, STREAM>(a, lds, stream, coop);
-    if (DP == 64) return launch_fwd_t<float, 64, STREAM>(a, lds, stream, coop);
+    if (DP == 32) return launch_fwd_t<float, 32, STREAM, FWD_UOT>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<float, 64, STREAM, FWD_UOT>(a, lds, stream, coop);
   }
   return hipErrorInvalidValue;
 }
