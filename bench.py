@@ -5,7 +5,7 @@ H=8, N=768 padded, d=32, bf16 inputs with fp32 accumulation, ragged valid
 lengths n_b ~ U[384, 768] with a padding mask, eps=0.5, 50 Sinkhorn iterations,
 20 CG iterations in the IFT solve, upstream gradient dO ~ N(0,1).  Synthetic
 data, seed 1002 (= 1000 + config#).  Unspecified terms are neutral: no position
-bins, w_dist = 0, x_res = 0, G = 0.
+bins, no geometry term (w_dist = 0, passed as None), x_res = 0, G = 0.
 
 One "step" = one forward (flash_sinkhorn_attn) + one backward (autograd) of the
 layer, inputs resident in HBM.  Prints ONE JSON line.
@@ -37,7 +37,7 @@ sys.path.insert(0, os.path.join(ROOT, "deepfold-linear_amd"))
 # MI355X published peaks (dense): bf16 MFMA 2.5 PFLOP/s, HBM 8 TB/s.
 PEAK_MFMA_BF16 = 2.5e15
 PEAK_HBM = 8.0e12
-# v_exp_f32 rate used by BASELINE.md's exp roof (quarter-rate estimate).
+# v_exp_f32 issue rate (quarter rate of fp32 FMA) used for the exp roof.
 PEAK_EXP_NOMINAL = 9.8e12
 PEAK_MFMA_F32 = 157.3e12
 
@@ -46,6 +46,10 @@ SINKHORN = {
                  workload="BASELINE configs[1]: flash-Sinkhorn fwd + IFT(CG) bwd"),
     "cfg5": dict(B=1, H=16, N=4096, d=64, eps=0.25, K_iter=100, n_cg=30, seed=1005, ragged=False, dirichlet=True,
                  workload="BASELINE configs[4]: large-scale flash-Sinkhorn fwd + IFT(CG) bwd (stream storage)"),
+    "cfg2-full": dict(B=2, H=8, N=768, d=32, eps=0.5, K_iter=50, n_cg=20, seed=1002, ragged=True, dirichlet=False,
+                      full_cost=True,
+                      workload="BASELINE configs[1] with the full cost: position bins (B,N,N) in [0,68), "
+                               "pos_weight ~ N(0,0.5^2), w_dist ~ U(0,1), x_res ~ N(0,3^2); fwd + IFT(CG) bwd"),
     "cfg2-unrolled": dict(B=2, H=8, N=768, d=32, eps=0.5, K_iter=50, n_cg=0, seed=1002, ragged=True,
                           dirichlet=False, unrolled=True,
                           workload="BASELINE configs[1] inputs, fwd + unrolled bwd (the reference GPU path's "
@@ -84,9 +88,15 @@ def make_workload(cfg, device, dtype=None):
     pw = torch.zeros(H, 68)
     eps = torch.full((H,), cfg["eps"])
     wd = torch.zeros(H)
-    cpu = dict(Q=Q, K=K, V=V, G=G, x_res=x, pos_weight=pw, eps=eps, w_dist=wd, log_mu=log_m,
+    bins = None
+    if cfg.get("full_cost"):  # drawn after the neutral terms, so the shared inputs stay identical
+        bins = torch.randint(0, 68, (B, N, N), generator=g, dtype=torch.int32)
+        pw = torch.randn(H, 68, generator=g) * 0.5
+        wd = torch.rand(H, generator=g)
+        x = torch.randn(B, N, 3, generator=g) * 3.0
+    cpu = dict(Q=Q, K=K, V=V, G=G, x_res=x, pos_weight=pw, pos_bins=bins, eps=eps, w_dist=wd, log_mu=log_m,
                log_nu=log_n, mask=None if not cfg["ragged"] else mask, dO=dO, lengths=lengths)
-    dev = {k: (v.to(device) if hasattr(v, "to") else v) for k, v in cpu.items()}
+    dev = {k: (v.to(device) if v is not None and hasattr(v, "to") else v) for k, v in cpu.items()}
     return cpu, dev
 
 
@@ -94,12 +104,19 @@ def step(cfg, t):
     from deepfold_amd import flash_sinkhorn_attn
 
     q, k, v, g = (t[n].detach().requires_grad_(True) for n in ("Q", "K", "V", "G"))
-    if cfg.get("unrolled"):
-        o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], t["w_dist"],
+    if cfg.get("full_cost"):  # position weights, geometry weights and coordinates receive gradients too
+        pw, wd, x = (t[n].detach().requires_grad_(True) for n in ("pos_weight", "w_dist", "x_res"))
+        o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, x, pw, t["pos_bins"], t["eps"], wd,
+                                            t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
+                                            ift_solver="cg", ift_iters=cfg["n_cg"])
+    elif cfg.get("unrolled"):
+        # neutral terms: no bins and no geometry weight (w_dist = None is the reference's
+        # w_dist = 0 without reading x), so the kernels built without the bias terms run
+        o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], None,
                                             t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
                                             ift_mode="unrolled")
     else:
-        o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], t["w_dist"],
+        o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], None,
                                             t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
                                             ift_solver="cg", ift_iters=cfg["n_cg"])
     o.backward(t["dO"])
@@ -107,7 +124,7 @@ def step(cfg, t):
 
 
 def algorithmic_counts(cfg, lengths):
-    """Per-layer algorithmic work (SURVEY.md section 8d): E = sum_b H n_b^2 valid
+    """Per-layer algorithmic work: E = sum_b H n_b^2 valid
     plan elements; forward 2K LSE sweeps at 2d flops + one output sweep at 4d;
     backward n_CG matvec sweeps at 2d + g_v sweep 6d + gradient sweep 8d; one
     exp per element per sweep."""
@@ -143,7 +160,8 @@ def _head_inputs(cfg, cpu, b, h, K_iter):
     sl = lambda a: a[b:b + 1, h:h + 1, :n].float().numpy()
     return dict(Q=sl(cpu["Q"]), K=sl(cpu["K"]), V=sl(cpu["V"]), G=sl(cpu["G"]),
                 x_res=cpu["x_res"][b:b + 1, :n].numpy(), pos_weight=cpu["pos_weight"][h:h + 1].numpy(),
-                pos_bins=None, eps=cpu["eps"][h:h + 1].numpy(), w_dist=cpu["w_dist"][h:h + 1].numpy(),
+                pos_bins=None if cpu.get("pos_bins") is None else cpu["pos_bins"][b:b + 1, :n, :n].numpy(),
+                eps=cpu["eps"][h:h + 1].numpy(), w_dist=cpu["w_dist"][h:h + 1].numpy(),
                 log_mu=cpu["log_mu"][b:b + 1, h:h + 1, :n].numpy(),
                 log_nu=cpu["log_nu"][b:b + 1, h:h + 1, :n].numpy(),
                 K_iter=K_iter, lam=1.0, r_0=10.0)
@@ -545,7 +563,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg5", "cfg2-unrolled", "cfg3", "cfg4", "balanced"],
+    ap.add_argument("--workload", default="cfg2",
+                    choices=["cfg2", "cfg5", "cfg2-full", "cfg2-unrolled", "cfg3", "cfg4", "balanced"],
                     help="cfg2 (default): the headline flash-Sinkhorn layer; cfg5: the N=4096 layer; "
                          "cfg3 / cfg4: attention rows")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -559,7 +578,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the flash-Sinkhorn "
-              "path shards by (b, h) with no communication, see DESIGN.md", file=sys.stderr)
+              "path shards by (b, h) with no communication between GPUs", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -39,6 +39,7 @@ hipError_t dense_sinkhorn_backward(const DenseSinkBwdArgs& a, hipStream_t s);
 hipError_t dense_zero(float* p, size_t n, hipStream_t s);
 hipError_t dense_transport_forward(const DenseTransportArgs& a, hipStream_t s);
 hipError_t dense_transport_backward(const DenseTransportArgs& a, hipStream_t s);
+hipError_t launch_bins8(const int* bins, int B, int N, uint8_t* b8, uint8_t* b8t, hipStream_t stream);
 size_t balanced_bwd_lds_bytes(int N, int DP);
 int balanced_max_tiles(int DP);
 hipError_t launch_balanced_prep(const BalPrepArgs& p, int DP, hipStream_t stream);
@@ -141,6 +142,26 @@ size_t stream_region_offset(int B, int H, int N, int G) {
   size_t off = WS_HEADER + xch_words(B, H, N) * 8 + partials_bytes(B, H, N, G);
   off += 3 * prep_operand_bytes(B, H, N) + (size_t)B * H * np32(N) * 4;
   return (off + 255) / 256 * 256;
+}
+
+// Padded uint8 bins (row-major and transposed, [B][Np][Np] each) at the end of a workspace.
+size_t bins8_bytes(int B, int N) { return (2 * (size_t)B * np32(N) * np32(N) + 255) / 256 * 256; }
+size_t sinkhorn_bins8_offset(int B, int H, int N) {
+  const int G = group_size(B, H, N);
+  return stream_region_offset(B, H, N, G) + stream_region_bytes(B, H, N, G);
+}
+// Converts the caller's int32 bins into the workspace copies; sets b8 / b8t (null without bins).
+int prepare_bins8(const int* bins, int B, int N, void* ws, size_t off, const uint8_t** b8, const uint8_t** b8t,
+                  void* stream) {
+  *b8 = *b8t = nullptr;
+  if (!bins) return 0;
+  uint8_t* p = static_cast<unsigned char*>(ws) + off;
+  const size_t per = (size_t)B * np32(N) * np32(N);
+  hipError_t e = dfl::launch_bins8(bins, B, N, p, p + per, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "bins conversion launch");
+  *b8 = p;
+  *b8t = p + per;
+  return 0;
 }
 
 struct StreamPtrs {
@@ -257,6 +278,10 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, void* workspace
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
   a.salt = next_salt();
+  if (a.bins)
+    if (int rc = prepare_bins8(a.bins, a.B, a.N, workspace, sinkhorn_bins8_offset(a.B, a.H, a.N), &a.bins8,
+                               &a.bins8t, stream))
+      return rc;
   const bool coop = G > 1;  // members wait on each other: all must be co-resident
   hipError_t e;
   if (stream_mode) {
@@ -342,7 +367,7 @@ UnrWs unr_ws_layout(int B, int H, int N, int d) {
   w.dx_part = w.xs + r256((size_t)B * 3 * np * 4);
   w.dpw_part = w.dx_part + r256((size_t)B * H * N * 3 * 4);
   w.dw_part = w.dpw_part + r256((size_t)B * H * G * 68 * 4);
-  w.total = w.dw_part + r256((size_t)B * H * G * 4);
+  w.total = w.dw_part + r256((size_t)B * H * G * 4) + bins8_bytes(B, N);  // bins copies last
   return w;
 }
 
@@ -368,7 +393,7 @@ const char* dfl_version(void) { return "deepfold_amd 0.1.0 (gfx950)"; }
 size_t dfl_sinkhorn_workspace_size(int B, int H, int N) {
   if (B <= 0 || H <= 0 || N <= 0) return 0;
   const int G = group_size(B, H, N);
-  return stream_region_offset(B, H, N, G) + stream_region_bytes(B, H, N, G);
+  return stream_region_offset(B, H, N, G) + stream_region_bytes(B, H, N, G) + bins8_bytes(B, N);
 }
 
 int dfl_workspace_error(const void* workspace, void* stream) {
@@ -480,6 +505,10 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   a.G = G;
   a.salt = next_salt();
   a.ch = CH;
+  if (p->pos_bins)
+    if (int rc = prepare_bins8(p->pos_bins, p->B, p->N, workspace, sinkhorn_bins8_offset(p->B, p->H, p->N),
+                               &a.bins8, &a.bins8t, stream))
+      return rc;
   const bool coop = G > 1;
   hipError_t e = dfl::launch_sinkhorn_bwd_prep(a, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward prep launch");
@@ -843,7 +872,10 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
   a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d; a.K = p->K_iter;
   a.eps = p->eps; a.lam = p->lam; a.r0 = p->r_0; a.mask = p->mask; a.hist = p->hist;
   a.log_mu = p->log_mu; a.log_nu = p->log_nu; a.log_u = p->log_u; a.log_z = p->log_z; a.v_init = p->log_v_init;
-  a.bins = p->pos_bins; a.pos_w = p->pos_weight; a.w_dist = p->w_dist;
+  if (int rc = prepare_bins8(p->pos_bins, p->B, p->N, workspace, L.total - bins8_bytes(p->B, p->N), &a.bins8,
+                             &a.bins8t, stream))
+    return rc;
+  a.pos_w = p->pos_weight; a.w_dist = p->w_dist;
   a.has_geo = (p->x_res && p->w_dist) ? 1 : 0;
   a.qp = pr.qp; a.kp = pr.kp; a.qt = pr.qt; a.kt = pr.kt; a.vp = pr.vp; a.gp = pr.gp; a.gt = pr.gt;
   a.dcoef = pr.dcoef; a.gxs = pr.gxs; a.xs = pr.xs;

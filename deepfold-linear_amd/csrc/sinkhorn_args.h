@@ -45,6 +45,9 @@ struct SinkFwdArgs {
   const void* kp;     // [B*H][Np][DP]
   const void* vt;     // [B*H][DP][Np]
   const float* xs_p;  // [B][Np][3]
+  // padded uint8 bins (bins8_kernel), row-major and transposed, [B][Np][Np] (null without bins)
+  const uint8_t* bins8;
+  const uint8_t* bins8t;
   // Balanced transport mode (flash_sinkhorn_transport.py:253-282, 289-320): column
   // update first, kappa = 1, uniform marginals -log(n_valid) per sample, cost
   // (1 - w_h)(1 - q.k) + w_h d/(r + d) with w_h = sigmoid(alpha_h), r = max(|r_h|, 0.1).
@@ -109,6 +112,8 @@ struct SinkBwdArgs {
   const void* qp;  // [B*H][Np][DP] zero-padded copies (sinkhorn_pad_kernel)
   const void* kp;
   float* vec_ws;   // per-workgroup vectors, BWD_STREAM_VECS * Np floats each
+  const uint8_t* bins8;   // padded uint8 bins [B][Np][Np] and transposed (null without bins)
+  const uint8_t* bins8t;
 };
 
 // Unrolled backward of the balanced transport (flash_sinkhorn_transport.py:322-373,
@@ -156,7 +161,8 @@ struct UnrBwdArgs {
   const float* log_u;    // (B,H,N) forward outputs: final u and LSE_j(u + L + v)
   const float* log_z;
   const float* v_init;   // (B,H,N) or null (zeros)
-  const int* bins;       // (B,N,N) or null
+  const uint8_t* bins8;  // padded uint8 bins [B][Np][Np] (bins8_kernel) or null
+  const uint8_t* bins8t; // transposed copy (unused here)
   const float* pos_w;    // (H,68) or null
   const float* w_dist;   // (H,) or null
   int has_geo;           // geometry term present (x given and w_dist given)

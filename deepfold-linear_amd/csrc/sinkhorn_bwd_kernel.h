@@ -100,17 +100,19 @@ __device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const
         for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
         float acc_s = 0.f;
 #pragma unroll
-        for (int k = 0; k < SCH; ++k)
+        for (int k = 0; k < SCH; ++k) {
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+            const int st = k0 + k < ks ? wave + BWD_NW * (k0 + k) : wave;
+            bv = bias.template quad<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), st * 16 + 4 * g);
+          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
-            if (GENERAL) {
-              const int ires = (rt0 + c0 + r) * 16 + (lane & 15);
-              const int jstr = (wave + BWD_NW * (k0 + k)) * 16 + 4 * g + e;
-              if (w[k][e] > 0.5f * NEG_BIG) xv += TRANS ? bias(jstr, ires) : bias(ires, jstr);
-            }
+            if (GENERAL) xv += bv[e];
             acc_s = __builtin_fmaf(fast_exp2(xv), z[k][e], acc_s);
           }
+        }
         s[r] += acc_s;
       }
     }
@@ -415,7 +417,9 @@ __host__ __device__ inline int bwd_chunk(int N) {
 }
 __host__ __device__ inline int bwd_local_rows(int N, int G) { return 16 * (((N + 15) / 16 + G - 1) / G); }
 
-template <typename T, int DP, bool STREAM>
+// GEN: the cost may carry position bins or geometry (set by the host when either is
+// passed); GEN = false compiles no bias code.
+template <typename T, int DP, bool STREAM, bool GEN>
 __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   using M = Mfma<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -523,20 +527,21 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   for (int q = threadIdx.x; q < 3 * loc; q += BWD_NT) dxs[q] = 0.f;
   for (int k = threadIdx.x; k < 68; k += BWD_NT) dpw[k] = 0.f;
   const float w_h = a.w_dist ? a.w_dist[h] : 0.f;
-  const bool use_geo = (a.x != nullptr) && (w_h != 0.f);
-  const bool use_pos = (a.bins != nullptr) && (a.pos_w != nullptr);
+  const bool use_geo = GEN && (a.x != nullptr) && (w_h != 0.f);
+  const bool use_pos = GEN && (a.bins8 != nullptr) && (a.pos_w != nullptr);
   if (use_pos)
     for (int k = threadIdx.x; k < 68; k += BWD_NT) sh.posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
   __syncthreads();
   Bias bias;
-  bias.bins = use_pos ? a.bins + (size_t)b * N * N : nullptr;
+  bias.b8 = use_pos ? a.bins8 + (size_t)b * Np * Np : nullptr;
+  bias.b8t = use_pos ? a.bins8t + (size_t)b * Np * Np : nullptr;
   bias.posw = sh.posw;
   bias.xs = use_geo ? xs : nullptr;
   bias.geo_scale = -LOG2E * w_h / eps;
   bias.r0 = a.r0;
-  bias.N = N;
+  bias.Np = Np;
   const bool general = use_pos || use_geo;
-  const bool geo_grad = a.geo_grad != 0 && a.x != nullptr;
+  const bool geo_grad = GEN && a.geo_grad != 0 && a.x != nullptr;
 
   // ---- D_i (prep kernel) for all rows
   const float* Dg = a.dcoef + bh * Np;
@@ -954,7 +959,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
                       dw_acc = __builtin_fmaf(dC, dist / rd, dw_acc);
                     }
                     if (use_pos) {
-                      const unsigned bk = (unsigned)bias.bins[(size_t)i * N + j];
+                      const unsigned bk = bias.b8[(size_t)i * Np + j];
                       if (bk < 68u) atomicAdd(&dpw[bk], dC);
                     }
                   }
@@ -1218,9 +1223,9 @@ inline size_t sinkhorn_bwd_lds_bytes_t(int N, int DP, int elem, int G, int CH, b
   return bytes;
 }
 
-template <typename T, int DP, bool STREAM>
+template <typename T, int DP, bool STREAM, bool GEN>
 static hipError_t launch_bwd_t(const SinkBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  auto kern = sinkhorn_bwd_kernel<T, DP, STREAM>;
+  auto kern = sinkhorn_bwd_kernel<T, DP, STREAM, GEN>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(BWD_NT);
@@ -1233,16 +1238,23 @@ static hipError_t launch_bwd_t(const SinkBwdArgs& a, size_t lds, hipStream_t str
   return hipGetLastError();
 }
 
-template <bool STREAM>
-hipError_t launch_bwd_mode(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+template <bool STREAM, bool GEN>
+hipError_t launch_bwd_dt(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
   if (bf16_in) {
-    if (DP == 32) return launch_bwd_t<bf16, 32, STREAM>(a, lds, stream, coop);
-    if (DP == 64) return launch_bwd_t<bf16, 64, STREAM>(a, lds, stream, coop);
+    if (DP == 32) return launch_bwd_t<bf16, 32, STREAM, GEN>(a, lds, stream, coop);
+    if (DP == 64) return launch_bwd_t<bf16, 64, STREAM, GEN>(a, lds, stream, coop);
   } else {
-    if (DP == 32) return launch_bwd_t<float, 32, STREAM>(a, lds, stream, coop);
-    if (DP == 64) return launch_bwd_t<float, 64, STREAM>(a, lds, stream, coop);
+    if (DP == 32) return launch_bwd_t<float, 32, STREAM, GEN>(a, lds, stream, coop);
+    if (DP == 64) return launch_bwd_t<float, 64, STREAM, GEN>(a, lds, stream, coop);
   }
   return hipErrorInvalidValue;
+}
+
+template <bool STREAM>
+hipError_t launch_bwd_mode(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+  const bool gen = (a.bins8 && a.pos_w) || (a.x && a.w_dist);
+  return gen ? launch_bwd_dt<STREAM, true>(a, bf16_in, DP, lds, stream, coop)
+             : launch_bwd_dt<STREAM, false>(a, bf16_in, DP, lds, stream, coop);
 }
 
 }  // namespace dfl

@@ -23,31 +23,63 @@ template <typename T, int DP> constexpr int sweep_sch() { return (sizeof(T) == 2
 
 // Position-bin / geometry bias of the cost, in log2 units of the logit:
 //   bias(i, j) = -(log2 e / eps) * (pw[bins_ij] + w * d_ij / (r0 + d_ij)).
+// Bins come as padded uint8 copies of the caller's int32 (B, N, N) array
+// (bins8_kernel): row-major b8[i][j] and transposed b8t[j][i], row stride Np,
+// 255 (no bias) outside [0, 68) and on padding, so that four consecutive indices
+// are one aligned 32-bit load in either sweep direction.
 struct Bias {
-  const int* bins;    // (N, N) of this batch row, or null
-  const float* posw;  // LDS: 68 pre-scaled weights of this head
-  const float* xs;    // LDS: coordinates [Np][3], or null (no geometry term)
-  float geo_scale;    // -log2e * w / eps
+  const uint8_t* b8;   // (Np, Np) bins of this batch row, or null
+  const uint8_t* b8t;  // the transposed copy
+  const float* posw;   // LDS: 68 pre-scaled weights of this head
+  const float* xs;     // coordinates [Np][3] (LDS or global), or null (no geometry term)
+  float geo_scale;     // -log2e * w / eps
   float r0;
-  int N;
+  int Np;
+  __device__ __forceinline__ float geo(float dx, float dy, float dz) const {
+    const float dist = fmaxf(__builtin_amdgcn_sqrtf(dx * dx + dy * dy + dz * dz), 1e-8f);
+    return geo_scale * dist * __builtin_amdgcn_rcpf(r0 + dist);
+  }
   __device__ __forceinline__ float operator()(int i, int j) const {
-    // Tile rounding can hand in rows up to 15 past the last one; their results
-    // are discarded, and clamping keeps every read inside the (N, N) bins.
-    i = min(i, N - 1);
-    j = min(j, N - 1);
+    // Tile rounding can hand in indices up to 15 past the last tile; their results
+    // are discarded, and clamping keeps every read inside the padded arrays.
+    i = min(i, Np - 1);
+    j = min(j, Np - 1);
     float b = 0.f;
-    if (bins) {
-      const unsigned k = (unsigned)bins[(size_t)i * N + j];
+    if (b8) {
+      const unsigned k = b8[(size_t)i * Np + j];
       if (k < 68u) b += posw[k];  // bins outside [0, 68) carry no bias
     }
-    if (xs) {
-      const float dx = xs[3 * i] - xs[3 * j], dy = xs[3 * i + 1] - xs[3 * j + 1], dz = xs[3 * i + 2] - xs[3 * j + 2];
-      const float dist = fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-8f);
-      b += geo_scale * dist / (r0 + dist);
-    }
+    if (xs) b += geo(xs[3 * i] - xs[3 * j], xs[3 * i + 1] - xs[3 * j + 1], xs[3 * i + 2] - xs[3 * j + 2]);
     return b;
   }
+  // The biases of resident index r against the four streamed indices s0..s0+3
+  // (s0 % 4 == 0, s0 + 3 < Np).  COL: the streamed indices are plan rows (column
+  // sweep), so the bins come from the transposed copy; the distance is symmetric.
+  template <bool COL>
+  __device__ __forceinline__ f32x4 quad(int r, int s0) const {
+    f32x4 out = {0.f, 0.f, 0.f, 0.f};
+    if (b8) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>((COL ? b8t : b8) + (size_t)r * Np + s0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned k = (w >> (8 * e)) & 0xffu;
+        out[e] = k < 68u ? posw[k] : 0.f;
+      }
+    }
+    if (xs) {
+      const float r0x = xs[3 * r], r1x = xs[3 * r + 1], r2x = xs[3 * r + 2];
+      const f32x4 p = *reinterpret_cast<const f32x4*>(xs + 3 * s0);      // rows s0, s0+1 (x, y, z, x)
+      const f32x4 q = *reinterpret_cast<const f32x4*>(xs + 3 * s0 + 4);  // (y, z, x, y)
+      const f32x4 t = *reinterpret_cast<const f32x4*>(xs + 3 * s0 + 8);  // (z, x, y, z)
+      out[0] += geo(r0x - p[0], r1x - p[1], r2x - p[2]);
+      out[1] += geo(r0x - p[3], r1x - q[0], r2x - q[1]);
+      out[2] += geo(r0x - q[2], r1x - q[3], r2x - t[0]);
+      out[3] += geo(r0x - t[1], r1x - t[2], r2x - t[3]);
+    }
+    return out;
+  }
 };
+
 
 // Stage rows [0, n) of a row-strided slice into LDS row-major [Np][DP]
 // (zero-filling columns >= d and rows >= n).  16-byte loads when the layout allows.
@@ -252,17 +284,18 @@ __device__ __forceinline__ void lse_sweep(const T* __restrict__ res_lds, const T
 #pragma unroll
         for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
 #pragma unroll
-        for (int k = 0; k < SCH; ++k)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
-            if (GENERAL) {
-              const int ires = (rt0 + c0 + r) * 16 + (lane & 15);
-              const int jstr = (wave + NW * (k0 + k)) * 16 + 4 * g + e;
-              if (w[k][e] > 0.5f * NEG_BIG) xv += TRANS ? bias(jstr, ires) : bias(ires, jstr);
-            }
-            x[k][e] = xv;
+        for (int k = 0; k < SCH; ++k) {
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+            const int st = k0 + k < ks ? wave + NW * (k0 + k) : wave;
+            bv = bias.template quad<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), st * 16 + 4 * g);
           }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {  // no `+ 0.f` without a bias: the add is not folded
+            const float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
+            x[k][e] = GENERAL ? xv + bv[e] : xv;
+          }
+        }
         if (ONLINE) {
           float tm = NEG_BIG;
 #pragma unroll
@@ -460,17 +493,18 @@ __device__ __forceinline__ void stream_sweep(const T* __restrict__ res, const T*
 #pragma unroll
           for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
 #pragma unroll
-          for (int k = 0; k < SCH; ++k)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
-              if (GENERAL) {
-                const int ires = t0 * 16 + q;
-                const int jstr = (wave + NW * (k0 + k)) * 16 + 4 * g + e;
-                if (w[k][e] > 0.5f * NEG_BIG) xv += TRANS ? bias(jstr, ires) : bias(ires, jstr);
-              }
-              x[k][e] = xv;
+          for (int k = 0; k < SCH; ++k) {
+            f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+            if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+              const int st = k0 + k < ks ? wave + NW * (k0 + k) : wave;
+              bv = bias.template quad<TRANS>(t0 * 16 + q, st * 16 + 4 * g);
             }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {  // no `+ 0.f` without a bias: the add is not folded
+              const float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
+              x[k][e] = GENERAL ? xv + bv[e] : xv;
+            }
+          }
           if (KIND == SW_LSE_ONLINE) {
             float tm = NEG_BIG;
 #pragma unroll

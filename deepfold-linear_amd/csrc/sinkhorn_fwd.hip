@@ -13,6 +13,30 @@ hipError_t launch_sinkhorn_fwd(const SinkFwdArgs& a, bool bf16_in, int DP, size_
   return launch_fwd_mode<false>(a, bf16_in, DP, lds, stream, coop);
 }
 
+// Padded uint8 bin copies (see Bias): one thread per (b, i, j) of (B, Np, Np).
+__global__ void __launch_bounds__(256) bins8_kernel(const int* __restrict__ bins, int B, int N, int Np,
+                                                    uint8_t* __restrict__ b8, uint8_t* __restrict__ b8t) {
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t per = (size_t)Np * Np;
+  if (e >= (size_t)B * per) return;
+  const int b = (int)(e / per);
+  const int i = (int)((e % per) / Np), j = (int)(e % Np);
+  int v = 255;
+  if (i < N && j < N) {
+    const int k = bins[((size_t)b * N + i) * N + j];
+    v = (k >= 0 && k < 68) ? k : 255;
+  }
+  b8[e] = (uint8_t)v;
+  b8t[(size_t)b * per + (size_t)j * Np + i] = (uint8_t)v;
+}
+
+hipError_t launch_bins8(const int* bins, int B, int N, uint8_t* b8, uint8_t* b8t, hipStream_t stream) {
+  const int Np = ((N + 31) / 32) * 32;
+  const size_t total = (size_t)B * Np * Np;
+  hipLaunchKernelGGL(bins8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, bins, B, N, Np, b8, b8t);
+  return hipGetLastError();
+}
+
 template <typename T, int DP>
 static hipError_t launch_pad_t(const PadArgs& p, hipStream_t stream) {
   const size_t Np = ((p.N + 31) / 32) * 32;

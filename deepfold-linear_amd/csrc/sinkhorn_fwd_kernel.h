@@ -152,8 +152,11 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
 // unrolled backward) or FWD_BALANCED (balanced transport, history recorded).  The
 // host picks FWD_BALANCED exactly when a.balanced != 0 and FWD_UOT_HIST when a.hist
 // is given.
+// GEN: the cost may carry position bins or geometry (the host sets it when either
+// is passed); GEN = false compiles no bias code, which keeps the content-only
+// sweeps at their register budget.
 enum FwdMode : int { FWD_UOT = 0, FWD_UOT_HIST = 1, FWD_BALANCED = 2 };
-template <typename T, int DP, bool STREAM, int MODE>
+template <typename T, int DP, bool STREAM, int MODE, bool GEN>
 __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   constexpr bool BAL = MODE == FWD_BALANCED;
   constexpr bool HIST = MODE != FWD_UOT;
@@ -257,8 +260,8 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     vecV[i] = ok ? (a.v_init ? a.v_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
   }
   const float w_h = bal ? w_bal : (a.w_dist ? a.w_dist[h] : 0.f);
-  const bool use_geo = (a.x != nullptr) && (w_h != 0.f);
-  const bool use_pos = (a.bins != nullptr) && (a.pos_w != nullptr);
+  const bool use_geo = GEN && (a.x != nullptr) && (w_h != 0.f);
+  const bool use_pos = GEN && (a.bins8 != nullptr) && (a.pos_w != nullptr);
   if (use_pos)
     for (int k = threadIdx.x; k < 68; k += FWD_NT) s_posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
   // coordinates of this batch row: LDS (resident) or the padded global copy (stream)
@@ -270,16 +273,18 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   }
   __syncthreads();
   Bias bias;
-  bias.bins = use_pos ? a.bins + (size_t)b * N * N : nullptr;
+  bias.b8 = use_pos ? a.bins8 + (size_t)b * Np * Np : nullptr;
+  bias.b8t = use_pos ? a.bins8t + (size_t)b * Np * Np : nullptr;
   bias.posw = s_posw;
   bias.xs = use_geo ? xsrc : nullptr;
   bias.geo_scale = -LOG2E * w_h / eps;
   bias.r0 = bal ? fmaxf(fabsf(a.r_h[h]), 0.1f) : a.r0;
-  bias.N = N;
+  bias.Np = Np;
   const bool general = use_pos || use_geo;
 
   // sweep dispatch: ROW = plan rows resident (Q), streamed K against v; else the transpose
-  auto sweep = [&](bool row, bool online, float* lse, float* mx, unsigned* s_reset, auto pub) {
+  auto sweep = [&](bool row, bool online, float* lse, float* mx, unsigned* s_reset, auto pub)
+                   __attribute__((always_inline)) {
     if constexpr (STREAM) {
       const T* res = row ? QS : KS;
       const T* str = row ? Kp : Qp;
@@ -312,7 +317,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
 
   // History for the unrolled backward: this member's stripe of the vector just
   // exchanged, copied from its own words (exact published values), outside the sweep.
-  auto record = [&](const uint64_t* words, int slot) {
+  auto record = [&](const uint64_t* words, int slot) __attribute__((always_inline)) {
     for (int q = threadIdx.x; q < nr * 16; q += FWD_NT) {
       const int i = r_lo + q;
       if (i < n) {
@@ -323,7 +328,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     }
   };
   // ---- row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j)) for my rows
-  auto row_update = [&](int it) -> bool {
+  auto row_update = [&](int it) __attribute__((always_inline)) -> bool {
     ++phase;
     {
       const uint32_t tag = salt | phase;
@@ -339,7 +344,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     return true;
   };
   // ---- column update: v_j = kappa (log nu_j - LSE_i(L_ij + u_i)) for my columns
-  auto col_update = [&](int it) -> bool {
+  auto col_update = [&](int it) __attribute__((always_inline)) -> bool {
     ++phase;
     {
       const uint32_t tag = salt | phase;
@@ -549,9 +554,9 @@ inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stre
   return bytes;
 }
 
-template <typename T, int DP, bool STREAM, int MODE>
+template <typename T, int DP, bool STREAM, int MODE, bool GEN>
 static hipError_t launch_fwd_t(const SinkFwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  auto kern = sinkhorn_fwd_kernel<T, DP, STREAM, MODE>;
+  auto kern = sinkhorn_fwd_kernel<T, DP, STREAM, MODE, GEN>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(FWD_NT);
@@ -564,32 +569,33 @@ static hipError_t launch_fwd_t(const SinkFwdArgs& a, size_t lds, hipStream_t str
   return hipGetLastError();
 }
 
-template <bool STREAM>
-hipError_t launch_fwd_mode(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
-  if (a.balanced) {  // the balanced transport computes in fp32 only
-    if (bf16_in || !a.hist) return hipErrorInvalidValue;
-    if (DP == 32) return launch_fwd_t<float, 32, STREAM, FWD_BALANCED>(a, lds, stream, coop);
-    if (DP == 64) return launch_fwd_t<float, 64, STREAM, FWD_BALANCED>(a, lds, stream, coop);
-    return hipErrorInvalidValue;
-  }
-  if (a.hist) {
-    if (bf16_in) {
-      if (DP == 32) return launch_fwd_t<bf16, 32, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
-      if (DP == 64) return launch_fwd_t<bf16, 64, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
-    } else {
-      if (DP == 32) return launch_fwd_t<float, 32, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
-      if (DP == 64) return launch_fwd_t<float, 64, STREAM, FWD_UOT_HIST>(a, lds, stream, coop);
-    }
-    return hipErrorInvalidValue;
-  }
+template <bool STREAM, int MODE, bool GEN>
+hipError_t launch_fwd_dt(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
   if (bf16_in) {
-    if (DP == 32) return launch_fwd_t<bf16, 32, STREAM, FWD_UOT>(a, lds, stream, coop);
-    if (DP == 64) return launch_fwd_t<bf16, 64, STREAM, FWD_UOT>(a, lds, stream, coop);
+    if constexpr (MODE == FWD_BALANCED) return hipErrorInvalidValue;  // the balanced transport is fp32 only
+    else {
+      if (DP == 32) return launch_fwd_t<bf16, 32, STREAM, MODE, GEN>(a, lds, stream, coop);
+      if (DP == 64) return launch_fwd_t<bf16, 64, STREAM, MODE, GEN>(a, lds, stream, coop);
+    }
   } else {
-    if (DP == 32) return launch_fwd_t<float, 32, STREAM, FWD_UOT>(a, lds, stream, coop);
-    if (DP == 64) return launch_fwd_t<float, 64, STREAM, FWD_UOT>(a, lds, stream, coop);
+    if (DP == 32) return launch_fwd_t<float, 32, STREAM, MODE, GEN>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<float, 64, STREAM, MODE, GEN>(a, lds, stream, coop);
   }
   return hipErrorInvalidValue;
+}
+
+template <bool STREAM>
+hipError_t launch_fwd_mode(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+  if (a.balanced) {
+    if (!a.hist) return hipErrorInvalidValue;
+    return launch_fwd_dt<STREAM, FWD_BALANCED, true>(a, bf16_in, DP, lds, stream, coop);
+  }
+  const bool gen = (a.bins8 && a.pos_w) || (a.x && a.w_dist);
+  if (a.hist)
+    return gen ? launch_fwd_dt<STREAM, FWD_UOT_HIST, true>(a, bf16_in, DP, lds, stream, coop)
+               : launch_fwd_dt<STREAM, FWD_UOT_HIST, false>(a, bf16_in, DP, lds, stream, coop);
+  return gen ? launch_fwd_dt<STREAM, FWD_UOT, true>(a, bf16_in, DP, lds, stream, coop)
+             : launch_fwd_dt<STREAM, FWD_UOT, false>(a, bf16_in, DP, lds, stream, coop);
 }
 
 }  // namespace dfl

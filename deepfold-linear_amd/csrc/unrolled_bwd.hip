@@ -198,8 +198,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const float bsc = -LOG2E / eps;  // bias (pw + w d/(r0 + d)) -> log2 logit
   const float wd = a.w_dist ? a.w_dist[h] : 0.f;
   const bool geo = a.has_geo != 0 && wd != 0.f;
-  const bool use_bins = a.bins != nullptr;
-  const int* bins_b = use_bins ? a.bins + (size_t)b * N * N : nullptr;
+  const bool use_bins = a.bins8 != nullptr;
+  const uint8_t* bins_b = use_bins ? a.bins8 + (size_t)b * Np * Np : nullptr;
   const float r0 = a.r0;
   const int r_lo = t0 * 16;
   const float* hist = a.hist;
@@ -394,8 +394,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const int sj = min(o + e, N - 1);  // streamed index (clamped for the bins read)
-              const int ii = ROW ? min(ri, N - 1) : sj, jj = ROW ? sj : min(ri, N - 1);
+              const int sj = o + e;  // streamed index (< Np: padded bins read 255)
+              const int ii = ROW ? ri : sj, jj = ROW ? sj : ri;
               float bias = 0.f, cg = 0.f, dist = 1.f;
               const float dx = xr0[s] - sx0[e], dy = xr1[s] - sx1[e], dz = xr2[s] - sx2[e];
               if (geo) {
@@ -405,8 +405,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
               }
               int bin = -1;
               if (use_bins) {
-                bin = bins_b[(size_t)ii * N + jj];
-                if ((unsigned)bin < 68u) bias += s_pw[bin];
+                bin = bins_b[(size_t)ii * Np + jj];
+                if (bin < 68) bias += s_pw[bin];
                 else bin = -1;
               }
               const float lg = __builtin_fmaf(x[e], sc, bsc * bias);

@@ -16,7 +16,7 @@ vv137/deepfold-linear's CPU fallback for ``flash_sinkhorn_attn``:
                             (b, h) (only the summation order differs from the
                             64x64 tiling).
 * ``backward_analytic``  -- the true implicit adjoint of the converged map
-                            (derivation in DESIGN.md; differs from the reference
+                            (implicit-function adjoint of the fixed point; differs from the reference
                             in the sign of the z_v*S_col term and of d log_mu).
 * ``cg_system``          -- the symmetric positive-definite form
                             (I - kappa^2 W^T W) y = D_c^{-1/2} g_v of the IFT
