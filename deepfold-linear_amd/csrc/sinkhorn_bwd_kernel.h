@@ -95,21 +95,23 @@ __device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const
         M::load(bf, res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
         const float ci = cres[(c0 + r) * 16 + (lane & 15)] * isc;
         const f32x4 cinit = f32x4{ci, ci, ci, ci};
+        f32x4 bv[SCH];
+        if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+          int s0[SCH];
+#pragma unroll
+          for (int k = 0; k < SCH; ++k) s0[k] = (k0 + k < ks ? wave + BWD_NW * (k0 + k) : wave) * 16 + 4 * g;
+          bias.template quads<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), s0, bv);
+        }
         f32x4 x[SCH];
 #pragma unroll
         for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
         float acc_s = 0.f;
 #pragma unroll
         for (int k = 0; k < SCH; ++k) {
-          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-          if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
-            const int st = k0 + k < ks ? wave + BWD_NW * (k0 + k) : wave;
-            bv = bias.template quad<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), st * 16 + 4 * g);
-          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
-            if (GENERAL) xv += bv[e];
+            if (GENERAL) xv += bv[k][e];
             acc_s = __builtin_fmaf(fast_exp2(xv), z[k][e], acc_s);
           }
         }
@@ -406,7 +408,7 @@ __device__ __forceinline__ void stage_jobs(const StageJob (&J)[NJ], int r0, int 
 
 struct BwdShared {
   int flag, tmp;
-  float posw[68];
+  float posw[BIN_NONE + 1];
   float red[2 * BWD_NW];
 };
 
@@ -530,7 +532,8 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const bool use_geo = GEN && (a.x != nullptr) && (w_h != 0.f);
   const bool use_pos = GEN && (a.bins8 != nullptr) && (a.pos_w != nullptr);
   if (use_pos)
-    for (int k = threadIdx.x; k < 68; k += BWD_NT) sh.posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
+    for (int k = threadIdx.x; k <= (int)BIN_NONE; k += BWD_NT)
+      sh.posw[k] = k < (int)BIN_NONE ? -LOG2E * a.pos_w[h * 68 + k] / eps : 0.f;
   __syncthreads();
   Bias bias;
   bias.b8 = use_pos ? a.bins8 + (size_t)b * Np * Np : nullptr;

@@ -25,12 +25,16 @@ template <typename T, int DP> constexpr int sweep_sch() { return (sizeof(T) == 2
 //   bias(i, j) = -(log2 e / eps) * (pw[bins_ij] + w * d_ij / (r0 + d_ij)).
 // Bins come as padded uint8 copies of the caller's int32 (B, N, N) array
 // (bins8_kernel): row-major b8[i][j] and transposed b8t[j][i], row stride Np,
-// 255 (no bias) outside [0, 68) and on padding, so that four consecutive indices
-// are one aligned 32-bit load in either sweep direction.
+// BIN_NONE = 68 outside [0, 68) and on padding (its table entry is 0), so that four
+// consecutive indices are one aligned 32-bit load in either sweep direction and the
+// lookup needs no range test.  The geometry term is evaluated from the coordinates
+// (LDS in resident storage): cheaper than reading a precomputed d/(r0 + d) matrix,
+// whose per-quad 16-byte global loads cost the forward a third more on MI355X.
+constexpr unsigned BIN_NONE = 68;
 struct Bias {
   const uint8_t* b8;   // (Np, Np) bins of this batch row, or null
   const uint8_t* b8t;  // the transposed copy
-  const float* posw;   // LDS: 68 pre-scaled weights of this head
+  const float* posw;   // LDS: 69 pre-scaled weights of this head, posw[BIN_NONE] = 0
   const float* xs;     // coordinates [Np][3] (LDS or global), or null (no geometry term)
   float geo_scale;     // -log2e * w / eps
   float r0;
@@ -45,38 +49,43 @@ struct Bias {
     i = min(i, Np - 1);
     j = min(j, Np - 1);
     float b = 0.f;
-    if (b8) {
-      const unsigned k = b8[(size_t)i * Np + j];
-      if (k < 68u) b += posw[k];  // bins outside [0, 68) carry no bias
-    }
+    if (b8) b += posw[b8[(size_t)i * Np + j]];
     if (xs) b += geo(xs[3 * i] - xs[3 * j], xs[3 * i + 1] - xs[3 * j + 1], xs[3 * i + 2] - xs[3 * j + 2]);
     return b;
   }
-  // The biases of resident index r against the four streamed indices s0..s0+3
-  // (s0 % 4 == 0, s0 + 3 < Np).  COL: the streamed indices are plan rows (column
-  // sweep), so the bins come from the transposed copy; the distance is symmetric.
-  template <bool COL>
-  __device__ __forceinline__ f32x4 quad(int r, int s0) const {
-    f32x4 out = {0.f, 0.f, 0.f, 0.f};
-    if (b8) {
-      const uint32_t w = *reinterpret_cast<const uint32_t*>((COL ? b8t : b8) + (size_t)r * Np + s0);
+  // The biases of resident index r against the four streamed indices s0[k]..s0[k]+3
+  // of each of S streamed tiles (s0 % 4 == 0, s0 + 3 < Np).  COL: the streamed
+  // indices are plan rows (column sweep), so the bins come from the transposed copy;
+  // the distance is symmetric.  All S bin words are loaded under one test, back to
+  // back, so their latencies overlap (a test per word leaves one wait per load).
+  template <bool COL, int S>
+  __device__ __forceinline__ void quads(int r, const int (&s0)[S], f32x4 (&out)[S]) const {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const unsigned k = (w >> (8 * e)) & 0xffu;
-        out[e] = k < 68u ? posw[k] : 0.f;
-      }
+    for (int k = 0; k < S; ++k) out[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (b8) {
+      const uint8_t* row = (COL ? b8t : b8) + (size_t)r * Np;
+      uint32_t w[S];
+#pragma unroll
+      for (int k = 0; k < S; ++k) w[k] = *reinterpret_cast<const uint32_t*>(row + s0[k]);
+#pragma unroll
+      for (int k = 0; k < S; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[k][e] = posw[(w[k] >> (8 * e)) & 0xffu];
     }
     if (xs) {
       const float r0x = xs[3 * r], r1x = xs[3 * r + 1], r2x = xs[3 * r + 2];
-      const f32x4 p = *reinterpret_cast<const f32x4*>(xs + 3 * s0);      // rows s0, s0+1 (x, y, z, x)
-      const f32x4 q = *reinterpret_cast<const f32x4*>(xs + 3 * s0 + 4);  // (y, z, x, y)
-      const f32x4 t = *reinterpret_cast<const f32x4*>(xs + 3 * s0 + 8);  // (z, x, y, z)
-      out[0] += geo(r0x - p[0], r1x - p[1], r2x - p[2]);
-      out[1] += geo(r0x - p[3], r1x - q[0], r2x - q[1]);
-      out[2] += geo(r0x - q[2], r1x - q[3], r2x - t[0]);
-      out[3] += geo(r0x - t[1], r1x - t[2], r2x - t[3]);
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        const float* c = xs + 3 * s0[k];
+        const f32x4 p = *reinterpret_cast<const f32x4*>(c);      // rows s0, s0+1 (x, y, z, x)
+        const f32x4 q = *reinterpret_cast<const f32x4*>(c + 4);  // (y, z, x, y)
+        const f32x4 t = *reinterpret_cast<const f32x4*>(c + 8);  // (z, x, y, z)
+        out[k][0] += geo(r0x - p[0], r1x - p[1], r2x - p[2]);
+        out[k][1] += geo(r0x - p[3], r1x - q[0], r2x - q[1]);
+        out[k][2] += geo(r0x - q[2], r1x - q[3], r2x - t[0]);
+        out[k][3] += geo(r0x - t[1], r1x - t[2], r2x - t[3]);
+      }
     }
-    return out;
   }
 };
 
@@ -280,22 +289,23 @@ __device__ __forceinline__ void lse_sweep(const T* __restrict__ res_lds, const T
           const float ci = -shift2[(c0 + r) * 16 + (lane & 15)] * isc;
           cinit = f32x4{ci, ci, ci, ci};
         }
+        f32x4 bv[SCH];
+        if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+          int s0[SCH];
+#pragma unroll
+          for (int k = 0; k < SCH; ++k) s0[k] = (k0 + k < ks ? wave + NW * (k0 + k) : wave) * 16 + 4 * g;
+          bias.template quads<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), s0, bv);
+        }
         f32x4 x[SCH];
 #pragma unroll
         for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
 #pragma unroll
-        for (int k = 0; k < SCH; ++k) {
-          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-          if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
-            const int st = k0 + k < ks ? wave + NW * (k0 + k) : wave;
-            bv = bias.template quad<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), st * 16 + 4 * g);
-          }
+        for (int k = 0; k < SCH; ++k)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {  // no `+ 0.f` without a bias: the add is not folded
             const float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
-            x[k][e] = GENERAL ? xv + bv[e] : xv;
+            x[k][e] = GENERAL ? xv + bv[k][e] : xv;
           }
-        }
         if (ONLINE) {
           float tm = NEG_BIG;
 #pragma unroll
@@ -489,22 +499,23 @@ __device__ __forceinline__ void stream_sweep(const T* __restrict__ res, const T*
             const float ci = (KIND == SW_LSE_FIXED ? -cres[q] : cres[q]) * isc;
             cinit = f32x4{ci, ci, ci, ci};
           }
+          f32x4 bv[SCH];
+          if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+            int s0[SCH];
+#pragma unroll
+            for (int k = 0; k < SCH; ++k) s0[k] = (k0 + k < ks ? wave + NW * (k0 + k) : wave) * 16 + 4 * g;
+            bias.template quads<TRANS>(t0 * 16 + q, s0, bv);
+          }
           f32x4 x[SCH];
 #pragma unroll
           for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
 #pragma unroll
-          for (int k = 0; k < SCH; ++k) {
-            f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-            if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
-              const int st = k0 + k < ks ? wave + NW * (k0 + k) : wave;
-              bv = bias.template quad<TRANS>(t0 * 16 + q, st * 16 + 4 * g);
-            }
+          for (int k = 0; k < SCH; ++k)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {  // no `+ 0.f` without a bias: the add is not folded
               const float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
-              x[k][e] = GENERAL ? xv + bv[e] : xv;
+              x[k][e] = GENERAL ? xv + bv[k][e] : xv;
             }
-          }
           if (KIND == SW_LSE_ONLINE) {
             float tm = NEG_BIG;
 #pragma unroll

@@ -21,10 +21,10 @@ __global__ void __launch_bounds__(256) bins8_kernel(const int* __restrict__ bins
   if (e >= (size_t)B * per) return;
   const int b = (int)(e / per);
   const int i = (int)((e % per) / Np), j = (int)(e % Np);
-  int v = 255;
+  int v = (int)BIN_NONE;
   if (i < N && j < N) {
     const int k = bins[((size_t)b * N + i) * N + j];
-    v = (k >= 0 && k < 68) ? k : 255;
+    v = (k >= 0 && k < 68) ? k : (int)BIN_NONE;
   }
   b8[e] = (uint8_t)v;
   b8t[(size_t)b * per + (size_t)j * Np + i] = (uint8_t)v;

@@ -164,7 +164,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   __shared__ int s_flag, s_tmp;
   __shared__ unsigned s_du, s_dv;
   __shared__ int s_cnt;
-  __shared__ float s_posw[68];
+  __shared__ float s_posw[BIN_NONE + 1];
   int grp, member;
   if (!group_of(a.B * a.H, a.G, grp, member)) return;  // surplus workgroup of the XCD-aligned grid
   const int b = grp / a.H, h = grp % a.H;
@@ -263,7 +263,8 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const bool use_geo = GEN && (a.x != nullptr) && (w_h != 0.f);
   const bool use_pos = GEN && (a.bins8 != nullptr) && (a.pos_w != nullptr);
   if (use_pos)
-    for (int k = threadIdx.x; k < 68; k += FWD_NT) s_posw[k] = -LOG2E * a.pos_w[h * 68 + k] / eps;
+    for (int k = threadIdx.x; k <= (int)BIN_NONE; k += FWD_NT)
+      s_posw[k] = k < (int)BIN_NONE ? -LOG2E * a.pos_w[h * 68 + k] / eps : 0.f;
   // coordinates of this batch row: LDS (resident) or the padded global copy (stream)
   const float* xsrc = xs;
   if constexpr (STREAM) {

@@ -394,7 +394,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const int sj = o + e;  // streamed index (< Np: padded bins read 255)
+              const int sj = o + e;  // streamed index (< Np: padded bins read BIN_NONE)
               const int ii = ROW ? ri : sj, jj = ROW ? sj : ri;
               float bias = 0.f, cg = 0.f, dist = 1.f;
               const float dx = xr0[s] - sx0[e], dy = xr1[s] - sx1[e], dz = xr2[s] - sx2[e];
