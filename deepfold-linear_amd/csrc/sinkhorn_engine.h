@@ -28,8 +28,8 @@ template <typename T, int DP> constexpr int sweep_sch() { return (sizeof(T) == 2
 // BIN_NONE = 68 outside [0, 68) and on padding (its table entry is 0), so that four
 // consecutive indices are one aligned 32-bit load in either sweep direction and the
 // lookup needs no range test.  The geometry term is evaluated from the coordinates
-// (LDS in resident storage): cheaper than reading a precomputed d/(r0 + d) matrix,
-// whose per-quad 16-byte global loads cost the forward a third more on MI355X.
+// (LDS in resident storage): on MI355X that is cheaper than reading a precomputed
+// fp32 d/(r0 + d) matrix from L2 (16-byte loads per quad made the forward 13% slower).
 constexpr unsigned BIN_NONE = 68;
 struct Bias {
   const uint8_t* b8;   // (Np, Np) bins of this batch row, or null

@@ -52,6 +52,8 @@ int dfl_workspace_error(const void* workspace, void* stream);
  * q, k, v, g: (B,H,N,d) elements of `dtype` at q + b*stride_b + h*stride_h + n*stride_n + c.
  * g may be NULL (no gate: o = O_avg).  x_res (B,N,3), pos_weight (H,68), pos_bins (B,N,N)
  * int32, w_dist (H,), log_u_init/log_v_init (B,H,N) and mask (B,N) may be NULL.
+ * Bins outside [0, 68) add no position bias.  NULL w_dist means no geometry term (the
+ * kernels then carry no distance code; x_res is still the coordinate input of x_centroid).
  * Outputs o_flat (B,N,H*d), x_centroid (B,H,N,3), log_u, log_v (B,H,N); saved for the
  * backward: o_avg (B,H,N,d), log_z (B,H,N) = LSE_j(u_i + L_ij + v_j) and
  * col_lse (B,H,N) = LSE_i(L_ij + u_i) of the last column update.

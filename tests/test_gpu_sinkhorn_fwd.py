@@ -91,6 +91,28 @@ def test_forward_general_cost(dtype, tol):
         assert_close_rel(gv, want[name], tol, name)
 
 
+def test_forward_bins_outside_table_add_no_bias():
+    """Bins outside [0, 68) carry no position bias (the reference's fallback raises on
+    them and its kernel gathers out of bounds): the result equals the oracle's with a
+    69-entry table whose entry 68 is 0 and those bins remapped to 68."""
+    inp = make_inputs(2, 2, 48, 32, seed=77, eps=[0.5, 1.0], pos_geo=True)
+    g = torch.Generator().manual_seed(78)
+    bins = inp["pos_bins"].clone()
+    sel = torch.rand(bins.shape, generator=g) < 0.2
+    bad = torch.tensor([-1, 68, 200, 1 << 20], dtype=torch.int32)[torch.randint(0, 4, bins.shape, generator=g)]
+    bins[sel] = bad[sel]
+    inp["pos_bins"] = bins
+    got = run_gpu(inp, 6, torch.float32)
+    oi = oracle_inputs(inp, torch.float32)
+    oi["pos_weight"] = np.concatenate([oi["pos_weight"], np.zeros((2, 1), np.float32)], 1)
+    b = oi["pos_bins"].astype(np.int64)
+    b[(b < 0) | (b >= 68)] = 68
+    oi["pos_bins"] = b
+    want = ref.forward(**oi, K_iter=6)
+    for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
+        assert_close_rel(gv, want[name], 1e-4, name)
+
+
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
 def test_forward_masked_equals_unpadded(dtype, tol):
     B, H, N, d = 3, 2, 96, 32
