@@ -12,8 +12,13 @@
 #include "attn_args.h"
 #include "dense_args.h"
 #include "sinkhorn_args.h"
+#include "trunk_args.h"
 
 namespace dfl {
+size_t proj_fwd_lds_bytes(int C, bool bf16_in);
+hipError_t launch_proj_fwd(const ProjArgs& a, bool bf16_in, hipStream_t s);
+hipError_t launch_proj_bwd(const ProjArgs& a, bool bf16_in, hipStream_t s);
+hipError_t launch_coord(const CoordArgs& a, bool bf16_in, bool bwd, hipStream_t s);
 size_t sinkhorn_fwd_lds_bytes(int N, int DP, int elem, int G, bool stream);
 hipError_t launch_sinkhorn_fwd(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                bool coop);
@@ -891,6 +896,126 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
   e = dfl::launch_unrolled_finalize(a, p->x_res ? p->dx_res : nullptr, p->dpos_weight, p->dw_dist,
                                     (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "unrolled backward finalize launch");
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// TokenOTBlock steps either side of the balanced transport.
+
+static size_t r256z(size_t x) { return (x + 255) / 256 * 256; }
+static constexpr int TRUNK_PARTS = 64;  // partial rows written by the per-token kernels
+
+static int check_proj(const dfl_sink_proj_params* p) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_F32 && p->dtype != DFL_BF16) return fail("dtype must be DFL_F32 or DFL_BF16");
+  if (p->M <= 0 || p->C <= 0 || p->H <= 0) return fail("M, C, H must be positive");
+  if (p->C % 64 != 0 || p->C > 1024 || p->C % p->H != 0)
+    return fail("C=%d must be a multiple of 64 and of H=%d, at most 1024", p->C, p->H);
+  const int dh = p->C / p->H;
+  if (dh != 16 && dh != 32 && dh != 64) return fail("head dim C/H=%d must be 16, 32 or 64", dh);
+  if (dfl::proj_fwd_lds_bytes(p->C, p->dtype == DFL_BF16) + 1024 > LDS_LIMIT)
+    return fail("C=%d too large for the %s projection (LDS)", p->C, p->dtype == DFL_BF16 ? "bf16" : "fp32");
+  if (!p->h || !p->ln_weight || !p->ln_bias || !p->w_q || !p->w_k) return fail("required input is NULL");
+  return 0;
+}
+
+static dfl::ProjArgs proj_args(const dfl_sink_proj_params* p) {
+  dfl::ProjArgs a;
+  memset(&a, 0, sizeof(a));
+  a.h = p->h; a.ln_w = p->ln_weight; a.ln_b = p->ln_bias;
+  a.w[0] = p->w_q; a.w[1] = p->w_k; a.w[2] = p->w_v;
+  a.y[0] = p->q_s; a.y[1] = p->k_s; a.y[2] = p->v_s;
+  a.norm[0] = p->q_norm; a.norm[1] = p->k_norm;
+  a.mean = p->ln_mean; a.rstd = p->ln_rstd;
+  a.M = p->M; a.C = p->C; a.H = p->H;
+  return a;
+}
+
+size_t dfl_sink_proj_workspace_size(int M, int C) {
+  if (M <= 0 || C <= 0) return 0;
+  const size_t mc = r256z((size_t)M * C * 4);
+  return 6 * mc + r256z((size_t)TRUNK_PARTS * 2 * C * 4);  // du x3, xa, xn, dxa; LayerNorm partials
+}
+
+int dfl_sink_proj_fwd(const dfl_sink_proj_params* p, void* stream) {
+  if (int rc = check_proj(p)) return rc;
+  if (!p->q_s || !p->k_s || (p->w_v && !p->v_s) || !p->q_norm || !p->k_norm || !p->ln_mean || !p->ln_rstd)
+    return fail("output pointer is NULL");
+  hipError_t e = dfl::launch_proj_fwd(proj_args(p), p->dtype == DFL_BF16, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "sink projection launch");
+  return 0;
+}
+
+int dfl_sink_proj_bwd(const dfl_sink_proj_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_proj(p)) return rc;
+  if (!p->q_s || !p->k_s || !p->q_norm || !p->k_norm || !p->ln_mean || !p->ln_rstd)
+    return fail("saved forward value is NULL");
+  if (!p->dh) return fail("dh is NULL");
+  if (p->dw_v && !p->w_v) return fail("dw_v needs w_v");
+  const size_t need = dfl_sink_proj_workspace_size(p->M, p->C);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  dfl::ProjArgs a = proj_args(p);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const size_t mc = r256z((size_t)p->M * p->C * 4);
+  for (int i = 0; i < 3; ++i) a.du[i] = reinterpret_cast<float*>(ws + i * mc);
+  a.xa = reinterpret_cast<float*>(ws + 3 * mc);
+  a.xn = reinterpret_cast<float*>(ws + 4 * mc);
+  a.dxa = reinterpret_cast<float*>(ws + 5 * mc);
+  a.part = reinterpret_cast<float*>(ws + 6 * mc);
+  a.dy[0] = p->dq_s; a.dy[1] = p->dk_s; a.dy[2] = p->w_v ? p->dv_s : nullptr;
+  a.dh = p->dh; a.dln_w = p->dln_weight; a.dln_b = p->dln_bias;
+  a.dw[0] = p->dw_q; a.dw[1] = p->dw_k; a.dw[2] = p->dw_v;
+  hipError_t e = dfl::launch_proj_bwd(a, p->dtype == DFL_BF16, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "sink projection backward launch");
+  return 0;
+}
+
+static int check_coord(const dfl_coord_update_params* p) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_F32 && p->dtype != DFL_BF16) return fail("dtype must be DFL_F32 or DFL_BF16");
+  if (p->B <= 0 || p->N <= 0 || p->C <= 0 || p->H <= 0) return fail("B, N, C, H must be positive");
+  if (p->C % 64 != 0 || p->C > 1024) return fail("C=%d must be a multiple of 64 and at most 1024", p->C);
+  if (p->H > 64) return fail("H=%d > 64 is not supported", p->H);
+  if (!p->h || !p->ln_weight || !p->ln_bias || !p->w_gate || !p->b_gate || !p->lambda_raw || !p->x_centroid ||
+      !p->x_res)
+    return fail("required input is NULL");
+  return 0;
+}
+
+static dfl::CoordArgs coord_args(const dfl_coord_update_params* p) {
+  dfl::CoordArgs a;
+  memset(&a, 0, sizeof(a));
+  a.h = p->h; a.ln_w = p->ln_weight; a.ln_b = p->ln_bias; a.w_gate = p->w_gate; a.b_gate = p->b_gate;
+  a.lam_raw = p->lambda_raw; a.xc = p->x_centroid; a.x = p->x_res; a.mask = p->mask; a.x_out = p->x_out;
+  a.B = p->B; a.N = p->N; a.C = p->C; a.H = p->H;
+  return a;
+}
+
+size_t dfl_coord_update_workspace_size(int C, int H) {
+  if (C <= 0 || H <= 0) return 0;
+  return r256z((size_t)TRUNK_PARTS * (3 * C + H + 1) * 4);
+}
+
+int dfl_coord_update_fwd(const dfl_coord_update_params* p, void* stream) {
+  if (int rc = check_coord(p)) return rc;
+  if (!p->x_out) return fail("x_out is NULL");
+  hipError_t e = dfl::launch_coord(coord_args(p), p->dtype == DFL_BF16, false, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "coordinate update launch");
+  return 0;
+}
+
+int dfl_coord_update_bwd(const dfl_coord_update_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_coord(p)) return rc;
+  if (!p->dx_out || !p->dx_res || !p->dx_centroid || !p->dh) return fail("gradient pointer is NULL");
+  const size_t need = dfl_coord_update_workspace_size(p->C, p->H);
+  if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
+  dfl::CoordArgs a = coord_args(p);
+  a.dx_out = p->dx_out; a.dx = p->dx_res; a.dxc = p->dx_centroid; a.dh = p->dh;
+  a.dln_w = p->dln_weight; a.dln_b = p->dln_bias; a.dw_gate = p->dw_gate; a.db_gate = p->db_gate;
+  a.dlam_raw = p->dlambda_raw;
+  a.part = static_cast<float*>(workspace);
+  hipError_t e = dfl::launch_coord(a, p->dtype == DFL_BF16, true, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "coordinate update backward launch");
   return 0;
 }
 

@@ -15,5 +15,7 @@ from .flash_sinkhorn_transport import (  # noqa: F401
     BalancedSinkhornDualFn, BalancedSinkhornFn, balanced_sinkhorn_transport, balanced_sinkhorn_transport_dual)
 from .sinkhorn import compute_transport_output, sinkhorn_solve  # noqa: F401
 from .sinkhorn_kernel import FlashSinkhornFunction, flash_sinkhorn  # noqa: F401
+from .trunk_steps import (  # noqa: F401
+    GatedCoordUpdateFn, SinkProjectionFn, gated_coordinate_update, sink_projections, token_ot_transport_step)
 
 __version__ = "0.1.0"

@@ -185,6 +185,33 @@ class BalancedBwdParams(ctypes.Structure):
     ]
 
 
+class SinkProjParams(ctypes.Structure):
+    """Mirror of ``dfl_sink_proj_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("h", P), ("ln_weight", P), ("ln_bias", P), ("w_q", P), ("w_k", P), ("w_v", P),
+        ("M", I32), ("C", I32), ("H", I32),
+        ("q_s", P), ("k_s", P), ("v_s", P), ("q_norm", P), ("k_norm", P), ("ln_mean", P), ("ln_rstd", P),
+        ("dq_s", P), ("dk_s", P), ("dv_s", P),
+        ("dh", P), ("dln_weight", P), ("dln_bias", P), ("dw_q", P), ("dw_k", P), ("dw_v", P),
+    ]
+
+
+class CoordUpdateParams(ctypes.Structure):
+    """Mirror of ``dfl_coord_update_params``."""
+
+    _fields_ = [
+        ("dtype", I32),
+        ("h", P), ("ln_weight", P), ("ln_bias", P), ("w_gate", P), ("b_gate", P), ("lambda_raw", P),
+        ("x_centroid", P), ("x_res", P), ("mask", P),
+        ("B", I32), ("N", I32), ("C", I32), ("H", I32),
+        ("x_out", P),
+        ("dx_out", P), ("dx_res", P), ("dx_centroid", P), ("dh", P), ("dln_weight", P), ("dln_bias", P),
+        ("dw_gate", P), ("db_gate", P), ("dlambda_raw", P),
+    ]
+
+
 DFL_ATTN_BIAS_NONE = 0
 DFL_ATTN_BIAS_BINS = 1
 DFL_ATTN_BIAS_DENSE = 2
@@ -216,6 +243,12 @@ SIGNATURES = [
     ("dfl_balanced_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32, I32]),
     ("dfl_balanced_fwd", I32, [ctypes.POINTER(BalancedFwdParams), P, ctypes.c_size_t, P]),
     ("dfl_balanced_bwd", I32, [ctypes.POINTER(BalancedBwdParams), P, ctypes.c_size_t, P]),
+    ("dfl_sink_proj_workspace_size", ctypes.c_size_t, [I32, I32]),
+    ("dfl_sink_proj_fwd", I32, [ctypes.POINTER(SinkProjParams), P]),
+    ("dfl_sink_proj_bwd", I32, [ctypes.POINTER(SinkProjParams), P, ctypes.c_size_t, P]),
+    ("dfl_coord_update_workspace_size", ctypes.c_size_t, [I32, I32]),
+    ("dfl_coord_update_fwd", I32, [ctypes.POINTER(CoordUpdateParams), P]),
+    ("dfl_coord_update_bwd", I32, [ctypes.POINTER(CoordUpdateParams), P, ctypes.c_size_t, P]),
 ]
 
 

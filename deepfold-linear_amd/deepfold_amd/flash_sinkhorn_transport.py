@@ -32,6 +32,17 @@ def _f32c(t):
     return None if t is None else t.detach().to(torch.float32).contiguous()
 
 
+def _qkv_operands(Q_s, K_s, V_h):
+    """fp32 q, k (and v) sharing one stride set with a unit inner stride, as the C ABI
+    reads them: (B, H, N, d) views of (B, N, H, d) arrays (the projections' layout,
+    trunk_block.py:165-171) pass without a copy; anything else is made contiguous."""
+    ts = [t.detach().to(torch.float32) for t in (Q_s, K_s, V_h) if t is not None]
+    st = ts[0].stride()
+    if st[-1] != 1 or any(t.stride() != st for t in ts):
+        ts = [t.contiguous() for t in ts]
+    return ts[0], ts[1], (ts[2] if V_h is not None else None)
+
+
 def _run_forward(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask):
     dev = _lib.require_gpu(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, mask)
     if Q_s.dim() != 4:
@@ -42,7 +53,7 @@ def _run_forward(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask):
     if V_h is not None and V_h.shape != Q_s.shape:
         raise ValueError("V_h must have the shape of Q_s (B, H, N, d)")
     K_iter = int(K_iter)
-    Qf, Kf, Vf = _f32c(Q_s), _f32c(K_s), _f32c(V_h)
+    Qf, Kf, Vf = _qkv_operands(Q_s, K_s, V_h)
     xf = _f32c(x_res)
     ef, af, rf = _f32c(eps), _f32c(alpha_h), _f32c(r_h)
     mf = None if mask is None else mask.detach().to(torch.float32).contiguous()

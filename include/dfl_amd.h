@@ -482,6 +482,99 @@ size_t dfl_balanced_workspace_size(int B, int H, int N, int d, int backward);
 int dfl_balanced_fwd(const dfl_balanced_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
 int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Sink projections: the step before the balanced transport in TokenOTBlock.forward
+ * (src/deepfold/model/trunk_block.py:165-175):
+ *   h_s = LayerNorm(h) (biased variance, eps 1e-5);  u_p = h_s W_p^T for p = q, k, v;
+ *   q_s, k_s = u / max(|u|, 1e-12) per head of C/H columns (F.normalize); v_s = u_v.
+ * h is (M, C) rows of d_model in `dtype` (the weights share it; bf16 runs the
+ * products on bf16 MFMA with fp32 accumulation, as autocast's bf16 Linear).  The
+ * weights are nn.Linear (out, in) = (C, C) row-major; w_v may be NULL.  Outputs are
+ * fp32 (M, C), i.e. (B, N, H, C/H): the (B, H, N, d) views the reference builds with
+ * .view().permute() are these arrays with strides (N*C, C/H, C), which
+ * dfl_balanced_fwd reads in place.  q_norm, k_norm (M, H) and ln_mean, ln_rstd (M)
+ * are saved for the backward.  C must be a multiple of 64 with C/H in {16, 32, 64}
+ * and at most 512 (fp32) or 1024 (bf16).
+ * The backward takes the forward's inputs and saved values, the upstream gradients
+ * dq_s, dk_s, dv_s (M, C) fp32 (any may be NULL: zero), and writes dh (M, C) fp32,
+ * dln_weight, dln_bias (C) and dw_q, dw_k, dw_v (C, C) fp32 (dw_v NULL when w_v
+ * is; any dw may be NULL).  Workspace: dfl_sink_proj_workspace_size(M, C) bytes,
+ * no initialisation needed.
+ */
+typedef struct dfl_sink_proj_params {
+  int dtype; /* DFL_F32 or DFL_BF16: h and the weights */
+  const void* h;
+  const float* ln_weight;
+  const float* ln_bias;
+  const void* w_q;
+  const void* w_k;
+  const void* w_v;
+  int M, C, H;
+  /* forward outputs; inputs of the backward */
+  float* q_s;
+  float* k_s;
+  float* v_s;
+  float* q_norm;
+  float* k_norm;
+  float* ln_mean;
+  float* ln_rstd;
+  /* backward */
+  const float* dq_s;
+  const float* dk_s;
+  const float* dv_s;
+  float* dh;
+  float* dln_weight;
+  float* dln_bias;
+  float* dw_q;
+  float* dw_k;
+  float* dw_v;
+} dfl_sink_proj_params;
+
+size_t dfl_sink_proj_workspace_size(int M, int C);
+int dfl_sink_proj_fwd(const dfl_sink_proj_params* p, void* stream);
+int dfl_sink_proj_bwd(const dfl_sink_proj_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Gated coordinate update: the step after the balanced transport in
+ * TokenOTBlock.forward (src/deepfold/model/trunk_block.py:189-204):
+ *   gate = sigmoid(w_gate . LayerNorm(h) + b_gate)   (LayerNorm with its own weights)
+ *   x_out = x_res + mask * gate * sum_h tanh(lambda_raw_h) / H * (x_centroid_h - x_res).
+ * h is (B*N, C) in `dtype`; ln_weight, ln_bias, w_gate (C), b_gate (1), lambda_raw
+ * (H), x_centroid (B,H,N,3), x_res (B,N,3) and mask (B,N) (may be NULL) are fp32.
+ * The backward takes dx_out (B,N,3) and writes dx_res (B,N,3), dx_centroid
+ * (B,H,N,3), dh (B*N, C) fp32, dln_weight, dln_bias, dw_gate (C), db_gate (1) and
+ * dlambda_raw (H) (the parameter gradients may be NULL).  C must be a multiple of 64
+ * and at most 1024; H at most 64.  Workspace: dfl_coord_update_workspace_size(C, H).
+ */
+typedef struct dfl_coord_update_params {
+  int dtype; /* of h */
+  const void* h;
+  const float* ln_weight;
+  const float* ln_bias;
+  const float* w_gate;
+  const float* b_gate;
+  const float* lambda_raw;
+  const float* x_centroid;
+  const float* x_res;
+  const float* mask;
+  int B, N, C, H;
+  float* x_out;
+  /* backward */
+  const float* dx_out;
+  float* dx_res;
+  float* dx_centroid;
+  float* dh;
+  float* dln_weight;
+  float* dln_bias;
+  float* dw_gate;
+  float* db_gate;
+  float* dlambda_raw;
+} dfl_coord_update_params;
+
+size_t dfl_coord_update_workspace_size(int C, int H);
+int dfl_coord_update_fwd(const dfl_coord_update_params* p, void* stream);
+int dfl_coord_update_bwd(const dfl_coord_update_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,7 +87,9 @@ def test_struct_layout_matches_c(lib_path):
                "dfl_dense_sinkhorn_bwd_params": _lib.DenseSinkhornBwdParams,
                "dfl_dense_transport_params": _lib.DenseTransportParams,
                "dfl_balanced_fwd_params": _lib.BalancedFwdParams,
-               "dfl_balanced_bwd_params": _lib.BalancedBwdParams}
+               "dfl_balanced_bwd_params": _lib.BalancedBwdParams,
+               "dfl_sink_proj_params": _lib.SinkProjParams,
+               "dfl_coord_update_params": _lib.CoordUpdateParams}
     assert set(mirrors) == set(structs)
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for sname, fields in structs.items():
@@ -116,7 +118,8 @@ def test_ops_refuse_cpu_tensors():
     import torch
     from deepfold_amd import (atom_to_token_attn, balanced_sinkhorn_transport, balanced_sinkhorn_transport_dual,
                               compute_transport_output, conjugate_gradient, flash_atom_attn, flash_diffusion_attn,
-                              flash_sinkhorn, flash_sinkhorn_attn, sinkhorn_solve, token_to_atom_attn)
+                              flash_sinkhorn, flash_sinkhorn_attn, gated_coordinate_update, sink_projections,
+                              sinkhorn_solve, token_to_atom_attn)
 
     B, H, N, d = 1, 2, 8, 4
     q = torch.randn(B, H, N, d)
@@ -139,7 +142,12 @@ def test_ops_refuse_cpu_tensors():
                  lambda: balanced_sinkhorn_transport(q, q, torch.zeros(B, N, 3), torch.ones(H), torch.zeros(H),
                                                      torch.ones(H)),
                  lambda: balanced_sinkhorn_transport_dual(q, q, torch.zeros(B, N, 3), q, torch.ones(H),
-                                                          torch.zeros(H), torch.ones(H))):
+                                                          torch.zeros(H), torch.ones(H)),
+                 lambda: sink_projections(torch.randn(B, N, 64), torch.ones(64), torch.zeros(64),
+                                          torch.randn(64, 64), torch.randn(64, 64), None, 2),
+                 lambda: gated_coordinate_update(torch.randn(B, N, 64), torch.zeros(B, N, 3),
+                                                 torch.zeros(B, H, N, 3), torch.ones(64), torch.zeros(64),
+                                                 torch.zeros(1, 64), torch.zeros(1), torch.zeros(H))):
         with pytest.raises(RuntimeError, match="GPU"):
             call()
 
