@@ -557,6 +557,169 @@ def bench_balanced(args):
     print(json.dumps(out), flush=True)
 
 
+def tokenot_block(C, H, seed, dev):
+    """The parameters TokenOTBlock holds for its transport steps (trunk_block.py:65-96):
+    LayerNorms near identity, Linear weights N(0, 1/C), alpha_h = -1, r_h = 10,
+    lambda_h_raw = 0.5, the trunk's eps buffer."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    blk = torch.nn.Module()
+    blk.n_heads, blk.feature_transport = H, True
+    blk.ln_sink, blk.ln_gate = torch.nn.LayerNorm(C), torch.nn.LayerNorm(C)
+    for n in ("w_q_sink", "w_k_sink", "w_v_sink", "w_o_sink"):
+        setattr(blk, n, torch.nn.Linear(C, C, bias=False))
+    blk.w_gate = torch.nn.Linear(C, 1, bias=True)
+    with torch.no_grad():
+        for ln in (blk.ln_sink, blk.ln_gate):
+            ln.weight.copy_(1 + 0.1 * torch.randn(C, generator=g))
+            ln.bias.copy_(0.1 * torch.randn(C, generator=g))
+        for lin in (blk.w_q_sink, blk.w_k_sink, blk.w_v_sink, blk.w_o_sink, blk.w_gate):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) / C ** 0.5)
+        blk.w_gate.bias.zero_()
+    blk.alpha_h = torch.nn.Parameter(torch.full((H,), -1.0))
+    blk.r_h = torch.nn.Parameter(torch.full((H,), 10.0))
+    blk.lambda_h_raw = torch.nn.Parameter(torch.full((H,), 0.5))
+    nr = H // 4
+    blk.register_buffer("eps", torch.tensor([0.5] * nr + [1.0] * nr + [2.0] * nr + [4.0] * nr))
+    return blk.to(dev)
+
+
+def bench_tokenot_step(args):
+    """TokenOTBlock steps 2-4 (trunk_block.py:165-204), fwd + bwd: sink projections ->
+    balanced dual transport -> w_o_sink -> gated coordinate update (token_ot_transport_step),
+    at the balanced workload's shape (B1 N256, d_model 512, H16, K = 20, fp32)."""
+    import torch
+    import torch.nn.functional as F
+    from deepfold_amd import _lib, gated_coordinate_update, sink_projections, token_ot_transport_step
+
+    dev = torch.device("cuda:0")
+    B, N, C, H, K = 1, 256, 512, 16, 20
+    blk = tokenot_block(C, H, 1007, dev)
+    g = torch.Generator().manual_seed(1007)
+    h0 = torch.randn(B, N, C, generator=g).to(dev)
+    x0 = (torch.randn(B, N, 3, generator=g) * 3).to(dev)
+    gh = torch.randn(B, N, C, generator=g).to(dev)
+    gx = torch.randn(B, N, 3, generator=g).to(dev)
+    xc_fixed = (torch.randn(B, H, N, 3, generator=g) * 3).to(dev)
+    mask = torch.ones(B, N, device=dev)
+
+    def step():
+        h = h0.detach().requires_grad_(True)
+        x = x0.detach().requires_grad_(True)
+        ho, xo = token_ot_transport_step(blk, h, x, mask, K_iter=K)
+        torch.autograd.backward((ho, xo), (gh, gx))
+
+    def steps_hip():  # the two steps alone, around a fixed centroid
+        h = h0.detach().requires_grad_(True)
+        q, k, v = sink_projections(h, blk.ln_sink.weight, blk.ln_sink.bias, blk.w_q_sink.weight,
+                                   blk.w_k_sink.weight, blk.w_v_sink.weight, H)
+        xo = gated_coordinate_update(h, x0, xc_fixed, blk.ln_gate.weight, blk.ln_gate.bias, blk.w_gate.weight,
+                                     blk.w_gate.bias, blk.lambda_h_raw, mask)
+        torch.autograd.backward((q, k, v, xo), (q.detach(), k.detach(), v.detach(), gx))
+
+    def steps_eager():  # the reference's eager form of the same two steps (trunk_block.py:165-175, 189-204)
+        h = h0.detach().requires_grad_(True)
+        hs = blk.ln_sink(h)
+        heads = lambda u: u.view(B, N, H, C // H).permute(0, 2, 1, 3)
+        q = F.normalize(heads(blk.w_q_sink(hs)), dim=-1)
+        k = F.normalize(heads(blk.w_k_sink(hs)), dim=-1)
+        v = heads(blk.w_v_sink(hs))
+        vec = xc_fixed - x0.unsqueeze(1)
+        gate = torch.sigmoid(blk.w_gate(blk.ln_gate(h)))
+        lam = torch.tanh(blk.lambda_h_raw).view(1, H, 1, 1) / H
+        xo = x0 + gate * (lam * vec).sum(dim=1) * mask.unsqueeze(-1)
+        torch.autograd.backward((q, k, v, xo), (q.detach(), k.detach(), v.detach(), gx))
+
+    def timed(fn, n):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    steps_hip_ms = timed(steps_hip, args.steps)
+    steps_eager_ms = timed(steps_eager, args.steps)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.launch_timings = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = {}
+    for name, s_, e_ in _lib.launch_timings:
+        per.setdefault(name, []).append(s_.elapsed_time(e_))
+    _lib.launch_timings = None
+    avg = {k: sum(v) / len(v) for k, v in per.items()}
+    ms = wall * 1e3 / args.steps
+    # projections: 2 M C^2 flops per projection forward (3 of them); backward twice that
+    M = B * N
+    f_proj = 3 * 2 * M * C * C
+    pf = f_proj / (avg["sink_proj_fwd"] * 1e-3)
+    pb = 2 * f_proj / (avg["sink_proj_bwd"] * 1e-3)
+    bcfg = dict(B=B, H=H, N=N, d=C // H, K_iter=K)
+    E, f_fwd, f_bwd, _, _ = balanced_counts(bcfg)
+    dom = max(avg, key=avg.get)
+    f_dom = {"balanced_fwd": f_fwd, "balanced_bwd": f_bwd, "sink_proj_fwd": f_proj,
+             "sink_proj_bwd": 2 * f_proj}.get(dom)
+    achieved = f_dom / (avg[dom] * 1e-3) if f_dom else None
+    out = {
+        "metric": "TokenOTBlock transport steps (projections, balanced transport, coordinate update) fwd+bwd "
+                  "ms/step @B1,N256,C512,H16 fp32 K20",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seed 1007): h ~ N(0,1), x_res ~ N(0,3^2), parameters near init, "
+                                "upstream grads N(0,1)",
+        "config": {"workload": "TokenOTBlock steps 2-4, token_ot_transport_step fwd+bwd", "B": B, "N": N, "C": C,
+                   "H": H, "K_iter": K},
+        "kernel_ms": {k: round(v, 4) for k, v in avg.items()},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": None if achieved is None else round(achieved / 1e12, 3),
+                     "peak": PEAK_MFMA_F32 / 1e12, "unit": "TFLOP/s",
+                     "frac": None if achieved is None else round(achieved / PEAK_MFMA_F32, 5),
+                     "traffic": profiled_traffic(dom, "balanced_tokenot_bench.md")},
+        "roofline_projections": {"fwd_tflops": round(pf / 1e12, 3), "bwd_tflops": round(pb / 1e12, 3),
+                                 "peak": PEAK_MFMA_F32 / 1e12, "unit": "TFLOP/s (fp32 MFMA)"},
+        "steps_only_ms": {"hip": round(steps_hip_ms, 4), "torch_eager": round(steps_eager_ms, 4),
+                          "what": "projections + coordinate update fwd+bwd around a fixed centroid; torch_eager is "
+                                  "the reference's eager formulation on the same GPU"},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = tokenot_cpu_baseline(blk, h0, x0, mask, gh, gx, K)
+    print(json.dumps(out), flush=True)
+
+
+def tokenot_cpu_baseline(blk, h0, x0, mask, gh, gx, K):
+    """oracle/trunk_steps.transport_step (float32 torch autograd on the host threads),
+    one full step, median of 3."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import trunk_steps as ts
+
+    P = {"ln_sink_w": blk.ln_sink.weight, "ln_sink_b": blk.ln_sink.bias, "w_q": blk.w_q_sink.weight,
+         "w_k": blk.w_k_sink.weight, "w_v": blk.w_v_sink.weight, "w_o": blk.w_o_sink.weight, "eps": blk.eps,
+         "alpha_h": blk.alpha_h, "r_h": blk.r_h, "ln_gate_w": blk.ln_gate.weight, "ln_gate_b": blk.ln_gate.bias,
+         "w_gate": blk.w_gate.weight, "b_gate": blk.w_gate.bias, "lambda_raw": blk.lambda_h_raw}
+    R = {k: v.detach().float().cpu().requires_grad_(k != "eps") for k, v in P.items()}
+    times = []
+    for _ in range(3):
+        h = h0.detach().cpu().requires_grad_(True)
+        x = x0.detach().cpu().requires_grad_(True)
+        t0 = time.perf_counter()
+        ho, xo = ts.transport_step(R, h, x, mask.cpu(), blk.n_heads, K_iter=K)
+        torch.autograd.backward((ho, xo), (gh.cpu(), gx.cpu()))
+        times.append((time.perf_counter() - t0) * 1e3)
+    times.sort()
+    return {"value": round(times[1], 2), "unit": "ms/step", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "the oracle's restatement of trunk_block.py:165-204 (with _sinkhorn_cpu) under torch "
+                      "autograd, float32, one full step, median of 3"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -564,7 +727,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="cfg2",
-                    choices=["cfg2", "cfg5", "cfg2-full", "cfg2-unrolled", "cfg3", "cfg4", "balanced"],
+                    choices=["cfg2", "cfg5", "cfg2-full", "cfg2-unrolled", "cfg3", "cfg4", "balanced", "tokenot-step"],
                     help="cfg2 (default): the headline flash-Sinkhorn layer; cfg5: the N=4096 layer; "
                          "cfg3 / cfg4: attention rows")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -600,6 +763,8 @@ def main():
         bench_sinkhorn(args, args.workload)
     elif args.workload == "balanced":
         bench_balanced(args)
+    elif args.workload == "tokenot-step":
+        bench_tokenot_step(args)
     else:
         bench_attention(args, args.workload)
 

@@ -30,15 +30,24 @@ struct ProjArgs {
   int M, C, H;
 };
 
-// C[i][j] = (acc ? C[i][j] : 0) + sum_k A(i, k) B(j, k), fp32 accumulation.
+// Up to three GEMMs per launch (blockIdx.z), each C[i][j] = sum_k A(i, k) B(j, k) in
+// fp32 with the k range split into nseg segments of kseg, segment s reading A[z + s]
+// and B[z + s] (one launch sums the three projections' products):
 // A(i, k) = A[k * lda + i] when A is K-major, else A[i * lda + k]; B likewise.
 struct GemmArgs {
-  const float* A;
-  const void* B;  // fp32 or bf16 (see the launcher)
-  float* C;
+  const float* A[3];
+  const void* B[3];  // fp32 or bf16 (see the launcher)
+  float* C[3];
   long long lda, ldb, ldc;
-  int m, n, K;
-  int acc;
+  int m, n, kseg, nseg;
+};
+
+// Sums of per-workgroup partial rows: out_s[c] = sum_r part[r][off_s + c], c < n_s.
+struct SumSegs {
+  const float* part;
+  int rows, width, nseg;
+  int off[5], n[5];
+  float* out[5];
 };
 
 // x <- x + mask * sigmoid(w_gate . LN(h) + b_gate) * sum_h tanh(lambda_h) / H * (x_c,h - x)

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstring>
 
 #include "common.h"
 #include "trunk_args.h"
@@ -165,65 +166,76 @@ __global__ void __launch_bounds__(TS_NT) proj_ln_recompute_kernel(ProjArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// fp32 GEMM on MFMA (16x16x4 f32): 64 x 64 output tile per workgroup, k-steps of 32
-// staged in LDS in the row-over-k layout of Mfma<float, 32>, transposing K-major
-// operands on the way in.  Wave w computes rows 32(w/2).. and columns 32(w%2).. (2 x 2 tiles).
+// fp32 GEMM on MFMA (16x16x4 f32) for the backward's small products (M ~ 10^2-10^3
+// tokens, C ~ 512): 32 x 32 output tiles (one 16 x 16 tile per wave), so that even
+// M = 256 gives 128+ workgroups; k-steps of 64 staged in LDS in the row-over-k layout
+// of Mfma<float, 64> (K-major operands transposed on the way in), with the next step's
+// global loads issued before the current step's MFMAs.
+constexpr int GB = 32;  // output tile edge
+constexpr int GK = 64;  // k-step
+constexpr int GQ = GB * GK / TS_NT;  // elements of one operand tile per thread (8)
+
 template <bool KMAJ, typename TS>
-__device__ __forceinline__ void gemm_stage(float (*S)[36], const TS* __restrict__ src, long long ld, int r0, int k0,
-                                           int nr, int nk) {
-  for (int e = threadIdx.x; e < 64 * 32; e += TS_NT) {
+__device__ __forceinline__ void gemm_fetch(float (&v)[GQ], const TS* __restrict__ src, long long ld, int r0, int k0,
+                                           int nr, int kend) {
+#pragma unroll
+  for (int q = 0; q < GQ; ++q) {
     // consecutive threads walk the contiguous dimension of the source
-    const int r = KMAJ ? (e & 63) : (e >> 5);
-    const int k = KMAJ ? (e >> 6) : (e & 31);
+    const int e = threadIdx.x + q * TS_NT;
+    const int r = KMAJ ? (e % GB) : (e / GK);
+    const int k = KMAJ ? (e / GB) : (e % GK);
     const int gr = r0 + r, gk = k0 + k;
-    float v = 0.f;
-    if (gr < nr && gk < nk) v = to_f32(KMAJ ? src[(size_t)gk * ld + gr] : src[(size_t)gr * ld + gk]);
-    S[r][k] = v;
+    v[q] = (gr < nr && gk < kend) ? to_f32(KMAJ ? src[(size_t)gk * ld + gr] : src[(size_t)gr * ld + gk]) : 0.f;
+  }
+}
+template <bool KMAJ>
+__device__ __forceinline__ void gemm_put(float (*S)[GK + 4], const float (&v)[GQ]) {
+#pragma unroll
+  for (int q = 0; q < GQ; ++q) {
+    const int e = threadIdx.x + q * TS_NT;
+    const int r = KMAJ ? (e % GB) : (e / GK);
+    const int k = KMAJ ? (e / GB) : (e % GK);
+    S[r][k] = v[q];
   }
 }
 
 template <bool AK, bool BK, typename TB>
 __global__ void __launch_bounds__(TS_NT) gemm_kernel(GemmArgs a) {
-  using MF = Mfma<float, 32>;
-  __shared__ __align__(16) float As[64][36];
-  __shared__ __align__(16) float Bs[64][36];
-  const int i0 = blockIdx.x * 64, j0 = blockIdx.y * 64;
+  using MF = Mfma<float, GK>;
+  __shared__ __align__(16) float As[GB][GK + 4];
+  __shared__ __align__(16) float Bs[GB][GK + 4];
+  const int z = blockIdx.z;
+  const int i0 = blockIdx.x * GB, j0 = blockIdx.y * GB;
   const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, g = lane >> 4;
-  const int wi = 32 * (wave >> 1), wj = 32 * (wave & 1);
-  const TB* B = static_cast<const TB*>(a.B);
-  f32x4 acc[2][2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int v = 0; v < 2; ++v) acc[u][v] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < a.K; k0 += 32) {
-    gemm_stage<AK>(As, a.A, a.lda, i0, k0, a.m, a.K);
-    gemm_stage<BK>(Bs, B, a.ldb, j0, k0, a.n, a.K);
+  const int ti = 16 * (wave >> 1), tj = 16 * (wave & 1);
+  const int sps = (a.kseg + GK - 1) / GK, steps = a.nseg * sps;
+  float va[GQ], vb[GQ];
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < steps; ++t) {
+    if (t == 0) {
+      gemm_fetch<AK>(va, a.A[z], a.lda, i0, 0, a.m, a.kseg);
+      gemm_fetch<BK>(vb, static_cast<const TB*>(a.B[z]), a.ldb, j0, 0, a.n, a.kseg);
+    }
+    gemm_put<AK>(As, va);
+    gemm_put<BK>(Bs, vb);
     __syncthreads();
-    MF::Frag af[2], bf[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) MF::load(af[u], &As[wi + 16 * u + (lane & 15)][0], lane);
-#pragma unroll
-    for (int v = 0; v < 2; ++v) MF::load(bf[v], &Bs[wj + 16 * v + (lane & 15)][0], lane);
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int v = 0; v < 2; ++v) acc[u][v] = MF::qk(bf[v], af[u], acc[u][v]);  // lane: row l%16, cols 4g+e
+    if (t + 1 < steps) {  // next step's loads in flight during this step's MFMAs
+      const int s = (t + 1) / sps, kl = (t + 1 - s * sps) * GK;
+      gemm_fetch<AK>(va, a.A[z + s], a.lda, i0, kl, a.m, a.kseg);
+      gemm_fetch<BK>(vb, static_cast<const TB*>(a.B[z + s]), a.ldb, j0, kl, a.n, a.kseg);
+    }
+    MF::Frag af, bf;
+    MF::load(af, &As[ti + (lane & 15)][0], lane);
+    MF::load(bf, &Bs[tj + (lane & 15)][0], lane);
+    acc = MF::qk(bf, af, acc);  // lane: row ti + l%16, columns tj + 4g + e
     __syncthreads();
   }
+  const int i = i0 + ti + (lane & 15);
+  if (i >= a.m) return;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int i = i0 + wi + 16 * u + (lane & 15);
-    if (i >= a.m) continue;
-#pragma unroll
-    for (int v = 0; v < 2; ++v)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int j = j0 + wj + 16 * v + 4 * g + e;
-        if (j >= a.n) continue;
-        float* c = a.C + (size_t)i * a.ldc + j;
-        *c = a.acc ? *c + acc[u][v][e] : acc[u][v][e];
-      }
+  for (int e = 0; e < 4; ++e) {
+    const int j = j0 + tj + 4 * g + e;
+    if (j < a.n) a.C[z][(size_t)i * a.ldc + j] = acc[e];
   }
 }
 
@@ -274,14 +286,21 @@ __global__ void __launch_bounds__(TS_NT) proj_ln_bwd_kernel(ProjArgs a) {
   }
 }
 
-// out[c] = sum over rows of part[row][off + c] (rows in a fixed order)
-__global__ void __launch_bounds__(TS_NT) sum_parts_kernel(const float* __restrict__ part, int rows, int width,
-                                                          int off, int n, float* __restrict__ out) {
-  const int c = blockIdx.x * TS_NT + threadIdx.x;
-  if (c >= n) return;
+// Column sums of the partial rows (rows split over the 4 waves, combined in a fixed
+// order), scattered to the segments' outputs.  One thread column per lane.
+__global__ void __launch_bounds__(TS_NT) sum_segs_kernel(SumSegs a) {
+  __shared__ float red[4][WAVE];
+  const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+  const int c = blockIdx.x * WAVE + lane;
   float s = 0.f;
-  for (int r = 0; r < rows; ++r) s += part[(size_t)r * width + off + c];
-  out[c] = s;
+  if (c < a.width)
+    for (int r = wave; r < a.rows; r += 4) s += a.part[(size_t)r * a.width + c];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave != 0 || c >= a.width) return;
+  const float tot = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  for (int sg = 0; sg < a.nseg; ++sg)
+    if (c >= a.off[sg] && c < a.off[sg] + a.n[sg] && a.out[sg]) a.out[sg][c - a.off[sg]] = tot;
 }
 
 // ---------------------------------------------------------------------------
@@ -402,10 +421,8 @@ __global__ void __launch_bounds__(TS_NT) coord_kernel(CoordArgs a) {
 
 // ---------------------------------------------------------------------------
 // Launchers.
-static hipError_t sum_parts(const float* part, int rows, int width, int off, int n, float* out, hipStream_t s) {
-  if (!out) return hipSuccess;
-  hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((n + TS_NT - 1) / TS_NT)), dim3(TS_NT), 0, s, part, rows, width,
-                     off, n, out);
+static hipError_t sum_segs(const SumSegs& g, hipStream_t s) {
+  hipLaunchKernelGGL(sum_segs_kernel, dim3((unsigned)((g.width + WAVE - 1) / WAVE)), dim3(TS_NT), 0, s, g);
   return hipGetLastError();
 }
 
@@ -427,11 +444,9 @@ hipError_t launch_proj_fwd(const ProjArgs& a, bool bf16_in, hipStream_t s) {
 }
 
 template <bool AK, bool BK, typename TB>
-static hipError_t gemm(const float* A, const void* B, float* C, long long lda, long long ldb, long long ldc, int m,
-                       int n, int K, bool acc, hipStream_t s) {
-  GemmArgs g{A, B, C, lda, ldb, ldc, m, n, K, acc ? 1 : 0};
-  hipLaunchKernelGGL((gemm_kernel<AK, BK, TB>), dim3((unsigned)((m + 63) / 64), (unsigned)((n + 63) / 64)), dim3(TS_NT),
-                     0, s, g);
+static hipError_t gemm(const GemmArgs& g, int batch, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_kernel<AK, BK, TB>), dim3((unsigned)((g.m + GB - 1) / GB), (unsigned)((g.n + GB - 1) / GB),
+                     (unsigned)batch), dim3(TS_NT), 0, s, g);
   return hipGetLastError();
 }
 
@@ -443,19 +458,41 @@ hipError_t launch_proj_bwd(const ProjArgs& a, bool bf16_in, hipStream_t s) {
   if (bf16_in) hipLaunchKernelGGL(proj_ln_recompute_kernel<bf16>, dim3(blocks), dim3(TS_NT), 0, s, a);
   else hipLaunchKernelGGL(proj_ln_recompute_kernel<float>, dim3(blocks), dim3(TS_NT), 0, s, a);
   hipError_t e = hipGetLastError();
-  for (int p = 0; p < np && e == hipSuccess; ++p) {
-    // dxa (M x C) += du_p (M x C, row layout over o) . W_p (o-major: K-major operand)
-    e = bf16_in ? gemm<false, true, bf16>(a.du[p], a.w[p], a.dxa, a.C, a.C, a.C, a.M, a.C, a.C, p > 0, s)
-                : gemm<false, true, float>(a.du[p], a.w[p], a.dxa, a.C, a.C, a.C, a.M, a.C, a.C, p > 0, s);
-    // dW_p (C x C) = du_p^T . xa: both operands token-major
-    if (e == hipSuccess && a.dw[p])
-      e = gemm<true, true, float>(a.du[p], a.xa, a.dw[p], a.C, a.C, a.C, a.C, a.C, a.M, false, s);
-  }
   if (e != hipSuccess) return e;
+  // dxa (M x C) = sum_p du_p (M x C, row layout over o) . W_p (o-major: a K-major operand)
+  GemmArgs gx;
+  memset(&gx, 0, sizeof(gx));
+  for (int p = 0; p < np; ++p) {
+    gx.A[p] = a.du[p];
+    gx.B[p] = a.w[p];
+  }
+  gx.C[0] = a.dxa;
+  gx.lda = gx.ldb = gx.ldc = a.C;
+  gx.m = a.M; gx.n = a.C; gx.kseg = a.C; gx.nseg = np;
+  e = bf16_in ? gemm<false, true, bf16>(gx, 1, s) : gemm<false, true, float>(gx, 1, s);
+  if (e != hipSuccess) return e;
+  // dW_p (C x C) = du_p^T . xa (both operands token-major), one launch for the requested ones
+  GemmArgs gw;
+  memset(&gw, 0, sizeof(gw));
+  int nw = 0;
+  for (int p = 0; p < np; ++p)
+    if (a.dw[p]) {
+      gw.A[nw] = a.du[p];
+      gw.B[nw] = a.xa;
+      gw.C[nw] = a.dw[p];
+      ++nw;
+    }
+  gw.lda = gw.ldb = gw.ldc = a.C;
+  gw.m = a.C; gw.n = a.C; gw.kseg = a.M; gw.nseg = 1;
+  if (nw > 0 && (e = gemm<true, true, float>(gw, nw, s)) != hipSuccess) return e;
   hipLaunchKernelGGL(proj_ln_bwd_kernel, dim3(TS_PARTS), dim3(TS_NT), 0, s, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  if ((e = sum_parts(a.part, TS_PARTS, 2 * a.C, 0, a.C, a.dln_w, s)) != hipSuccess) return e;
-  return sum_parts(a.part, TS_PARTS, 2 * a.C, a.C, a.C, a.dln_b, s);
+  SumSegs sg;
+  memset(&sg, 0, sizeof(sg));
+  sg.part = a.part; sg.rows = TS_PARTS; sg.width = 2 * a.C; sg.nseg = 2;
+  sg.off[0] = 0; sg.n[0] = a.C; sg.out[0] = a.dln_w;
+  sg.off[1] = a.C; sg.n[1] = a.C; sg.out[1] = a.dln_b;
+  return sum_segs(sg, s);
 }
 
 hipError_t launch_coord(const CoordArgs& a, bool bf16_in, bool bwd, hipStream_t s) {
@@ -470,12 +507,18 @@ hipError_t launch_coord(const CoordArgs& a, bool bf16_in, bool bwd, hipStream_t 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !bwd) return e;
-  const int C = a.C, H = a.H, width = 3 * C + H + 1;
-  if ((e = sum_parts(a.part, TS_PARTS, width, 0, C, a.dw_gate, s)) != hipSuccess) return e;
-  if ((e = sum_parts(a.part, TS_PARTS, width, C, C, a.dln_w, s)) != hipSuccess) return e;
-  if ((e = sum_parts(a.part, TS_PARTS, width, 2 * C, C, a.dln_b, s)) != hipSuccess) return e;
-  if ((e = sum_parts(a.part, TS_PARTS, width, 3 * C, H, a.dlam_raw, s)) != hipSuccess) return e;
-  return sum_parts(a.part, TS_PARTS, width, 3 * C + H, 1, a.db_gate, s);
+  const int C = a.C, H = a.H;
+  SumSegs sg;
+  memset(&sg, 0, sizeof(sg));
+  sg.part = a.part; sg.rows = TS_PARTS; sg.width = 3 * C + H + 1; sg.nseg = 5;
+  const int off[5] = {0, C, 2 * C, 3 * C, 3 * C + H}, n[5] = {C, C, C, H, 1};
+  float* out[5] = {a.dw_gate, a.dln_w, a.dln_b, a.dlam_raw, a.db_gate};
+  for (int i = 0; i < 5; ++i) {
+    sg.off[i] = off[i];
+    sg.n[i] = n[i];
+    sg.out[i] = out[i];
+  }
+  return sum_segs(sg, s);
 }
 
 }  // namespace dfl
