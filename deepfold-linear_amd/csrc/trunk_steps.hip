@@ -89,6 +89,7 @@ __global__ void __launch_bounds__(TS_NT) proj_fwd_kernel(ProjArgs a) {
   f32x4 acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4  // C % 128 == 0 is not required: the remainder loop handles C = 64 (mod 128)
   for (int kc = 0; kc < C; kc += 32) {
     typename M::Frag wf;
     M::load(wf, wrow + kc, lane);
