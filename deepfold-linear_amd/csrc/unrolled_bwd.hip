@@ -113,7 +113,9 @@ __global__ void __launch_bounds__(256) unrolled_finalize_kernel(UnrBwdArgs a, fl
   }
 }
 
-template <int DP>
+// GEN: the cost may carry position bins or geometry (set by the host when either is
+// passed); GEN = false compiles none of their per-element code.
+template <int DP, bool GEN>
 __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   using M = Mfma<float, DP>;
   constexpr int NC = DP / 16;
@@ -197,8 +199,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const float sc = LOG2E / (sqrtf((float)d) * eps);
   const float bsc = -LOG2E / eps;  // bias (pw + w d/(r0 + d)) -> log2 logit
   const float wd = a.w_dist ? a.w_dist[h] : 0.f;
-  const bool geo = a.has_geo != 0 && wd != 0.f;
-  const bool use_bins = a.bins8 != nullptr;
+  const bool geo = GEN && a.has_geo != 0 && wd != 0.f;
+  const bool use_bins = GEN && a.bins8 != nullptr;
   const uint8_t* bins_b = use_bins ? a.bins8 + (size_t)b * Np * Np : nullptr;
   const float r0 = a.r0;
   const int r_lo = t0 * 16;
@@ -284,12 +286,14 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
 
   // One sweep.  ROW: resident rows i (streamed j), else resident columns j
   // (streamed i).  CENT: the centroid sweep of that orientation.  Index k as in
-  // the header comment (CS_cent uses k = K).
-  auto sweep = [&](auto row_tag, auto cent_tag, int k) -> bool {
+  // the header comment (CS_cent uses k = K).  USE_C (the recurrence term: all but
+  // RS(-1) and CS_cent) and TERM2 (the mirror term: all but RS(K-1) and CS_cent) are
+  // compile-time, so the element loop carries no test of them.
+  auto sweep = [&](auto row_tag, auto cent_tag, auto usec_tag, auto term2_tag, int k) -> bool {
     constexpr bool ROW = decltype(row_tag)::value;
     constexpr bool CENT = decltype(cent_tag)::value;
-    const bool use_c = ROW ? k >= 0 : !CENT;     // term 1 (recurrence term)
-    const bool term2 = ROW ? k <= K - 2 : !CENT;  // term 2 (mirror term)
+    constexpr bool use_c = decltype(usec_tag)::value;
+    constexpr bool term2 = decltype(term2_tag)::value;
     const bool publish = ROW ? k >= 0 : (CENT || k >= 1);
     __syncthreads();  // readers of STA / STB and of the gathered vectors are done
     for (int i = tid; i < Np; i += UNR_NT) {
@@ -486,14 +490,14 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
 
   using TRUE_ = std::integral_constant<bool, true>;
   using FALSE_ = std::integral_constant<bool, false>;
-  if (!sweep(FALSE_{}, TRUE_{}, K)) return;
-  if (!sweep(TRUE_{}, TRUE_{}, K - 1)) return;
-  if (!sweep(FALSE_{}, FALSE_{}, K - 1)) return;
-  for (int k = K - 2; k >= 0; --k) {
-    if (!sweep(TRUE_{}, FALSE_{}, k)) return;
-    if (!sweep(FALSE_{}, FALSE_{}, k)) return;
+  // (row, cent, use_c, term2)
+  if (!sweep(FALSE_{}, TRUE_{}, FALSE_{}, FALSE_{}, K)) return;
+  if (!sweep(TRUE_{}, TRUE_{}, TRUE_{}, FALSE_{}, K - 1)) return;
+  for (int k = K - 1; k >= 0; --k) {
+    if (k < K - 1 && !sweep(TRUE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k)) return;
+    if (!sweep(FALSE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k)) return;
   }
-  if (!sweep(TRUE_{}, FALSE_{}, -1)) return;
+  if (!sweep(TRUE_{}, FALSE_{}, FALSE_{}, TRUE_{}, -1)) return;
 
   // ---- outputs of my stripe
   const float fs = -1.f / (sqrtf((float)d) * eps);
@@ -573,9 +577,9 @@ hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipS
   return hipErrorInvalidValue;
 }
 
-template <int DP>
+template <int DP, bool GEN>
 static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  auto kern = unrolled_bwd_kernel<DP>;
+  auto kern = unrolled_bwd_kernel<DP, GEN>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(UNR_NT);
@@ -589,8 +593,9 @@ static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stre
 }
 
 hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop) {
-  if (DP == 32) return launch_unr_t<32>(a, lds, stream, coop);
-  if (DP == 64) return launch_unr_t<64>(a, lds, stream, coop);
+  const bool gen = (a.bins8 && a.pos_w) || (a.has_geo && a.w_dist);
+  if (DP == 32) return gen ? launch_unr_t<32, true>(a, lds, stream, coop) : launch_unr_t<32, false>(a, lds, stream, coop);
+  if (DP == 64) return gen ? launch_unr_t<64, true>(a, lds, stream, coop) : launch_unr_t<64, false>(a, lds, stream, coop);
   return hipErrorInvalidValue;
 }
 
