@@ -534,8 +534,10 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
     e = dfl::launch_sinkhorn_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop);
   }
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward launch");
-  e = dfl::launch_sinkhorn_bwd_finalize(a, p->dx_res, p->dpos_weight, p->dw_dist, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "sinkhorn backward finalize launch");
+  if (p->dx_res || p->dpos_weight || p->dw_dist) {  // the partial sums feed only these
+    e = dfl::launch_sinkhorn_bwd_finalize(a, p->dx_res, p->dpos_weight, p->dw_dist, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "sinkhorn backward finalize launch");
+  }
   return 0;
 }
 

@@ -88,10 +88,10 @@ struct SinkBwdArgs {
   float cg_rtol;  // CG early stop on ||r|| <= rtol ||b|| (0 = run all iterations)
   int geo_grad;   // compute d x_res / d w_dist cost terms (x given and requested)
   // outputs (every position written; zeros where padded)
-  float* dq;        // (B,H,N,d)
-  float* dk;
-  float* dv;
-  float* dg;
+  void* dq;         // (B,H,N,d) in the input type T
+  void* dk;
+  void* dv;
+  void* dg;
   float* dlog_mu;   // (B,H,N)
   float* dlog_nu;
   float* dx_part;   // (B,H,N,3) per-head partials, summed over h by the finaliser

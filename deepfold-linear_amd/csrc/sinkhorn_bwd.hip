@@ -26,10 +26,10 @@ __global__ void __launch_bounds__(256) sinkhorn_bwd_prep_kernel(SinkBwdArgs a) {
     if (a.g) {
       const T* Gg = reinterpret_cast<const T*>(a.g) + (size_t)b * a.sb + (size_t)h * a.sh;
       s = sigm(to_f32(Gg[(size_t)i * a.sn + c]));
-      a.dg[((size_t)bh * N + i) * d + c] = s * (1.f - s) * oa * go;
+      put_grad<T>(a.dg, ((size_t)bh * N + i) * d + c, s * (1.f - s) * oa * go);
     }
   } else if (a.g && i < N && c < d) {
-    a.dg[((size_t)bh * N + i) * d + c] = 0.f;
+    put_grad<T>(a.dg, ((size_t)bh * N + i) * d + c, 0.f);
   }
   const float g = s * go;
   const T hi = from_f32<T>(g);

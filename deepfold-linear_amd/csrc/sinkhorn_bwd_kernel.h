@@ -406,6 +406,12 @@ __device__ __forceinline__ void stage_jobs(const StageJob (&J)[NJ], int r0, int 
   }
 }
 
+// Gradients of q, k, v, g are stored in the input type (one rounding of the fp32 sums).
+template <typename T>
+__device__ __forceinline__ void put_grad(void* p, size_t i, float v) {
+  static_cast<T*>(p)[i] = from_f32<T>(v);
+}
+
 struct BwdShared {
   int flag, tmp;
   float posw[BIN_NONE + 1];
@@ -481,9 +487,9 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   // where the stripe's outputs are written.
   for (int i = n_tiles * 16 + member; i < N; i += a.G) {
     for (int c = threadIdx.x; c < d; c += BWD_NT) {
-      a.dq[(bh * N + i) * d + c] = 0.f;
-      a.dk[(bh * N + i) * d + c] = 0.f;
-      a.dv[(bh * N + i) * d + c] = 0.f;
+      put_grad<T>(a.dq, (bh * N + i) * d + c, 0.f);
+      put_grad<T>(a.dk, (bh * N + i) * d + c, 0.f);
+      put_grad<T>(a.dv, (bh * N + i) * d + c, 0.f);
     }
     if (threadIdx.x == 0) {
       a.dlog_mu[bh * N + i] = 0.f;
@@ -703,7 +709,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 const int col = c * 16 + (lane & 15);
-                if (col < d) a.dv[(bh * N + j) * d + col] = jv ? dvacc[k][c][r] : 0.f;
+                if (col < d) put_grad<T>(a.dv, (bh * N + j) * d + col, jv ? dvacc[k][c][r] : 0.f);
               }
             }
           }
@@ -1020,7 +1026,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 const int col = c * 16 + (lane & 15);
-                if (col < d) a.dq[(bh * N + i) * d + col] = iv ? -inv_sqrt_d * dqacc[k][c][r] : 0.f;
+                if (col < d) put_grad<T>(a.dq, (bh * N + i) * d + col, iv ? -inv_sqrt_d * dqacc[k][c][r] : 0.f);
               }
             }
           }
@@ -1180,7 +1186,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 const int col = c * 16 + (lane & 15);
-                if (col < d) a.dk[(bh * N + j) * d + col] = jv ? -inv_sqrt_d * dkacc[k][c][r] : 0.f;
+                if (col < d) put_grad<T>(a.dk, (bh * N + j) * d + col, jv ? -inv_sqrt_d * dkacc[k][c][r] : 0.f);
               }
             }
           }

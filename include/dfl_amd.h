@@ -114,8 +114,9 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
  * term of dC and d log_mu change sign).  Padded tokens (mask == 0) are excluded,
  * which equals evaluating each sample on its unpadded slice.
  * Inputs are the forward's inputs and saved outputs plus grad_o (B,N,H*d) fp32 and
- * grad_xc (B,H,N,3) fp32 (may be NULL).  Outputs (fp32, fully written):
- * dq, dk, dv, dg (B,H,N,d), dlog_mu, dlog_nu (B,H,N); optional (NULL = not requested,
+ * grad_xc (B,H,N,3) fp32 (may be NULL).  Outputs (fully written): dq, dk, dv, dg
+ * (B,H,N,d) in `dtype` (bf16 inputs get bf16 gradients, accumulated in fp32 and
+ * rounded once), dlog_mu, dlog_nu (B,H,N) fp32; optional fp32 (NULL = not requested,
  * which also skips their per-element work): dx_res (B,N,3), dpos_weight (H,68), dw_dist (H,).
  * storage: as for the forward (the two calls choose independently).
  */
@@ -150,10 +151,10 @@ typedef struct dfl_sinkhorn_bwd_params {
   int iters;
   int mode;
   float cg_rtol;
-  float* dq;
-  float* dk;
-  float* dv;
-  float* dg;
+  void* dq; /* in `dtype` */
+  void* dk;
+  void* dv;
+  void* dg;
   float* dlog_mu;
   float* dlog_nu;
   float* dx_res;
