@@ -236,8 +236,7 @@ static hipError_t attn_fwd_f(const AttnArgs& a, hipStream_t s) {
   using E = Eng<T, DP, WIN>;
   constexpr int lds = attn_fwd_lds<T, DP, WIN>();
   auto kern = attn_fwd2_kernel<T, DP, BIAS, WIN, FAST>;
-  static const hipError_t attr =
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  const hipError_t attr = set_lds_limit((const void*)kern, lds);
   if (attr != hipSuccess) return attr;
   const int nqb = (a.Mq + E::RQ - 1) / E::RQ;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nqb * a.B * a.H)), dim3(E::NT), lds, s, a);
@@ -273,10 +272,8 @@ static hipError_t attn_bwd_f(const AttnArgs& a, hipStream_t s) {
   constexpr int lkv = attn_bwdkv_lds<T, DP>(), lq = attn_bwdq_lds<T, DP, WIN>();
   auto kkv = attn_bwd_kv2_kernel<T, DP, BIAS, WIN, FAST>;
   auto kq = attn_bwd_q2_kernel<T, DP, BIAS, WIN, FAST>;
-  static const hipError_t attr =
-      hipFuncSetAttribute((const void*)kkv, hipFuncAttributeMaxDynamicSharedMemorySize, lkv) != hipSuccess
-          ? hipErrorInvalidValue
-          : hipFuncSetAttribute((const void*)kq, hipFuncAttributeMaxDynamicSharedMemorySize, lq);
+  const hipError_t attr = set_lds_limit((const void*)kkv, lkv) != hipSuccess ? hipErrorInvalidValue
+                                                                             : set_lds_limit((const void*)kq, lq);
   if (attr != hipSuccess) return attr;
   const int BH = a.B * a.H;
   const size_t rows = (size_t)BH * a.Mq;

@@ -514,7 +514,7 @@ hipError_t launch_balanced_prep(const BalPrepArgs& p, int DP, hipStream_t stream
 template <int DP>
 static hipError_t launch_bal_t(const BalBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
   auto kern = balanced_bwd_kernel<DP>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(BAL_NT);
   BalBwdArgs copy = a;

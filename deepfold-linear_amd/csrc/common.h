@@ -12,7 +12,28 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 namespace dfl {
+
+// Raises a kernel's dynamic-LDS limit once per (kernel, device) and size: the
+// attribute call costs host time that would otherwise sit in front of every launch.
+inline hipError_t set_lds_limit(const void* kern, size_t lds) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> done;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(kern, dev);
+  const auto it = done.find(key);
+  if (it != done.end() && it->second >= lds) return hipSuccess;
+  e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e == hipSuccess) done[key] = lds;
+  return e;
+}
 
 typedef __bf16 bf16;
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;

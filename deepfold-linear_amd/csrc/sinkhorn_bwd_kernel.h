@@ -1235,7 +1235,7 @@ inline size_t sinkhorn_bwd_lds_bytes_t(int N, int DP, int elem, int G, int CH, b
 template <typename T, int DP, bool STREAM, bool GEN>
 static hipError_t launch_bwd_t(const SinkBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
   auto kern = sinkhorn_bwd_kernel<T, DP, STREAM, GEN>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(BWD_NT);
   SinkBwdArgs copy = a;

@@ -558,7 +558,7 @@ inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stre
 template <typename T, int DP, bool STREAM, int MODE, bool GEN>
 static hipError_t launch_fwd_t(const SinkFwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
   auto kern = sinkhorn_fwd_kernel<T, DP, STREAM, MODE, GEN>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(FWD_NT);
   SinkFwdArgs copy = a;

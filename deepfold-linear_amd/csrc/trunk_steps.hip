@@ -431,13 +431,11 @@ hipError_t launch_proj_fwd(const ProjArgs& a, bool bf16_in, hipStream_t s) {
   const size_t lds = proj_fwd_lds_bytes(a.C, bf16_in);
   const dim3 grid((unsigned)((a.M + 63) / 64), (unsigned)(a.C / 64), a.w[2] ? 3u : 2u);
   if (bf16_in) {
-    hipError_t e = hipFuncSetAttribute((const void*)proj_fwd_kernel<bf16>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
+    hipError_t e = set_lds_limit((const void*)proj_fwd_kernel<bf16>, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(proj_fwd_kernel<bf16>, grid, dim3(TS_NT), lds, s, a);
   } else {
-    hipError_t e = hipFuncSetAttribute((const void*)proj_fwd_kernel<float>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
+    hipError_t e = set_lds_limit((const void*)proj_fwd_kernel<float>, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(proj_fwd_kernel<float>, grid, dim3(TS_NT), lds, s, a);
   }

@@ -580,7 +580,7 @@ hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipS
 template <int DP, bool GEN>
 static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
   auto kern = unrolled_bwd_kernel<DP, GEN>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(UNR_NT);
   UnrBwdArgs copy = a;
