@@ -53,7 +53,7 @@ hipError_t launch_balanced_finalize(const BalBwdArgs& a, float* dx, float* dalph
 size_t unrolled_bwd_lds_bytes(int N);
 int unrolled_max_tiles(int DP);
 hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipStream_t stream);
-hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop);
+hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop);
 hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream);
 }  // namespace dfl
 
@@ -893,7 +893,7 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
   a.salt = next_salt();
-  e = dfl::launch_unrolled_bwd(a, DP, lds, (hipStream_t)stream, G > 1);
+  e = dfl::launch_unrolled_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, G > 1);
   if (e != hipSuccess) return hip_fail(e, "unrolled backward launch");
   e = dfl::launch_unrolled_finalize(a, p->x_res ? p->dx_res : nullptr, p->dpos_weight, p->dw_dist,
                                     (hipStream_t)stream);

@@ -166,9 +166,9 @@ struct UnrBwdArgs {
   const float* pos_w;    // (H,68) or null
   const float* w_dist;   // (H,) or null
   int has_geo;           // geometry term present (x given and w_dist given)
-  const float* qp;       // [B*H][Np][DP] fp32 copies, zero on masked rows / padding
-  const float* kp;
-  const float* qt;       // [B*H][DP][Np]
+  const void* qp;        // [B*H][Np][DP] copies in the input type, zero on masked rows / padding
+  const void* kp;
+  const float* qt;       // [B*H][DP][Np] fp32
   const float* kt;
   const float* vp;       // V rows
   const float* gp;       // gO rows (gO = sigma(G) dO)
@@ -204,7 +204,8 @@ struct UnrPrepArgs {
   const float* grad_o;   // (B,N,H*d) fp32
   const float* grad_xc;  // (B,H,N,3) or null
   int B, H, N, d;
-  float* qp; float* kp; float* qt; float* kt; float* vp; float* gp; float* gt;
+  void* qp; void* kp;    // in the input type (the cost recompute's MFMA operands)
+  float* qt; float* kt; float* vp; float* gp; float* gt;
   float* dcoef; float* gxs; float* xs;
   float* dg;             // (B,H,N,d) or null (no gate)
 };

@@ -69,8 +69,8 @@ __global__ void __launch_bounds__(256) unrolled_prep_kernel(UnrPrepArgs p) {
   } else if (p.g && i < N && c < d) {
     p.dg[((size_t)bh * N + i) * d + c] = 0.f;
   }
-  p.qp[row * DP + c] = qv;
-  p.kp[row * DP + c] = kv;
+  static_cast<T*>(p.qp)[row * DP + c] = from_f32<T>(qv);  // exact: qv, kv come from T
+  static_cast<T*>(p.kp)[row * DP + c] = from_f32<T>(kv);
   p.vp[row * DP + c] = vv;
   p.gp[row * DP + c] = go;
   p.qt[((size_t)bh * DP + c) * Np + i] = qv;
@@ -115,9 +115,13 @@ __global__ void __launch_bounds__(256) unrolled_finalize_kernel(UnrBwdArgs a, fl
 
 // GEN: the cost may carry position bins or geometry (set by the host when either is
 // passed); GEN = false compiles none of their per-element code.
-template <int DP, bool GEN>
+// T: the input type.  The cost recompute q.k runs on Mfma<T, DP> (bf16 inputs: the
+// bf16 MFMA, exact products with fp32 accumulation, as the forward); the centroid and
+// gradient products, whose operands are not bf16-exact, run on the fp32 MFMA.
+template <typename T, int DP, bool GEN>
 __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   using M = Mfma<float, DP>;
+  using MQ = Mfma<T, DP>;
   constexpr int NC = DP / 16;
   constexpr int NW = UNR_NW;
   constexpr int MAXT = unr_maxt<DP>();
@@ -216,8 +220,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const int nts = NW / wpt;
   const int ts = wave / wpt, part = wave % wpt;
   const int n_pairs = (n_tiles + 1) / 2;
-  const float* qp = a.qp + bh * Np * DP;
-  const float* kp = a.kp + bh * Np * DP;
+  const T* qp = static_cast<const T*>(a.qp) + bh * Np * DP;
+  const T* kp = static_cast<const T*>(a.kp) + bh * Np * DP;
   const float* qt = a.qt + bh * DP * Np;
   const float* kt = a.kt + bh * DP * Np;
   const float* vp = a.vp + bh * Np * DP;
@@ -315,11 +319,12 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     }
     __syncthreads();
     const float* STC = ROW ? GLV : GLU;  // streamed recurrence coefficients
-    const float* Sop = ROW ? kp : qp;
+    const T* Sop = ROW ? kp : qp;
     const float* Sot = ROW ? kt : qt;
-    const float* Rop = ROW ? qp : kp;
+    const T* Rop = ROW ? qp : kp;
 
-    typename M::Frag bf[MAXT], cbf[MAXT];
+    typename MQ::Frag bf[MAXT];
+    typename M::Frag cbf[MAXT];
     float ra[MAXT], rb[MAXT], dd[MAXT], xr0[MAXT], xr1[MAXT], xr2[MAXT], Dr[MAXT], gr0[MAXT], gr1[MAXT], gr2[MAXT];
     float red[MAXT];
     f32x4 gVa[MAXT][NC];
@@ -328,7 +333,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       const int rt = ts + nts * s;
       const int ri = (t0 + min(rt, nr - 1)) * 16 + (lane & 15);
       const bool ok = rt < nr && ri < n && valid[ri];
-      M::load(bf[s], Rop + (size_t)ri * DP, lane);
+      MQ::load(bf[s], Rop + (size_t)ri * DP, lane);
       if (CENT) M::load(cbf[s], (ROW ? gp : vp) + (size_t)ri * DP, lane);
       ra[s] = rb[s] = NEG_BIG;
       dd[s] = 0.f;
@@ -373,8 +378,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           for (int hh = 0; hh < 2; ++hh) {
             const int st = 2 * sp + hh;
             const int o = st * 16 + 4 * g;
-            typename M::Frag af;
-            M::load(af, Sop + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+            typename MQ::Frag af;
+            MQ::load(af, Sop + (size_t)(st * 16 + (lane & 15)) * DP, lane);
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
             f32x4 t = zero;
             if (CENT) {
@@ -382,7 +387,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
               M::load(cf, (ROW ? vp : gp) + (size_t)(st * 16 + (lane & 15)) * DP, lane);
               t = M::qk(cf, cbf[s], zero);
             }
-            const f32x4 x = M::qk(af, bf[s], zero);
+            const f32x4 x = MQ::qk(af, bf[s], zero);
             const f32x4 sa = *reinterpret_cast<const f32x4*>(STA + o);
             const f32x4 sb = *reinterpret_cast<const f32x4*>(STB + o);
             const f32x4 scf = use_c ? *reinterpret_cast<const f32x4*>(STC + o) : zero;
@@ -577,9 +582,9 @@ hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipS
   return hipErrorInvalidValue;
 }
 
-template <int DP, bool GEN>
+template <typename T, int DP, bool GEN>
 static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  auto kern = unrolled_bwd_kernel<DP, GEN>;
+  auto kern = unrolled_bwd_kernel<T, DP, GEN>;
   hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(UNR_NT);
@@ -592,11 +597,18 @@ static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stre
   return hipGetLastError();
 }
 
-hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop) {
+template <typename T>
+static hipError_t launch_unr_dt(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop) {
   const bool gen = (a.bins8 && a.pos_w) || (a.has_geo && a.w_dist);
-  if (DP == 32) return gen ? launch_unr_t<32, true>(a, lds, stream, coop) : launch_unr_t<32, false>(a, lds, stream, coop);
-  if (DP == 64) return gen ? launch_unr_t<64, true>(a, lds, stream, coop) : launch_unr_t<64, false>(a, lds, stream, coop);
+  if (DP == 32)
+    return gen ? launch_unr_t<T, 32, true>(a, lds, stream, coop) : launch_unr_t<T, 32, false>(a, lds, stream, coop);
+  if (DP == 64)
+    return gen ? launch_unr_t<T, 64, true>(a, lds, stream, coop) : launch_unr_t<T, 64, false>(a, lds, stream, coop);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+  return bf16_in ? launch_unr_dt<bf16>(a, DP, lds, stream, coop) : launch_unr_dt<float>(a, DP, lds, stream, coop);
 }
 
 hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream) {
