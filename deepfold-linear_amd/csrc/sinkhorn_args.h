@@ -168,8 +168,8 @@ struct UnrBwdArgs {
   int has_geo;           // geometry term present (x given and w_dist given)
   const void* qp;        // [B*H][Np][DP] copies in the input type, zero on masked rows / padding
   const void* kp;
-  const float* qt;       // [B*H][DP][Np] fp32
-  const float* kt;
+  const void* qt;        // [B*H][DP][Np] in the input type
+  const void* kt;
   const float* vp;       // V rows
   const float* gp;       // gO rows (gO = sigma(G) dO)
   const float* gt;       // gO transposed
@@ -204,8 +204,9 @@ struct UnrPrepArgs {
   const float* grad_o;   // (B,N,H*d) fp32
   const float* grad_xc;  // (B,H,N,3) or null
   int B, H, N, d;
-  void* qp; void* kp;    // in the input type (the cost recompute's MFMA operands)
-  float* qt; float* kt; float* vp; float* gp; float* gt;
+  void* qp; void* kp;    // in the input type (the MFMA operands of the cost recompute and of dQ, dK)
+  void* qt; void* kt;
+  float* vp; float* gp; float* gt;
   float* dcoef; float* gxs; float* xs;
   float* dg;             // (B,H,N,d) or null (no gate)
 };

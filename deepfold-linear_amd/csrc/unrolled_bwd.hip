@@ -73,8 +73,8 @@ __global__ void __launch_bounds__(256) unrolled_prep_kernel(UnrPrepArgs p) {
   static_cast<T*>(p.kp)[row * DP + c] = from_f32<T>(kv);
   p.vp[row * DP + c] = vv;
   p.gp[row * DP + c] = go;
-  p.qt[((size_t)bh * DP + c) * Np + i] = qv;
-  p.kt[((size_t)bh * DP + c) * Np + i] = kv;
+  static_cast<T*>(p.qt)[((size_t)bh * DP + c) * Np + i] = from_f32<T>(qv);
+  static_cast<T*>(p.kt)[((size_t)bh * DP + c) * Np + i] = from_f32<T>(kv);
   p.gt[((size_t)bh * DP + c) * Np + i] = go;
   float part = go * oa;
 #pragma unroll
@@ -115,9 +115,10 @@ __global__ void __launch_bounds__(256) unrolled_finalize_kernel(UnrBwdArgs a, fl
 
 // GEN: the cost may carry position bins or geometry (set by the host when either is
 // passed); GEN = false compiles none of their per-element code.
-// T: the input type.  The cost recompute q.k runs on Mfma<T, DP> (bf16 inputs: the
-// bf16 MFMA, exact products with fp32 accumulation, as the forward); the centroid and
-// gradient products, whose operands are not bf16-exact, run on the fp32 MFMA.
+// T: the input type.  The cost recompute q.k and the products dQ += W K, dK += W^T Q
+// run on Mfma<T, DP> (bf16 inputs: the bf16 MFMA with exact operands, W as a hi + lo
+// bf16 pair, fp32 accumulation, as the forward); the centroid sweep's products, whose
+// operands (sigma(G) dO) are not bf16-exact, run on the fp32 MFMA.
 template <typename T, int DP, bool GEN>
 __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   using M = Mfma<float, DP>;
@@ -222,8 +223,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const int n_pairs = (n_tiles + 1) / 2;
   const T* qp = static_cast<const T*>(a.qp) + bh * Np * DP;
   const T* kp = static_cast<const T*>(a.kp) + bh * Np * DP;
-  const float* qt = a.qt + bh * DP * Np;
-  const float* kt = a.kt + bh * DP * Np;
+  const T* qt = static_cast<const T*>(a.qt) + bh * DP * Np;
+  const T* kt = static_cast<const T*>(a.kt) + bh * DP * Np;
   const float* vp = a.vp + bh * Np * DP;
   const float* gp = a.gp + bh * Np * DP;
   const float* gt = a.gt + bh * DP * Np;
@@ -320,7 +321,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     __syncthreads();
     const float* STC = ROW ? GLV : GLU;  // streamed recurrence coefficients
     const T* Sop = ROW ? kp : qp;
-    const float* Sot = ROW ? kt : qt;
+    const T* Sot = ROW ? kt : qt;
     const T* Rop = ROW ? qp : kp;
 
     typename MQ::Frag bf[MAXT];
@@ -457,9 +458,11 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           }
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
-            const float* vt_row = Sot + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32;
-            if (ROW) dQa[s][c] = M::pv(wop[0], wop[1], vt_row, lane, dQa[s][c]);
-            else dKa[s][c] = M::pv(wop[0], wop[1], vt_row, lane, dKa[s][c]);
+            // dQ += W K (dK += W^T Q): for bf16 inputs W is carried as a bf16 hi + lo pair
+            // against the exact bf16 operand (two bf16 MFMAs), as the forward's P V
+            const T* vt_row = Sot + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32;
+            if (ROW) dQa[s][c] = MQ::pv_split(wop[0], wop[1], vt_row, lane, dQa[s][c]);
+            else dKa[s][c] = MQ::pv_split(wop[0], wop[1], vt_row, lane, dKa[s][c]);
             if (CENT && !ROW)
               gVa[s][c] = M::pv(pop[0], pop[1], gt + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, gVa[s][c]);
           }
