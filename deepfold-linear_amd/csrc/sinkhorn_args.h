@@ -176,9 +176,9 @@ struct UnrBwdArgs {
   const float* dcoef;    // [B*H][Np] D_i = gO_i.O_i + dxc_i.xc_i
   const float* gxs;      // [B*H][3][Np] grad x_c
   const float* xs;       // [B][3][Np] coordinates
-  float* dq;             // (B,H,N,d) fp32
-  float* dk;
-  float* dv;
+  void* dq;              // (B,H,N,d) in the input type
+  void* dk;
+  void* dv;
   float* dlog_mu;        // (B,H,N)
   float* dlog_nu;
   float* dv_init;        // (B,H,N) or null
@@ -208,7 +208,7 @@ struct UnrPrepArgs {
   void* qt; void* kt;
   float* vp; float* gp; float* gt;
   float* dcoef; float* gxs; float* xs;
-  float* dg;             // (B,H,N,d) or null (no gate)
+  void* dg;              // (B,H,N,d) in the input type, or null (no gate)
 };
 
 struct BalPrepArgs {

@@ -63,11 +63,11 @@ __global__ void __launch_bounds__(256) unrolled_prep_kernel(UnrPrepArgs p) {
     float s = 1.f;
     if (p.g) {
       s = 1.f / (1.f + __expf(-to_f32(reinterpret_cast<const T*>(p.g)[off])));
-      p.dg[((size_t)bh * N + i) * d + c] = s * (1.f - s) * oa * dO;
+      static_cast<T*>(p.dg)[((size_t)bh * N + i) * d + c] = from_f32<T>(s * (1.f - s) * oa * dO);
     }
     go = s * dO;
   } else if (p.g && i < N && c < d) {
-    p.dg[((size_t)bh * N + i) * d + c] = 0.f;
+    static_cast<T*>(p.dg)[((size_t)bh * N + i) * d + c] = from_f32<T>(0.f);
   }
   static_cast<T*>(p.qp)[row * DP + c] = from_f32<T>(qv);  // exact: qv, kv come from T
   static_cast<T*>(p.kp)[row * DP + c] = from_f32<T>(kv);
@@ -170,9 +170,9 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const int nr = t1 - t0;
   for (int i = n_tiles * 16 + member; i < N; i += a.G) {
     for (int c = tid; c < d; c += UNR_NT) {
-      a.dq[(bh * N + i) * d + c] = 0.f;
-      a.dk[(bh * N + i) * d + c] = 0.f;
-      a.dv[(bh * N + i) * d + c] = 0.f;
+      static_cast<T*>(a.dq)[(bh * N + i) * d + c] = from_f32<T>(0.f);
+      static_cast<T*>(a.dk)[(bh * N + i) * d + c] = from_f32<T>(0.f);
+      static_cast<T*>(a.dv)[(bh * N + i) * d + c] = from_f32<T>(0.f);
     }
     if (tid < 3) a.dx_part[(bh * N + i) * 3 + tid] = 0.f;
     if (tid == 0) {
@@ -244,7 +244,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
 
-  auto write_rows = [&](f32x4 (&acc)[MAXT][NC], float* out, float scale) {
+  auto write_rows = [&](f32x4 (&acc)[MAXT][NC], void* out, float scale) {  // gradients in the input type
     __syncthreads();
     if (wpt > 1 && part > 0 && ts < nr) {
 #pragma unroll
@@ -265,7 +265,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
             float v = acc[s][c][r];
             for (int p = 1; p < wpt; ++p) v += spart[(size_t)(wave + p) * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)];
             const int row = (t0 + rt) * 16 + 4 * g + r, col = c * 16 + (lane & 15);
-            if (row < N && col < d) out[(bh * N + row) * d + col] = (row < n && valid[row]) ? scale * v : 0.f;
+            if (row < N && col < d)
+              static_cast<T*>(out)[(bh * N + row) * d + col] = from_f32<T>((row < n && valid[row]) ? scale * v : 0.f);
           }
       }
     }

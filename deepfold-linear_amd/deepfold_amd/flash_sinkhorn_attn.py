@@ -148,10 +148,9 @@ class FlashSinkhornAttn(torch.autograd.Function):
             grad_o_flat = torch.zeros(B, N, H * d, **f32)
         go = grad_o_flat.detach().to(torch.float32).contiguous()
         gxc = None if grad_xc is None else grad_xc.detach().to(torch.float32).contiguous()
-        # the kernels write every position of these (zeros where padded); the IFT
-        # backward writes q, k, v, g gradients in the inputs' dtype, the unrolled one fp32
-        gdt = torch.float32 if ctx.unrolled is not None else dt
-        dq, dk, dv, dg = (torch.empty(B, H, N, d, device=dev, dtype=gdt) for _ in range(4))
+        # the kernels write every position of these (zeros where padded), in the
+        # inputs' dtype
+        dq, dk, dv, dg = (torch.empty(B, H, N, d, device=dev, dtype=dt) for _ in range(4))
         dlmu = torch.empty(B, H, N, **f32)
         dlnu = torch.empty(B, H, N, **f32)
         # optional outputs: NULL skips their per-element work in the kernel

@@ -174,10 +174,12 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
  * w_dist, log_mu, log_nu, log_v_init, mask, B, H, N, d, K_iter >= 1, lam, r_0) and
  * outputs (o_avg, x_centroid, log_u, log_z, and hist, which the forward must have
  * written), grad_o (B,N,H*d) fp32 and grad_xc (B,H,N,3) (may be NULL).  Outputs
- * (fp32, fully written): dq, dk, dv, dg (dg may be NULL without g) (B,H,N,d),
- * dlog_mu, dlog_nu (B,H,N); optional (NULL = not requested): dlog_v_init (B,H,N),
- * dx_res (B,N,3), dpos_weight (H,68), dw_dist (H,).  Padded tokens are excluded, as
- * in dfl_sinkhorn_bwd.  The sweeps run in fp32 for either dtype.  Workspace:
+ * (fully written): dq, dk, dv, dg (dg may be NULL without g) (B,H,N,d) in `dtype`;
+ * fp32 dlog_mu, dlog_nu (B,H,N); optional fp32 (NULL = not requested): dlog_v_init
+ * (B,H,N), dx_res (B,N,3), dpos_weight (H,68), dw_dist (H,).  Padded tokens are
+ * excluded, as in dfl_sinkhorn_bwd.  Accumulation is fp32; with bf16 inputs the cost
+ * recompute and the dq / dk products run on the bf16 MFMA (exact operands; the plan
+ * weights as a bf16 hi + lo pair), the rest in fp32.  Workspace:
  * dfl_sinkhorn_unrolled_workspace_size(B, H, N, d) bytes; the forward's workspace
  * rules apply (a workspace that served the forward may serve this call if large enough).
  */
@@ -208,10 +210,10 @@ typedef struct dfl_sinkhorn_unrolled_bwd_params {
   const float* hist;
   const float* grad_o;
   const float* grad_xc;
-  float* dq;
-  float* dk;
-  float* dv;
-  float* dg;
+  void* dq; /* in `dtype` */
+  void* dk;
+  void* dv;
+  void* dg;
   float* dlog_mu;
   float* dlog_nu;
   float* dlog_v_init;
