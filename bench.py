@@ -297,7 +297,7 @@ def bench_sinkhorn(args, name):
     x_dom = x_fwd if dom == "sinkhorn_fwd" else x_bwd
     achieved = f_dom / (avg[dom] * 1e-3)
     traffic = profiled_traffic(dom, "sinkhorn_cfg2_bench.md" if name == "cfg2" else f"sinkhorn_{name}_bench.md")
-    peak = PEAK_MFMA_F32 if cfg.get("unrolled") and dom != "sinkhorn_fwd" else PEAK_MFMA_BF16
+    peak = PEAK_MFMA_BF16  # bf16 inputs: both backwards run their products on the bf16 MFMA
     t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
     metric = ("flash-Sinkhorn fwd+IFT-bwd ms/layer @B2,H8,N768,d32 bf16; % of MFMA/HBM roof" if name == "cfg2"
               else f"flash-Sinkhorn fwd+{'unrolled' if cfg.get('unrolled') else 'IFT'}-bwd ms/layer "
