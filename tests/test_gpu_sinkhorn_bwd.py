@@ -178,3 +178,28 @@ def test_backward_general_cost_fp32():
     fo = ref.forward(**oi, K_iter=5)
     want = ref.backward_reference(dict(oi, K_iter=5), fo, go.numpy(), gxc.numpy())
     compare(got, want, 1e-4, "general")
+
+
+def test_backward_bins_outside_table():
+    """Bins outside [0, 68) carry no bias and receive no d pos_weight: the gradients
+    equal the oracle's with a 69-entry table (entry 68 = 0) and those bins remapped
+    to 68, whose extra gradient entry is dropped."""
+    B, H, N, d = 2, 2, 40, 32
+    inp = make_inputs(B, H, N, d, seed=83, eps=[0.5, 2.0], pos_geo=True)
+    g = torch.Generator().manual_seed(84)
+    bins = inp["pos_bins"].clone()
+    sel = torch.rand(bins.shape, generator=g) < 0.2
+    bad = torch.tensor([-1, 68, 200, 1 << 20], dtype=torch.int32)[torch.randint(0, 4, bins.shape, generator=g)]
+    bins[sel] = bad[sel]
+    inp["pos_bins"] = bins
+    go, gxc = grad_inputs(B, H, N, d, seed=85, with_xc=True)
+    got = run_gpu_bwd(inp, 5, torch.float32, go, gxc)
+    oi = oracle_inputs(inp, torch.float32)
+    oi["pos_weight"] = np.concatenate([oi["pos_weight"], np.zeros((H, 1), np.float32)], 1)
+    b = oi["pos_bins"].astype(np.int64)
+    b[(b < 0) | (b >= 68)] = 68
+    oi["pos_bins"] = b
+    fo = ref.forward(**oi, K_iter=5)
+    want = ref.backward_reference(dict(oi, K_iter=5), fo, go.numpy(), gxc.numpy())
+    compare(got, want, 1e-4, "bins-outside", skip=("pos_weight",))
+    assert_close_rel(got["pos_weight"], np.asarray(want["pos_weight"])[:, :68], 1e-4, "bins-outside:pos_weight")
