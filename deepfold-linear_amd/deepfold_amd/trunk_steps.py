@@ -214,7 +214,7 @@ def token_ot_transport_step(block, h: torch.Tensor, x_res: torch.Tensor, mask: t
         x_centroid, h_centroid = balanced_sinkhorn_transport_dual(Q_s, K_s, x_res, V_s, block.eps, block.alpha_h,
                                                                   block.r_h, K_iter=K_iter, mask=mask)
         h_transport = h_centroid.permute(0, 2, 1, 3).reshape(B, N, C)
-        h = h + block.w_o_sink(h_transport.to(h.dtype)) * mask.unsqueeze(-1).to(h.dtype)
+        h = h + block.w_o_sink(h_transport) * mask.unsqueeze(-1)  # dtypes promote as in the reference
     else:
         x_centroid = balanced_sinkhorn_transport(Q_s, K_s, x_res, block.eps, block.alpha_h, block.r_h,
                                                  K_iter=K_iter, mask=mask)
