@@ -77,7 +77,8 @@ class SinkProjectionFn(torch.autograd.Function):
                               kn, mean, rstd)
         ctx.has_v = w_v is not None
         ctx.H = H
-        ctx.like = (h, ln_weight, ln_bias, w_q, w_k, w_v)
+        # only the dtypes of the inputs are needed to return their gradients
+        ctx.dtypes = tuple(None if t is None else t.dtype for t in (h, ln_weight, ln_bias, w_q, w_k, w_v))
         return q, k, v
 
     @staticmethod
@@ -107,10 +108,10 @@ class SinkProjectionFn(torch.autograd.Function):
         _launch("sink_proj_bwd", dev, lambda: lib.dfl_sink_proj_bwd(
             ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))),
             "dfl_sink_proj_bwd")
-        h, lnw, lnb, w_q, w_k, w_v = ctx.like
-        cast = lambda g, like: None if g is None else g.to(like.dtype)
-        return (cast(dh, h), cast(dlw, lnw), cast(dlb, lnb), cast(dwq, w_q), cast(dwk, w_k),
-                cast(dwv, w_v) if w_v is not None else None, None)
+        dts = ctx.dtypes
+        cast = lambda g, dt: None if g is None or dt is None else g.to(dt)
+        return (cast(dh, dts[0]), cast(dlw, dts[1]), cast(dlb, dts[2]), cast(dwq, dts[3]), cast(dwk, dts[4]),
+                cast(dwv, dts[5]), None)
 
 
 def sink_projections(h: torch.Tensor, ln_weight: torch.Tensor, ln_bias: torch.Tensor, w_q: torch.Tensor,
@@ -149,7 +150,8 @@ class GatedCoordUpdateFn(torch.autograd.Function):
             ctypes.byref(p), ctypes.c_void_p(_lib.stream_handle(dev))), "dfl_coord_update_fwd")
         ctx.save_for_backward(hc, *t, mk if mk is not None else hc.new_empty(0))
         ctx.has_mask = mk is not None
-        ctx.like = (h, x_res, x_centroid, ln_weight, ln_bias, w_gate, b_gate, lambda_raw)
+        ctx.dtypes = tuple(t.dtype for t in (h, x_res, x_centroid, ln_weight, ln_bias, w_gate, b_gate, lambda_raw))
+        ctx.shapes = (w_gate.shape, b_gate.shape)
         return out.to(x_res.dtype)
 
     @staticmethod
@@ -176,10 +178,10 @@ class GatedCoordUpdateFn(torch.autograd.Function):
         _launch("coord_update_bwd", dev, lambda: lib.dfl_coord_update_bwd(
             ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))),
             "dfl_coord_update_bwd")
-        h, x_res, x_centroid, ln_weight, ln_bias, w_gate, b_gate, lambda_raw = ctx.like
-        return (dh.to(h.dtype), dx.to(x_res.dtype), dxc.to(x_centroid.dtype), dlw.to(ln_weight.dtype),
-                dlb.to(ln_bias.dtype), dwg.reshape(w_gate.shape).to(w_gate.dtype),
-                dbg.reshape(b_gate.shape).to(b_gate.dtype), dlr.to(lambda_raw.dtype), None)
+        dts = ctx.dtypes
+        wg_shape, bg_shape = ctx.shapes
+        return (dh.to(dts[0]), dx.to(dts[1]), dxc.to(dts[2]), dlw.to(dts[3]), dlb.to(dts[4]),
+                dwg.reshape(wg_shape).to(dts[5]), dbg.reshape(bg_shape).to(dts[6]), dlr.to(dts[7]), None)
 
 
 def gated_coordinate_update(h: torch.Tensor, x_res: torch.Tensor, x_centroid: torch.Tensor, ln_weight: torch.Tensor,
