@@ -111,8 +111,13 @@ def _run_backward(saved, K_iter, grad_xc, grad_hc):
     return dq, dk, dv, dx, da, dr
 
 
-def _cast(t, like):
-    return None if t is None else t.to(like.dtype)
+def _cast(t, dtype):
+    return None if t is None or dtype is None else t.to(dtype)
+
+
+def _dtypes(*ts):
+    # only the inputs' dtypes are kept for the backward, not the tensors
+    return tuple(None if t is None else t.dtype for t in ts)
 
 
 class BalancedSinkhornFn(torch.autograd.Function):
@@ -123,15 +128,15 @@ class BalancedSinkhornFn(torch.autograd.Function):
         saved = _run_forward(Q_s, K_s, x_res, None, eps, alpha_h, r_h, K_iter, mask)
         ctx.saved = saved
         ctx.K_iter = int(K_iter)
-        ctx.dtypes = (Q_s, K_s, x_res, alpha_h, r_h)
+        ctx.dtypes = _dtypes(Q_s, K_s, x_res, alpha_h, r_h)
         return saved[8].to(Q_s.dtype)
 
     @staticmethod
     def backward(ctx, grad_xc):
-        Q_s, K_s, x_res, alpha_h, r_h = ctx.dtypes
+        t_q, t_k, t_x, t_a, t_r = ctx.dtypes
         dq, dk, _, dx, da, dr = _run_backward(ctx.saved, ctx.K_iter, grad_xc, None)
         ctx.saved = None
-        return (_cast(dq, Q_s), _cast(dk, K_s), _cast(dx, x_res), None, _cast(da, alpha_h), _cast(dr, r_h),
+        return (_cast(dq, t_q), _cast(dk, t_k), _cast(dx, t_x), None, _cast(da, t_a), _cast(dr, t_r),
                 None, None)
 
 
@@ -143,16 +148,16 @@ class BalancedSinkhornDualFn(torch.autograd.Function):
         saved = _run_forward(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask)
         ctx.saved = saved
         ctx.K_iter = int(K_iter)
-        ctx.dtypes = (Q_s, K_s, x_res, V_h, alpha_h, r_h)
+        ctx.dtypes = _dtypes(Q_s, K_s, x_res, V_h, alpha_h, r_h)
         return saved[8].to(Q_s.dtype), saved[9].to(Q_s.dtype)
 
     @staticmethod
     def backward(ctx, grad_xc, grad_hc):
-        Q_s, K_s, x_res, V_h, alpha_h, r_h = ctx.dtypes
+        t_q, t_k, t_x, t_v, t_a, t_r = ctx.dtypes
         dq, dk, dv, dx, da, dr = _run_backward(ctx.saved, ctx.K_iter, grad_xc, grad_hc)
         ctx.saved = None
-        return (_cast(dq, Q_s), _cast(dk, K_s), _cast(dx, x_res), _cast(dv, V_h), None, _cast(da, alpha_h),
-                _cast(dr, r_h), None, None)
+        return (_cast(dq, t_q), _cast(dk, t_k), _cast(dx, t_x), _cast(dv, t_v), None, _cast(da, t_a),
+                _cast(dr, t_r), None, None)
 
 
 def balanced_sinkhorn_transport(
