@@ -100,27 +100,91 @@ def make_workload(cfg, device, dtype=None):
     return cpu, dev
 
 
-def step(cfg, t):
+def step(cfg, t, want=False):
+    """One layer: forward + backward with upstream dO.  want=True also makes log mu /
+    log nu leaves and returns every output and gradient (the same kernels run)."""
     from deepfold_amd import flash_sinkhorn_attn
 
     q, k, v, g = (t[n].detach().requires_grad_(True) for n in ("Q", "K", "V", "G"))
+    lmu, lnu = t["log_mu"], t["log_nu"]
+    if want:
+        lmu, lnu = lmu.detach().requires_grad_(True), lnu.detach().requires_grad_(True)
     if cfg.get("full_cost"):  # position weights, geometry weights and coordinates receive gradients too
         pw, wd, x = (t[n].detach().requires_grad_(True) for n in ("pos_weight", "w_dist", "x_res"))
         o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, x, pw, t["pos_bins"], t["eps"], wd,
-                                            t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
+                                            lmu, lnu, K_iter=cfg["K_iter"], mask=t["mask"],
                                             ift_solver="cg", ift_iters=cfg["n_cg"])
     elif cfg.get("unrolled"):
         # neutral terms: no bins and no geometry weight (w_dist = None is the reference's
         # w_dist = 0 without reading x), so the kernels built without the bias terms run
         o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], None,
-                                            t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
+                                            lmu, lnu, K_iter=cfg["K_iter"], mask=t["mask"],
                                             ift_mode="unrolled")
     else:
         o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], None,
-                                            t["log_mu"], t["log_nu"], K_iter=cfg["K_iter"], mask=t["mask"],
+                                            lmu, lnu, K_iter=cfg["K_iter"], mask=t["mask"],
                                             ift_solver="cg", ift_iters=cfg["n_cg"])
     o.backward(t["dO"])
-    return q.grad
+    if not want:
+        return q.grad
+    res = dict(o_flat=o, x_centroid=xc, log_u=lu, log_v=lv, Q=q.grad, K=k.grad, V=v.grad, G=g.grad,
+               log_mu=lmu.grad, log_nu=lnu.grad)
+    return {n: x.detach().float().cpu().numpy() for n, x in res.items()}
+
+
+def verify_head(cfg, cpu, res, tol=2e-2):
+    """Parity of one (b, h) head of a bench step against the CPU oracle, run after and
+    outside the timed region on the same inputs: the longest sample's head 0 on its
+    valid tokens.  IFT workloads: oracle forward + reference-mode backward with the
+    bench's CG step count (oracle/sinkhorn.py, flash_sinkhorn_attn.py:144-218,
+    246-667); unrolled: float64 autograd through the dense iteration
+    (oracle/sinkhorn_dense_ref.py, the gradient of sinkhorn_kernel.py:2085-2382).
+    Normwise relative errors of the outputs, potentials and per-head gradients."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import sinkhorn as ref
+
+    B, H, d, K = cfg["B"], cfg["H"], cfg["d"], cfg["K_iter"]
+    b = max(range(B), key=lambda i: cpu["lengths"][i])
+    h, n = 0, cpu["lengths"][b]
+    inp = _head_inputs(cfg, cpu, b, h, K)
+    inp = {k: (np.asarray(v, dtype=np.float64) if isinstance(v, np.ndarray) and k != "pos_bins" else v)
+           for k, v in inp.items()}
+    go = cpu["dO"].reshape(B, -1, H, d)[b:b + 1, :n, h, :].double().numpy()
+    fo = ref.forward(**inp)
+    if cfg.get("unrolled"):
+        from oracle import sinkhorn_dense_ref as dref
+
+        f64 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).double()
+        q, k, v, g = (f64(inp[n_]).requires_grad_(True) for n_ in ("Q", "K", "V", "G"))
+        lmu, lnu = f64(inp["log_mu"]).requires_grad_(True), f64(inp["log_nu"]).requires_grad_(True)
+        C = -(q @ k.transpose(-1, -2)) / math.sqrt(d)
+        lu, lv = dref.sinkhorn_solve(C, lmu, lnu, f64(inp["eps"]), K=K)
+        o, _, _ = dref.compute_transport_output(v, g, lu, lv, C, f64(inp["eps"]))
+        (o * f64(go)).sum().backward()
+        gr = {n_: x.grad.numpy() for n_, x in (("Q", q), ("K", k), ("V", v), ("G", g), ("log_mu", lmu),
+                                                  ("log_nu", lnu))}
+    else:
+        gr = ref.backward_reference(inp, fo, go, None, solver="cg", n_cg=cfg["n_cg"])
+
+    def rel(got, want):
+        got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+        return float(np.max(np.abs(got - want)) / max(float(np.max(np.abs(want))), 1e-30))
+
+    errs = {
+        "o_flat": rel(res["o_flat"][b, :n, h * d:(h + 1) * d], fo["o_flat"][0]),
+        "x_centroid": rel(res["x_centroid"][b, h, :n], fo["x_centroid"][0, 0]),
+        "log_u": rel(res["log_u"][b, h, :n], fo["log_u"][0, 0]),
+        "log_v": rel(res["log_v"][b, h, :n], fo["log_v"][0, 0]),
+    }
+    for k_ in ("Q", "K", "V", "G", "log_mu", "log_nu"):
+        errs["d" + k_] = rel(res[k_][b, h, :n], gr[k_][0, 0])
+    return {"head": [b, h], "n_valid": n, "oracle": "oracle/sinkhorn.py" if not cfg.get("unrolled")
+            else "oracle/sinkhorn_dense_ref.py (float64 autograd)", "tol": tol,
+            "max_rel_err": {k_: float(f"{v_:.3e}") for k_, v_ in errs.items()},
+            "pass": bool(all(v_ <= tol for v_ in errs.values()))}
 
 
 def algorithmic_counts(cfg, lengths):
@@ -165,6 +229,59 @@ def _head_inputs(cfg, cpu, b, h, K_iter):
                 log_mu=cpu["log_mu"][b:b + 1, h:h + 1, :n].numpy(),
                 log_nu=cpu["log_nu"][b:b + 1, h:h + 1, :n].numpy(),
                 K_iter=K_iter, lam=1.0, r_0=10.0)
+
+
+def host_cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_torch(cfg, cpu, reps=3):
+    """The reference CPU fallback's algorithm restated densely in torch (float32, all
+    host cores): per sample on its valid tokens, all heads at once, the dense forward
+    (K log-domain iterations, flash_sinkhorn_attn.py:144-218) and the reference-mode
+    IFT backward with K_back = K_iter Gauss-Seidel sweeps (:246-667), i.e.
+    oracle/sinkhorn_dense_torch.forward + backward(solver="fixed_point").  One warm-up
+    layer, then the median of `reps` layers."""
+    import statistics
+
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import sinkhorn_dense_torch as dense
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    B, H, d, K = cfg["B"], cfg["H"], cfg["d"], cfg["K_iter"]
+    lengths = cpu["lengths"]
+    f32 = lambda x: x.float()
+
+    def layer():
+        t0 = time.perf_counter()
+        for b, n in enumerate(lengths):
+            sl = lambda a: f32(a[b:b + 1, :, :n]).contiguous()
+            q, k, v, g = sl(cpu["Q"]), sl(cpu["K"]), sl(cpu["V"]), sl(cpu["G"])
+            lmu, lnu = f32(cpu["log_mu"][b:b + 1, :, :n]), f32(cpu["log_nu"][b:b + 1, :, :n])
+            eps = f32(cpu["eps"])
+            fo = dense.forward(q, k, v, g, eps, lmu, lnu, K)
+            go = f32(cpu["dO"][b:b + 1, :n]).contiguous()
+            dense.backward(q, k, v, g, eps, fo, go, K, solver="fixed_point")
+        return time.perf_counter() - t0
+
+    with torch.no_grad():
+        layer()
+        times = [layer() for _ in range(reps)]
+    med = statistics.median(times)
+    return dict(value=round(med * 1e3, 1), unit="ms/layer", cores=cores, kind="port",
+                sample=(f"CPU restatement of the reference fallback (oracle/sinkhorn_dense_torch.py): dense forward "
+                        f"K={K} + reference fixed-point IFT backward ({K} sweeps), float32 torch on {cores} threads "
+                        f"({host_cpu_model()}), the whole layer (n_b={lengths}, {H} heads), 1 warm-up + median of "
+                        f"{reps} ({', '.join(f'{x * 1e3:.0f}' for x in times)} ms)"))
 
 
 def cpu_baseline(cfg, cpu, budget_s=12.0):
@@ -285,6 +402,9 @@ def bench_sinkhorn(args, name):
     wall = time.perf_counter() - t0
     timings = _lib.launch_timings
     _lib.launch_timings = None
+    import deepfold_amd
+
+    deepfold_amd.check_errors(dev)  # raises if any timed kernel gave up on a cross-workgroup wait
     per = {}
     for kname, s, e in timings:
         per.setdefault(kname, []).append(s.elapsed_time(e))
@@ -328,8 +448,22 @@ def bench_sinkhorn(args, name):
                          "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
                          "layer_t_roof_ms": t_roof * 1e3, "layer_frac": t_roof * 1e3 / ms_per_step},
     }
+    out["kernel_errors"] = 0  # check_errors passed after the timed steps
+    if cfg["N"] <= 1024:
+        # after and outside the timed region: the same step, checked against the oracle
+        res = step(cfg, t, want=True)
+        deepfold_amd.check_errors(dev)
+        out["parity_check"] = verify_head(cfg, cpu, res)
+    else:
+        out["parity_check"] = {"skipped": "the float64 oracle needs minutes per N=4096 head; this workload's parity "
+                                          "is tested in tests/test_gpu_sinkhorn_stream.py"}
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = unrolled_cpu_baseline(cfg, cpu) if cfg.get("unrolled") else cpu_baseline(cfg, cpu)
+        if cfg.get("unrolled"):
+            out["cpu_baseline"] = unrolled_cpu_baseline(cfg, cpu)
+        elif name == "cfg2":
+            out["cpu_baseline"] = cpu_baseline_torch(cfg, cpu)
+        else:
+            out["cpu_baseline"] = cpu_baseline(cfg, cpu)
     print(json.dumps(out), flush=True)
 
 

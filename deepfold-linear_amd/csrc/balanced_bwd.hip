@@ -135,7 +135,7 @@ __global__ void __launch_bounds__(BAL_NT) balanced_bwd_kernel(BalBwdArgs a) {
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, g = lane >> 4;
   if (tid == 0) { s_flag = 0; s_cnt = 0; }
   if (blockIdx.x == 0 && tid == 0)
-    __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.err.ws + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- LDS carve-up (must match balanced_bwd_lds_bytes)
   unsigned char* valid = smem;

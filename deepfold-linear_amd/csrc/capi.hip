@@ -6,7 +6,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 
 #include "../../include/dfl_amd.h"
 #include "attn_args.h"
@@ -45,6 +47,7 @@ hipError_t dense_zero(float* p, size_t n, hipStream_t s);
 hipError_t dense_transport_forward(const DenseTransportArgs& a, hipStream_t s);
 hipError_t dense_transport_backward(const DenseTransportArgs& a, hipStream_t s);
 hipError_t launch_bins8(const int* bins, int B, int N, uint8_t* b8, uint8_t* b8t, hipStream_t stream);
+hipError_t launch_fill_u64(uint64_t* p, size_t n, hipStream_t stream);
 size_t balanced_bwd_lds_bytes(int N, int DP);
 int balanced_max_tiles(int DP);
 hipError_t launch_balanced_prep(const BalPrepArgs& p, int DP, hipStream_t stream);
@@ -77,11 +80,83 @@ int hip_fail(hipError_t e, const char* what) {
   return (int)e;
 }
 
-std::atomic<uint32_t> g_salt{1};
-uint32_t next_salt() {
-  uint32_t s = g_salt.fetch_add(1) & 0xfffffu;
-  if (s == 0) s = g_salt.fetch_add(1) & 0xfffffu;
-  return s == 0 ? 1u : s;
+// Exchange tags carry a 20-bit call salt (common.h).  The counter behind it is
+// 64-bit: its bits above the salt count the salt's wrap-arounds ("epochs").  A
+// workspace first used in one epoch and used again in a later one could hold a
+// word whose salt and phase match a current tag, so its exchange region and
+// header are cleared (fill kernel, on the call's stream) at its first use in each
+// new epoch.  A workspace never seen before is taken as zero-filled, as the ABI
+// requires of a new workspace.
+std::atomic<uint64_t> g_salt_counter{1};
+std::mutex g_ws_mu;
+struct WsState {
+  uint64_t epoch;      // epoch of the last clear (or of the first use)
+  size_t clean_bytes;  // bytes from the workspace start known free of older epochs' words
+};
+std::unordered_map<const void*, WsState> g_ws_state;
+
+// Salt for a launch on `workspace` whose kernels read the first `xch_end` bytes
+// (header + exchange words); clears what an earlier epoch may have left there.
+// Returns 0 or a hipError_t of the clear launch.
+int acquire_salt(void* workspace, size_t xch_end, void* stream, uint32_t* salt_out) {
+  uint64_t c = g_salt_counter.fetch_add(1);
+  if ((c & 0xfffffu) == 0) c = g_salt_counter.fetch_add(1);  // salt 0 is never used
+  const uint64_t epoch = c >> 20;
+  *salt_out = (uint32_t)(c & 0xfffffu);
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  auto it = g_ws_state.find(workspace);
+  if (it == g_ws_state.end()) {
+    g_ws_state.emplace(workspace, WsState{epoch, ~(size_t)0});
+    return 0;
+  }
+  size_t from = 0;
+  if (it->second.epoch != epoch) {
+    it->second = WsState{epoch, 0};
+  } else if (it->second.clean_bytes >= xch_end) {
+    return 0;
+  } else {
+    from = it->second.clean_bytes;
+  }
+  from &= ~(size_t)7;
+  const size_t words = (xch_end - from + 7) / 8;
+  hipError_t e = dfl::launch_fill_u64(reinterpret_cast<uint64_t*>(static_cast<unsigned char*>(workspace) + from),
+                                      words, (hipStream_t)stream);
+  if (e != hipSuccess) return (int)e;
+  it->second.clean_bytes = from + words * 8;
+  return 0;
+}
+
+// Pinned, device-mapped host word that a kernel writes when one of its waits
+// expires (common.h: ErrRef); read and cleared by dfl_pending_error().  Allocated
+// once per process; null if the allocation fails (errors then stay in the
+// workspace word only).
+uint32_t* g_mailbox_host = nullptr;
+uint32_t* g_mailbox_dev = nullptr;
+std::once_flag g_mailbox_once;
+uint32_t* mailbox() {
+  std::call_once(g_mailbox_once, [] {
+    void* h = nullptr;
+    if (hipHostMalloc(&h, 256, hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) != hipSuccess) {
+      (void)hipGetLastError();
+      return;
+    }
+    memset(h, 0, 256);
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      d = h;  // unified addressing: the host address is valid on the device
+    }
+    g_mailbox_host = static_cast<uint32_t*>(h);
+    g_mailbox_dev = static_cast<uint32_t*>(d);
+  });
+  return g_mailbox_dev;
+}
+
+dfl::ErrRef err_ref(void* workspace) {
+  dfl::ErrRef r;
+  r.ws = static_cast<uint32_t*>(workspace);
+  r.host = mailbox();
+  return r;
 }
 
 constexpr size_t WS_HEADER = 256;  // error word + last salt, cache-line padded
@@ -279,10 +354,11 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, void* workspace
     return fail("N=%d, d=%d, %s storage needs %zu bytes of LDS per workgroup (limit %zu)", a.N, a.d,
                 stream_mode ? "stream" : "resident", lds, LDS_LIMIT);
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.err = err_ref(ws);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
-  a.salt = next_salt();
+  if (int rc = acquire_salt(ws, WS_HEADER + xch_words(a.B, a.H, a.N) * 8, stream, &a.salt))
+    return hip_fail((hipError_t)rc, "workspace clear launch");
   if (a.bins)
     if (int rc = prepare_bins8(a.bins, a.B, a.N, workspace, sinkhorn_bins8_offset(a.B, a.H, a.N), &a.bins8,
                                &a.bins8t, stream))
@@ -401,6 +477,16 @@ size_t dfl_sinkhorn_workspace_size(int B, int H, int N) {
   return stream_region_offset(B, H, N, G) + stream_region_bytes(B, H, N, G) + bins8_bytes(B, N);
 }
 
+int dfl_pending_error(void) {
+  if (!g_mailbox_host) return 0;
+  const uint32_t w = __atomic_exchange_n(g_mailbox_host, 0u, __ATOMIC_ACQ_REL);
+  if (w == 0) return 0;
+  const int code = (int)(w & 0xfffu);
+  g_err = "a kernel launched earlier reported error code " + std::to_string(code) +
+          " (a cross-workgroup wait expired; its outputs are invalid)";
+  return code;
+}
+
 int dfl_workspace_error(const void* workspace, void* stream) {
   if (!workspace) return fail("workspace is NULL");
   uint32_t words[2] = {0, 0};
@@ -494,7 +580,7 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dg = p->dg;
   a.dlog_mu = p->dlog_mu; a.dlog_nu = p->dlog_nu;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.err = err_ref(ws);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   unsigned char* cur = ws + WS_HEADER + xch_words(p->B, p->H, p->N) * 8;
   float* parts = reinterpret_cast<float*>(cur);
@@ -508,7 +594,8 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   a.go_t = cur + 2 * opb;
   a.dcoef = reinterpret_cast<float*>(cur + 3 * opb);
   a.G = G;
-  a.salt = next_salt();
+  if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
+    return hip_fail((hipError_t)rc, "workspace clear launch");
   a.ch = CH;
   if (p->pos_bins)
     if (int rc = prepare_bins8(p->pos_bins, p->B, p->N, workspace, sinkhorn_bins8_offset(p->B, p->H, p->N),
@@ -819,10 +906,11 @@ int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t w
   a.qp = pr.qp; a.kp = pr.kp; a.qt = pr.qt; a.kt = pr.kt; a.vp = pr.vp; a.gp = pr.gp; a.gt = pr.gt;
   a.dcoef = pr.dcoef; a.gxs = pr.gxs; a.xs = pr.xs; a.has_h = has_h ? 1 : 0;
   a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dx_part = F(L.dx_part); a.ar_part = F(L.ar_part);
-  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.err = err_ref(ws);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
-  a.salt = next_salt();
+  if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
+    return hip_fail((hipError_t)rc, "workspace clear launch");
   e = dfl::launch_balanced_bwd(a, DP, lds, (hipStream_t)stream, G > 1);
   if (e != hipSuccess) return hip_fail(e, "balanced backward launch");
   e = dfl::launch_balanced_finalize(a, p->dx_res, p->dalpha_h, p->dr_h, (hipStream_t)stream);
@@ -889,10 +977,11 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
   a.dq = p->dq; a.dk = p->dk; a.dv = p->dv; a.dlog_mu = p->dlog_mu; a.dlog_nu = p->dlog_nu;
   a.dv_init = p->dlog_v_init;
   a.dx_part = F(L.dx_part); a.dpw_part = F(L.dpw_part); a.dw_part = F(L.dw_part);
-  a.err = reinterpret_cast<uint32_t*>(ws);
+  a.err = err_ref(ws);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
-  a.salt = next_salt();
+  if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
+    return hip_fail((hipError_t)rc, "workspace clear launch");
   e = dfl::launch_unrolled_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, G > 1);
   if (e != hipSuccess) return hip_fail(e, "unrolled backward launch");
   e = dfl::launch_unrolled_finalize(a, p->x_res ? p->dx_res : nullptr, p->dpos_weight, p->dw_dist,

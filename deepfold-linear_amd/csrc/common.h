@@ -249,13 +249,22 @@ __device__ __forceinline__ void block_atomic_max_u32(unsigned* s, unsigned x) {
 // Error flag and tagged exchange.
 constexpr uint32_t SPIN_LIMIT = 1u << 22;  // ~2-4 s of polling
 
-// The error word holds (salt << 12) | code for the call that raised it; a word
-// carrying another call's salt is stale and ignored.
-__device__ __forceinline__ void raise_error(uint32_t* err, uint32_t salt, uint32_t code) {
-  __hip_atomic_store(err, (salt << 12) | (code & 0xfffu), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Where a kernel reports an expired wait: the workspace's error word, which holds
+// (salt << 12) | code for the call that raised it (a word carrying another call's
+// salt is stale and ignored), and, when the library has one, a word of pinned,
+// device-mapped host memory that the host reads at its next call without a
+// synchronisation (only a kernel that gives up writes it).
+struct ErrRef {
+  uint32_t* ws;    // workspace error word (word 1 of the header holds the latest salt)
+  uint32_t* host;  // mapped host mailbox, or null
+};
+__device__ __forceinline__ void raise_error(ErrRef err, uint32_t salt, uint32_t code) {
+  const uint32_t w = (salt << 12) | (code & 0xfffu);
+  __hip_atomic_store(err.ws, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (err.host) __hip_atomic_store(err.host, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
-__device__ __forceinline__ bool error_raised(const uint32_t* err, uint32_t salt) {
-  const uint32_t e = __hip_atomic_load(const_cast<uint32_t*>(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ bool error_raised(ErrRef err, uint32_t salt) {
+  const uint32_t e = __hip_atomic_load(err.ws, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return (e >> 12) == salt && (e & 0xfffu) != 0u;
 }
 

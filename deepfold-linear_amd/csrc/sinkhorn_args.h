@@ -2,6 +2,8 @@
 #pragma once
 #include <stdint.h>
 
+#include "common.h"
+
 namespace dfl {
 
 // Workgroups launched for n_groups groups of G members: whole 8-XCD slots.
@@ -37,7 +39,7 @@ struct SinkFwdArgs {
   float* col_lse;     // (B,H,N)    LSE_i(L_ij + u_i) of the last column update
   // workspace
   uint64_t* xch;  // B*H*2*Np exchange words
-  uint32_t* err;  // error word
+  ErrRef err;     // error word (workspace) and host mailbox
   int G;          // workgroups per (b,h)
   uint32_t salt;  // 20-bit call salt for exchange tags
   // stream mode only (sinkhorn_pad_kernel output): zero-padded operand copies
@@ -99,7 +101,7 @@ struct SinkBwdArgs {
   float* dw_part;   // (B*H*G) per-workgroup partials
   // workspace
   uint64_t* xch;  // B*H*4*Np exchange words
-  uint32_t* err;
+  ErrRef err;
   // prepared by the prep kernel (per (b,h), Np rows, zero on invalid rows / padded columns):
   void* go_hi;    // [B*H][Np][DP]  T(gO), gO = sigma(G) * dO
   void* go_lo;    // [B*H][Np][DP]  T(gO - T(gO)) (bf16 inputs only)
@@ -143,7 +145,7 @@ struct BalBwdArgs {
   float* dx_part;      // (B,H,N,3) per-head partials
   float* ar_part;      // (B*H*G, 2) per-workgroup d alpha, d r partials
   uint64_t* xch;       // B*H*2*Np exchange words
-  uint32_t* err;
+  ErrRef err;
   int G;
   uint32_t salt;
 };
@@ -186,7 +188,7 @@ struct UnrBwdArgs {
   float* dpw_part;       // (B*H*G, 68)
   float* dw_part;        // (B*H*G)
   uint64_t* xch;
-  uint32_t* err;
+  ErrRef err;
   int G;
   uint32_t salt;
 };

@@ -158,7 +158,7 @@ __device__ __forceinline__ float block_sum(int n, F f, float* red, int& flip) {
 // (invalid entries and the tail [n, Np)); one barrier at the end.  Returns false
 // (uniformly) if the error flag is raised or a wait expires.
 __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
-                                              const unsigned char* valid, uint32_t* err, int* s_flag) {
+                                              const unsigned char* valid, ErrRef err, int* s_flag) {
   const uint32_t salt = tag >> 12;
   const int t = threadIdx.x;
   for (int i = n + t; i < Np; i += BWD_NT) dst[i] = 0.f;
@@ -445,7 +445,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const int g = lane >> 4;
   if (threadIdx.x == 0) sh.flag = 0;
   if (blockIdx.x == 0 && threadIdx.x == 0)
-    __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.err.ws + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   const size_t bh = (size_t)b * a.H + h;
   const size_t wg_id = bh * a.G + member;

@@ -185,7 +185,7 @@ __device__ __forceinline__ int mask_setup(const float* mask, int N, unsigned cha
 // Returns false (uniformly) if the error flag is raised or a wait expires.
 template <int NT>
 __device__ __forceinline__ bool gather_potential(const uint64_t* buf, int n, uint32_t tag, float* dst,
-                                                 const unsigned char* valid, uint32_t* err, int* s_flag,
+                                                 const unsigned char* valid, ErrRef err, int* s_flag,
                                                  unsigned* s_delta) {
   const int t = threadIdx.x;
   const uint32_t salt = tag >> 12;

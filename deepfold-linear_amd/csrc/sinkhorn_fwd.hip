@@ -37,6 +37,19 @@ hipError_t launch_bins8(const int* bins, int B, int N, uint8_t* b8, uint8_t* b8t
   return hipGetLastError();
 }
 
+// Zero fill of n 64-bit words (workspace exchange regions): a kernel rather than
+// hipMemsetAsync, so that a caller may capture the launch in a HIP graph.
+__global__ void __launch_bounds__(256) fill_u64_kernel(uint64_t* __restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0;
+}
+
+hipError_t launch_fill_u64(uint64_t* p, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_u64_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, stream, p, n);
+  return hipGetLastError();
+}
+
 template <typename T, int DP>
 static hipError_t launch_pad_t(const PadArgs& p, hipStream_t stream) {
   const size_t Np = ((p.N + 31) / 32) * 32;

@@ -174,7 +174,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const bool has_v = !BAL || (a.v != nullptr && a.o_avg != nullptr);  // UOT mode always has V
   if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; s_cnt = 0; }
   if (blockIdx.x == 0 && threadIdx.x == 0)
-    __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.err.ws + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- LDS carve-up (must match sinkhorn_fwd_lds_bytes)
   const int loc = fwd_local_rows(N, a.G);

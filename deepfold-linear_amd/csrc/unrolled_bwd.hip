@@ -144,7 +144,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     s_dpw[tid] = 0.f;
   }
   if (blockIdx.x == 0 && tid == 0)
-    __hip_atomic_store(a.err + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.err.ws + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- LDS carve-up (must match unrolled_bwd_lds_bytes)
   unsigned char* valid = smem;

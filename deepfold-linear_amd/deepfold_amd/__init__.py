@@ -19,3 +19,13 @@ from .trunk_steps import (  # noqa: F401
     GatedCoordUpdateFn, SinkProjectionFn, gated_coordinate_update, sink_projections, token_ot_transport_step)
 
 __version__ = "0.1.0"
+
+
+def check_errors(device=None) -> None:
+    """Synchronise ``device`` and raise if any kernel launched so far reported an
+    expired cross-workgroup wait (its outputs are then invalid).  Every op also
+    checks, without synchronising, before its own launch."""
+    import torch
+
+    torch.cuda.synchronize(device)
+    _lib.raise_pending("deepfold_amd.check_errors")

@@ -223,6 +223,7 @@ SIGNATURES = [
     ("dfl_last_error", ctypes.c_char_p, []),
     ("dfl_version", ctypes.c_char_p, []),
     ("dfl_workspace_error", I32, [P, P]),
+    ("dfl_pending_error", I32, []),
     ("dfl_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
     ("dfl_sinkhorn_fwd", I32, [ctypes.POINTER(SinkhornFwdParams), P, ctypes.c_size_t, P]),
     ("dfl_sinkhorn_bwd", I32, [ctypes.POINTER(SinkhornBwdParams), P, ctypes.c_size_t, P]),
@@ -321,8 +322,23 @@ def workspace(device: torch.device, nbytes: int, kind: str = "sinkhorn") -> torc
 launch_timings: list | None = None
 
 
+def raise_pending(what: str = "deepfold_amd") -> None:
+    """Raise if a kernel launched earlier reported an expired cross-workgroup wait.
+
+    Reads a pinned host word that such a kernel writes (no synchronisation): it
+    sees what kernels completed so far reported.  Every C-ABI launch below calls
+    it first, so a failed launch raises at the next call at the latest; call
+    ``torch.cuda.synchronize()`` before it to check a finished batch of work."""
+    code = load().dfl_pending_error()
+    if code != 0:
+        msg = load().dfl_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {msg}")
+
+
 def timed_launch(name: str, device: torch.device, fn):
-    """Run ``fn()`` (one C-ABI call), bracketing it with events if timing is on."""
+    """Run ``fn()`` (one C-ABI call), bracketing it with events if timing is on.
+    Raises first if an earlier launch reported an expired wait."""
+    raise_pending(name)
     if launch_timings is None:
         return fn()
     s = torch.cuda.Event(enable_timing=True)

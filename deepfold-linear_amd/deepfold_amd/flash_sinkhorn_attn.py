@@ -131,8 +131,10 @@ class FlashSinkhornAttn(torch.autograd.Function):
             raise ValueError(f"ift_solver must be one of {sorted(_SOLVERS)}, got {solver!r}")
         if mode not in _MODES and mode != "unrolled":
             raise ValueError(f"ift_mode must be one of {sorted(_MODES) + ['unrolled']}, got {mode!r}")
-        ctx.save_for_backward(q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c)
-        ctx.unrolled = (hist, lmu, lnu, lv0, int(K_iter)) if mode == "unrolled" else None
+        unr = (hist, lmu, lnu, lv0) if mode == "unrolled" else (None,) * 4
+        ctx.save_for_backward(q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c, *unr)
+        ctx.unrolled = mode == "unrolled"
+        ctx.k_iter = int(K_iter)
         ctx.meta = (B, H, N, d, dt, float(lam), float(r_0), solver, int(iters), mode, rtol, len(opts),
                     Q_ln.dtype, G is not None, storage)
         ctx.set_materialize_grads(False)
@@ -140,7 +142,7 @@ class FlashSinkhornAttn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_o_flat, grad_xc, grad_lu_unused, grad_lv_unused):
-        (q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c) = ctx.saved_tensors
+        (q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c) = ctx.saved_tensors[:16]
         (B, H, N, d, dt, lam, r_0, solver, iters, mode, rtol, n_opts, in_dtype, has_g, storage) = ctx.meta
         dev = q.device
         f32 = dict(device=dev, dtype=torch.float32)
@@ -160,7 +162,7 @@ class FlashSinkhornAttn(torch.autograd.Function):
         dx = torch.empty(B, N, 3, **f32) if need_dx else None
         dpw = torch.empty(H, 68, **f32) if need_dpw else None
         dw = torch.empty(H, **f32) if need_dw else None
-        if ctx.unrolled is not None:
+        if ctx.unrolled:
             return FlashSinkhornAttn._backward_unrolled(ctx, go, gxc, dq, dk, dv, dg, dlmu, dlnu, dx, dpw, dw)
         lib = _lib.load()
         ws = _lib.workspace(dev, lib.dfl_sinkhorn_workspace_size(B, H, N))
@@ -190,9 +192,10 @@ class FlashSinkhornAttn(torch.autograd.Function):
 
     @staticmethod
     def _backward_unrolled(ctx, go, gxc, dq, dk, dv, dg, dlmu, dlnu, dx, dpw, dw):
-        (q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c) = ctx.saved_tensors
+        (q, k, v, g, x, pw, bins, eps_t, wd, m, log_u, log_v, log_z, col_lse, o_avg, x_c,
+         hist, lmu, lnu, lv0) = ctx.saved_tensors
         (B, H, N, d, dt, lam, r_0, solver, iters, mode, rtol, n_opts, in_dtype, has_g, storage) = ctx.meta
-        hist, lmu, lnu, lv0, K_iter = ctx.unrolled
+        K_iter = ctx.k_iter
         dev = q.device
         dlv0 = torch.empty(B, H, N, device=dev, dtype=torch.float32) if (lv0 is not None and
                                                                          ctx.needs_input_grad[15]) else None
@@ -216,7 +219,6 @@ class FlashSinkhornAttn(torch.autograd.Function):
         _lib.check(rc, "dfl_sinkhorn_unrolled_bwd")
         if _lib.debug_checks():
             _lib.check_workspace(ws, "dfl_sinkhorn_unrolled_bwd")
-        ctx.unrolled = None
         return ((dq, dk, dv, dg if has_g else None, dx, dpw, None, None, dw,
                  dlmu, dlnu, None, None, None, None, dlv0, None) + (None,) * n_opts)
 

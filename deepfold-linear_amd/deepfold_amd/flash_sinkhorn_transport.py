@@ -126,7 +126,7 @@ class BalancedSinkhornFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, Q_s, K_s, x_res, eps, alpha_h, r_h, K_iter, mask):
         saved = _run_forward(Q_s, K_s, x_res, None, eps, alpha_h, r_h, K_iter, mask)
-        ctx.saved = saved
+        ctx.save_for_backward(*saved)  # None entries are kept as None
         ctx.K_iter = int(K_iter)
         ctx.dtypes = _dtypes(Q_s, K_s, x_res, alpha_h, r_h)
         return saved[8].to(Q_s.dtype)
@@ -134,8 +134,7 @@ class BalancedSinkhornFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_xc):
         t_q, t_k, t_x, t_a, t_r = ctx.dtypes
-        dq, dk, _, dx, da, dr = _run_backward(ctx.saved, ctx.K_iter, grad_xc, None)
-        ctx.saved = None
+        dq, dk, _, dx, da, dr = _run_backward(ctx.saved_tensors, ctx.K_iter, grad_xc, None)
         return (_cast(dq, t_q), _cast(dk, t_k), _cast(dx, t_x), None, _cast(da, t_a), _cast(dr, t_r),
                 None, None)
 
@@ -146,7 +145,7 @@ class BalancedSinkhornDualFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask):
         saved = _run_forward(Q_s, K_s, x_res, V_h, eps, alpha_h, r_h, K_iter, mask)
-        ctx.saved = saved
+        ctx.save_for_backward(*saved)
         ctx.K_iter = int(K_iter)
         ctx.dtypes = _dtypes(Q_s, K_s, x_res, V_h, alpha_h, r_h)
         return saved[8].to(Q_s.dtype), saved[9].to(Q_s.dtype)
@@ -154,8 +153,7 @@ class BalancedSinkhornDualFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_xc, grad_hc):
         t_q, t_k, t_x, t_v, t_a, t_r = ctx.dtypes
-        dq, dk, dv, dx, da, dr = _run_backward(ctx.saved, ctx.K_iter, grad_xc, grad_hc)
-        ctx.saved = None
+        dq, dk, dv, dx, da, dr = _run_backward(ctx.saved_tensors, ctx.K_iter, grad_xc, grad_hc)
         return (_cast(dq, t_q), _cast(dk, t_k), _cast(dx, t_x), _cast(dv, t_v), None, _cast(da, t_a),
                 _cast(dr, t_r), None, None)
 

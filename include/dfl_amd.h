@@ -19,8 +19,13 @@
  *  - Return value: 0 = success, < 0 = argument error (see dfl_last_error()),
  *    > 0 = hipError_t of a failed launch.
  *  - Kernels that wait on other workgroups have bounded spins; if a wait ever
- *    expires the kernel exits and records an error in the workspace, which
- *    dfl_workspace_error() reports (it synchronises `stream`).
+ *    expires the kernel exits (its outputs are then invalid) and records an
+ *    error in the workspace, which dfl_workspace_error() reports (it
+ *    synchronises `stream`), and in a pinned host word, which
+ *    dfl_pending_error() reads without synchronising.
+ *  - Exchange words are tagged with a 20-bit call salt.  When the salt wraps
+ *    (every 2^20 calls), the first call on each workspace clears that
+ *    workspace's exchange region with a fill kernel on its stream.
  */
 #ifndef DFL_AMD_H
 #define DFL_AMD_H
@@ -42,6 +47,13 @@ const char* dfl_version(void);
 /* Reports (and clears nothing) the error recorded by the most recent call that
  * used `workspace`: 0 = none, else the kernel's error code.  Synchronises `stream`. */
 int dfl_workspace_error(const void* workspace, void* stream);
+
+/* Error code of a kernel wait that expired in any launch since the last call to
+ * this function (0 = none), read from pinned host memory that such a kernel writes:
+ * no synchronisation, so it sees what completed kernels reported.  Clears it.
+ * The reference has no counterpart: its ops fall back to the CPU on any exception
+ * (flash_sinkhorn_attn.py:144, 751); here a failure is reported, never hidden. */
+int dfl_pending_error(void);
 
 /* ---------------------------------------------------------------------------
  * Flash-Sinkhorn forward.

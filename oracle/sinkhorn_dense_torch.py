@@ -12,10 +12,16 @@ that configuration uses; the other cost terms are checked against the numpy
 oracle at small sizes.
 
 * ``forward``     -- flash_sinkhorn_attn.py:144-218 (== oracle.sinkhorn.forward)
-* ``backward_cg`` -- flash_sinkhorn_attn.py:246-667 with the IFT system solved by
-                     CG on its symmetric form (== oracle.sinkhorn.backward_reference
-                     with solver="cg", and ``mode="analytic"`` flips the signs as
-                     oracle.sinkhorn.backward_analytic does)
+* ``backward``    -- flash_sinkhorn_attn.py:246-667 with the IFT system solved either
+                     by the reference's Gauss-Seidel sweeps (solver="fixed_point",
+                     :471-542; == oracle.sinkhorn.backward_reference) or by CG on its
+                     symmetric form (solver="cg"; == backward_reference with
+                     solver="cg"); ``mode="analytic"`` flips the signs as
+                     oracle.sinkhorn.backward_analytic does.  ``backward_cg`` is the
+                     CG form.
+
+bench.py's CPU baseline times ``forward`` + ``backward(solver="fixed_point")``
+(the reference CPU fallback's algorithm) in float32 on the host cores.
 
 Pinned by tests/test_oracle_sinkhorn_dense.py: equal to the numpy oracle in
 float64 on CPU (both modes, several shapes, general marginals).
@@ -84,9 +90,18 @@ def _cg(matvec, b, n_iter):
 
 
 def backward_cg(Q, K, V, G, eps, fwd, grad_o_flat, n_cg, lam=1.0, mode="reference", grad_xc=None, x_res=None):
+    """IFT backward with the system solved by n_cg CG steps (see ``backward``)."""
+    return backward(Q, K, V, G, eps, fwd, grad_o_flat, n_cg, lam=lam, mode=mode, grad_xc=grad_xc, x_res=x_res,
+                    solver="cg")
+
+
+def backward(Q, K, V, G, eps, fwd, grad_o_flat, n_iter, lam=1.0, mode="reference", grad_xc=None, x_res=None,
+             solver="cg"):
     """IFT backward of ``forward`` (flash_sinkhorn_attn.py:246-667), dense, batched.
 
-    The linear system (I - kappa^2 S_row^T S_col) z_v = g_v is solved with n_cg CG
+    The linear system (I - kappa^2 S_row^T S_col) z_v = g_v is solved either by
+    n_iter reference Gauss-Seidel sweeps from z = g (solver="fixed_point",
+    :471-542: z_u = kappa S_col z_v, z_v = g_v + kappa S_row^T z_u) or by n_iter CG
     steps on (I - kappa^2 W^T W) y = D_c^{-1/2} g_v, W = D_r^{-1/2} T D_c^{-1/2}.
     Returns dict of gradients Q, K, V, G, log_mu, log_nu.
     """
@@ -114,21 +129,31 @@ def backward_cg(Q, K, V, G, eps, fwd, grad_o_flat, n_cg, lam=1.0, mode="referenc
     gls = T * (dT - D[:, :, :, None])                                 # :386
     g_v = gls.sum(-2)                                                 # :388
     dV = torch.matmul(T.transpose(-1, -2).contiguous(), gO)           # :389
-    # CG on the symmetric form: T_un = exp(u + L + v - max logZ) (a scalar rescaling of T)
-    T_un = T * torch.exp(logZ - logZ.amax(dim=-1, keepdim=True))[:, :, :, None]
-    r = T_un.sum(-1)
-    c = T_un.sum(-2)
-    W = T_un / r.sqrt()[:, :, :, None] / c.sqrt()[:, :, None, :]
-    Wt = W.transpose(-1, -2).contiguous()
-    k2 = (kappa * kappa)
+    if solver == "fixed_point":
+        S_row_t = S_row.transpose(-1, -2).contiguous()
+        z_v = g_v.clone()                                             # :472-473 (g_u = 0)
+        z_u = torch.zeros_like(g_v)
+        for _ in range(n_iter):                                       # :475-542
+            z_u = kappa * torch.matmul(S_col, z_v[..., None])[..., 0]
+            z_v = g_v + kappa * torch.matmul(S_row_t, z_u[..., None])[..., 0]
+    elif solver == "cg":
+        # CG on the symmetric form: T_un = exp(u + L + v - max logZ) (a scalar rescaling of T)
+        T_un = T * torch.exp(logZ - logZ.amax(dim=-1, keepdim=True))[:, :, :, None]
+        r = T_un.sum(-1)
+        c = T_un.sum(-2)
+        W = T_un / r.sqrt()[:, :, :, None] / c.sqrt()[:, :, None, :]
+        Wt = W.transpose(-1, -2).contiguous()
+        k2 = (kappa * kappa)
 
-    def A(y):
-        t = torch.matmul(W, y[..., None])[..., 0]
-        return y - k2 * torch.matmul(Wt, t[..., None])[..., 0]
+        def A(y):
+            t = torch.matmul(W, y[..., None])[..., 0]
+            return y - k2 * torch.matmul(Wt, t[..., None])[..., 0]
 
-    y = _cg(A, g_v / c.sqrt(), n_cg)
-    z_v = c.sqrt() * y
-    z_u = kappa * torch.matmul(S_col, z_v[..., None])[..., 0]
+        y = _cg(A, g_v / c.sqrt(), n_iter)
+        z_v = c.sqrt() * y
+        z_u = kappa * torch.matmul(S_col, z_v[..., None])[..., 0]
+    else:
+        raise ValueError(f"unknown solver {solver!r}")
     sgn = -1.0 if mode == "reference" else 1.0
     # reference: dC = -(1/eps) gls - (kappa/eps)(z_u S_row + z_v S_col)          (:594-615)
     # analytic : lambda_v = z_v, lambda_u = -z_u; dC = -(1/eps) gls + (kappa/eps)(lambda_u S_row + lambda_v S_col)

@@ -114,6 +114,31 @@ def test_struct_layout_matches_c(lib_path):
             assert getattr(cls, f).offset == c_layout[(sname, f)], (sname, f)
 
 
+def test_integration_snippet_matches_binding():
+    """The ctypes struct INTEGRATION.md shows a maintainer lists every field of
+    dfl_sinkhorn_fwd_params, in order and with the right C types: a struct that
+    stops short hands the library whatever memory follows it."""
+    from deepfold_amd import _lib
+
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text[text.index("class FwdParams(ctypes.Structure)"):]
+    block = block[:block.index("lib.dfl_sinkhorn_workspace_size")]
+    fields = re.findall(r'\("(\w+)",\s*(\w)\)', block)
+    types = {"P": ctypes.c_void_p, "I": ctypes.c_int, "L": ctypes.c_longlong, "F": ctypes.c_float}
+    assert [n for n, _ in fields] == [n for n, _ in _lib.SinkhornFwdParams._fields_]
+    assert [n for n, _ in fields] == header_structs()["dfl_sinkhorn_fwd_params"]
+    for (n, t), (_, want) in zip(fields, _lib.SinkhornFwdParams._fields_):
+        assert types[t] is want, n
+
+
+def test_pending_error_is_clear_without_launches(lib_path):
+    """The error mailbox reads 0 before any kernel ran (and reading it needs no GPU)."""
+    from deepfold_amd import _lib
+
+    assert _lib.load(lib_path).dfl_pending_error() == 0
+    _lib.raise_pending("test")
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
     from deepfold_amd import (atom_to_token_attn, balanced_sinkhorn_transport, balanced_sinkhorn_transport_dual,

@@ -62,6 +62,24 @@ def test_dense_backward_cg_reference_equals_numpy_oracle(with_xc):
         assert_close_rel(got[k].numpy(), want[k], 1e-9, k)
 
 
+@pytest.mark.parametrize("K_back", [1, 3, 25])
+def test_dense_backward_fixed_point_equals_numpy_oracle(K_back):
+    """The reference's Gauss-Seidel sweeps, sweep for sweep (a short K_back leaves the
+    solve unconverged, so the sweep order and count are what is compared)."""
+    B, H, N, d, K = 2, 2, 20, 8, 25
+    t, go, gxc = _case(B, H, N, d, 13, [0.5, 1.0])
+    fo = dense.forward(t["Q"], t["K"], t["V"], t["G"], t["eps"], t["log_mu"], t["log_nu"], K, x_res=t["x_res"])
+    got = dense.backward(t["Q"], t["K"], t["V"], t["G"], t["eps"], fo, go, K_back, grad_xc=gxc, x_res=t["x_res"],
+                         solver="fixed_point")
+    oi = _np_inputs(t, K)
+    want = ref.backward_reference(oi, ref.forward(**oi), go.numpy(), gxc.numpy(), K_back=K_back)
+    for k in ("Q", "K", "V", "G", "log_mu", "log_nu"):
+        assert_close_rel(got[k].numpy(), want[k], 1e-9, k)
+    if K_back == 1:  # one sweep differs from the converged solve: the comparison discriminates
+        conv = ref.backward_reference(oi, ref.forward(**oi), go.numpy(), gxc.numpy(), K_back=60)
+        assert np.max(np.abs(got["log_nu"].numpy() - conv["log_nu"])) > 1e-6
+
+
 def test_dense_backward_analytic_equals_numpy_oracle():
     """Analytic signs; CG run long enough to reach the exact solve of the numpy oracle."""
     B, H, N, d, K = 1, 2, 20, 8, 40
