@@ -60,6 +60,11 @@ hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, bool bf16_in, int DP, size_t
 hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream);
 }  // namespace dfl
 
+// Scratch of dfl_sinkhorn_fwd_noalloc: exchange words, error word and bins copies.
+// One copy per GPU, allocated with the code object and held until the process ends.
+// Host code uses the device address from hipGetSymbolAddress, never this name.
+static __device__ __align__(256) unsigned char scratch[DFL_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_err;
@@ -98,31 +103,37 @@ std::unordered_map<const void*, WsState> g_ws_state;
 // Salt for a launch on `workspace` whose kernels read the first `xch_end` bytes
 // (header + exchange words); clears what an earlier epoch may have left there.
 // Returns 0 or a hipError_t of the clear launch.
-int acquire_salt(void* workspace, size_t xch_end, void* stream, uint32_t* salt_out) {
+// fixed: the record of a buffer the library owns (the allocation-free entry point's
+// static array), used instead of a map entry so that nothing is allocated.
+int acquire_salt(void* workspace, size_t xch_end, void* stream, uint32_t* salt_out, WsState* fixed = nullptr) {
   uint64_t c = g_salt_counter.fetch_add(1);
   if ((c & 0xfffffu) == 0) c = g_salt_counter.fetch_add(1);  // salt 0 is never used
   const uint64_t epoch = c >> 20;
   *salt_out = (uint32_t)(c & 0xfffffu);
   std::lock_guard<std::mutex> lock(g_ws_mu);
-  auto it = g_ws_state.find(workspace);
-  if (it == g_ws_state.end()) {
-    g_ws_state.emplace(workspace, WsState{epoch, ~(size_t)0});
-    return 0;
+  WsState* st = fixed;
+  if (!st) {
+    auto it = g_ws_state.find(workspace);
+    if (it == g_ws_state.end()) {
+      g_ws_state.emplace(workspace, WsState{epoch, ~(size_t)0});
+      return 0;
+    }
+    st = &it->second;
   }
   size_t from = 0;
-  if (it->second.epoch != epoch) {
-    it->second = WsState{epoch, 0};
-  } else if (it->second.clean_bytes >= xch_end) {
+  if (st->epoch != epoch) {
+    *st = WsState{epoch, 0};
+  } else if (st->clean_bytes >= xch_end) {
     return 0;
   } else {
-    from = it->second.clean_bytes;
+    from = st->clean_bytes;
   }
   from &= ~(size_t)7;
   const size_t words = (xch_end - from + 7) / 8;
   hipError_t e = dfl::launch_fill_u64(reinterpret_cast<uint64_t*>(static_cast<unsigned char*>(workspace) + from),
                                       words, (hipStream_t)stream);
   if (e != hipSuccess) return (int)e;
-  it->second.clean_bytes = from + words * 8;
+  st->clean_bytes = from + words * 8;
   return 0;
 }
 
@@ -131,7 +142,7 @@ int acquire_salt(void* workspace, size_t xch_end, void* stream, uint32_t* salt_o
 // once per process; null if the allocation fails (errors then stay in the
 // workspace word only).
 uint32_t* g_mailbox_host = nullptr;
-uint32_t* g_mailbox_dev = nullptr;
+std::atomic<uint32_t*> g_mailbox_dev{nullptr};
 std::once_flag g_mailbox_once;
 uint32_t* mailbox() {
   std::call_once(g_mailbox_once, [] {
@@ -147,15 +158,17 @@ uint32_t* mailbox() {
       d = h;  // unified addressing: the host address is valid on the device
     }
     g_mailbox_host = static_cast<uint32_t*>(h);
-    g_mailbox_dev = static_cast<uint32_t*>(d);
+    g_mailbox_dev.store(static_cast<uint32_t*>(d));
   });
-  return g_mailbox_dev;
+  return g_mailbox_dev.load();
 }
 
-dfl::ErrRef err_ref(void* workspace) {
+// may_allocate = false (allocation-free entry point): the mailbox only if an
+// earlier call already allocated it.
+dfl::ErrRef err_ref(void* workspace, bool may_allocate = true) {
   dfl::ErrRef r;
   r.ws = static_cast<uint32_t*>(workspace);
-  r.host = mailbox();
+  r.host = may_allocate ? mailbox() : g_mailbox_dev.load();
   return r;
 }
 
@@ -342,27 +355,84 @@ dfl::A2TArgs a2t_args(const dfl_a2t_params* p) {
   return a;
 }
 
+// Argument checks of dfl_sinkhorn_fwd_params (all but the workspace) and the kernel
+// argument block; 0 or a negative argument error.
+int fwd_args(const dfl_sinkhorn_fwd_params* p, dfl::SinkFwdArgs& a) {
+  if (!p) return fail("params is NULL");
+  if (p->dtype != DFL_BF16 && p->dtype != DFL_F32) return fail("dtype must be DFL_BF16 or DFL_F32");
+  if (p->B <= 0 || p->H <= 0 || p->N <= 0 || p->d <= 0) return fail("B, H, N, d must be positive");
+  if (head_dim_pad(p->d) < 0) return fail("head dim d=%d > 64 is not supported", p->d);
+  if (p->K_iter < 0 || p->K_iter > 2000) return fail("K_iter=%d outside [0, 2000]", p->K_iter);
+  if (!p->q || !p->k || !p->v || !p->eps || !p->log_mu || !p->log_nu) return fail("required input is NULL");
+  if (!p->o_flat || !p->x_centroid || !p->log_u || !p->log_v || !p->o_avg || !p->log_z || !p->col_lse)
+    return fail("output pointer is NULL");
+  if (p->stride_n < p->d) return fail("stride_n must be >= d (unit inner stride)");
+  if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
+  if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_STREAM) return fail("unknown storage %d", p->storage);
+  memset(&a, 0, sizeof(a));
+  a.q = p->q; a.k = p->k; a.v = p->v; a.g = p->g;
+  a.sb = p->stride_b; a.sh = p->stride_h; a.sn = p->stride_n;
+  a.x = p->x_res; a.pos_w = p->pos_weight; a.bins = p->pos_bins;
+  a.eps = p->eps; a.w_dist = p->w_dist; a.log_mu = p->log_mu; a.log_nu = p->log_nu;
+  a.u_init = p->log_u_init; a.v_init = p->log_v_init; a.mask = p->mask;
+  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d;
+  a.K_iter = p->K_iter; a.lam = p->lam; a.r0 = p->r_0;
+  a.o_flat = p->o_flat; a.x_centroid = p->x_centroid; a.log_u = p->log_u; a.log_v = p->log_v;
+  a.o_avg = p->o_avg; a.log_z = p->log_z; a.col_lse = p->col_lse;
+  a.hist = p->hist;
+  return 0;
+}
+
+// The allocation-free forward's per-device scratch (static array `scratch` at file
+// scope below): its device address on each GPU, resolved once per device, and that
+// buffer's salt-epoch record.
+constexpr size_t NOALLOC_SCRATCH_BYTES = DFL_NOALLOC_SCRATCH_BYTES;
+constexpr int MAX_DEVICES = 64;
+struct ScratchSlot {
+  unsigned char* ptr;
+  WsState state;
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[MAX_DEVICES];
+
+// Where a forward keeps its scratch: a caller's workspace (dfl_sinkhorn_fwd,
+// dfl_balanced_fwd) or the library's static per-device array
+// (dfl_sinkhorn_fwd_noalloc).  Layout: header, exchange words from WS_HEADER, the
+// uint8 bins copies at bins_off; stream storage also uses the workspace's stream region.
+struct FwdScratch {
+  unsigned char* base;
+  size_t bins_off;
+  bool allow_stream;   // false: the buffer has no stream region
+  WsState* fixed;      // salt-epoch record of a library-owned buffer (else the map)
+  bool may_allocate;   // the host mailbox may be allocated by this call
+};
+
 // Storage-mode choice, workspace pointers and launches of the persistent forward
-// (shared by the UOT and the balanced entry points).  a holds inputs and outputs.
-int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, void* workspace, void* stream) {
+// (shared by the UOT, the balanced and the allocation-free entry points).  a holds
+// inputs and outputs.
+int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratch& w, void* stream) {
   const int G = group_size(a.B, a.H, a.N);
   const int elem = bf16 ? 2 : 4;
   const size_t lds_res = dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, false);
   const bool stream_mode = storage == DFL_STORAGE_STREAM || (storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT);
   const size_t lds = stream_mode ? dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, true) : lds_res;
+  if (stream_mode && !w.allow_stream)
+    return fail("N=%d, d=%d needs stream storage (resident needs %zu bytes of LDS, limit %zu), which the "
+                "allocation-free forward does not provide", a.N, a.d, lds_res, LDS_LIMIT);
   if (lds > LDS_LIMIT)
     return fail("N=%d, d=%d, %s storage needs %zu bytes of LDS per workgroup (limit %zu)", a.N, a.d,
                 stream_mode ? "stream" : "resident", lds, LDS_LIMIT);
-  unsigned char* ws = static_cast<unsigned char*>(workspace);
-  a.err = err_ref(ws);
+  unsigned char* ws = w.base;
+  void* workspace = ws;
+  a.err = err_ref(ws, w.may_allocate);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
-  if (int rc = acquire_salt(ws, WS_HEADER + xch_words(a.B, a.H, a.N) * 8, stream, &a.salt))
+  // the forward's exchange words: u and v of every (b,h)
+  const size_t xch_end = WS_HEADER + (size_t)a.B * a.H * 2 * np32(a.N) * 8;
+  if (int rc = acquire_salt(ws, xch_end, stream, &a.salt, w.fixed))
     return hip_fail((hipError_t)rc, "workspace clear launch");
   if (a.bins)
-    if (int rc = prepare_bins8(a.bins, a.B, a.N, workspace, sinkhorn_bins8_offset(a.B, a.H, a.N), &a.bins8,
-                               &a.bins8t, stream))
-      return rc;
+    if (int rc = prepare_bins8(a.bins, a.B, a.N, workspace, w.bins_off, &a.bins8, &a.bins8t, stream)) return rc;
   const bool coop = G > 1;  // members wait on each other: all must be co-resident
   hipError_t e;
   if (stream_mode) {
@@ -501,34 +571,47 @@ int dfl_workspace_error(const void* workspace, void* stream) {
 }
 
 int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!p) return fail("params is NULL");
-  if (p->dtype != DFL_BF16 && p->dtype != DFL_F32) return fail("dtype must be DFL_BF16 or DFL_F32");
-  if (p->B <= 0 || p->H <= 0 || p->N <= 0 || p->d <= 0) return fail("B, H, N, d must be positive");
-  const int DP = head_dim_pad(p->d);
-  if (DP < 0) return fail("head dim d=%d > 64 is not supported", p->d);
-  if (p->K_iter < 0 || p->K_iter > 2000) return fail("K_iter=%d outside [0, 2000]", p->K_iter);
-  if (!p->q || !p->k || !p->v || !p->eps || !p->log_mu || !p->log_nu) return fail("required input is NULL");
-  if (!p->o_flat || !p->x_centroid || !p->log_u || !p->log_v || !p->o_avg || !p->log_z || !p->col_lse)
-    return fail("output pointer is NULL");
-  if (p->stride_n < p->d) return fail("stride_n must be >= d (unit inner stride)");
-  if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
+  dfl::SinkFwdArgs a;
+  if (int rc = fwd_args(p, a)) return rc;
   const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
   if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
-  if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_STREAM) return fail("unknown storage %d", p->storage);
+  const FwdScratch w{static_cast<unsigned char*>(workspace), sinkhorn_bins8_offset(p->B, p->H, p->N), true, nullptr,
+                     true};
+  return run_fwd(a, p->dtype == DFL_BF16, head_dim_pad(p->d), p->storage, w, stream);
+}
 
+int dfl_sinkhorn_fwd_noalloc(const dfl_sinkhorn_fwd_params* p, void* stream) {
   dfl::SinkFwdArgs a;
-  memset(&a, 0, sizeof(a));
-  a.q = p->q; a.k = p->k; a.v = p->v; a.g = p->g;
-  a.sb = p->stride_b; a.sh = p->stride_h; a.sn = p->stride_n;
-  a.x = p->x_res; a.pos_w = p->pos_weight; a.bins = p->pos_bins;
-  a.eps = p->eps; a.w_dist = p->w_dist; a.log_mu = p->log_mu; a.log_nu = p->log_nu;
-  a.u_init = p->log_u_init; a.v_init = p->log_v_init; a.mask = p->mask;
-  a.B = p->B; a.H = p->H; a.N = p->N; a.d = p->d;
-  a.K_iter = p->K_iter; a.lam = p->lam; a.r0 = p->r_0;
-  a.o_flat = p->o_flat; a.x_centroid = p->x_centroid; a.log_u = p->log_u; a.log_v = p->log_v;
-  a.o_avg = p->o_avg; a.log_z = p->log_z; a.col_lse = p->col_lse;
-  a.hist = p->hist;
-  return run_fwd(a, p->dtype == DFL_BF16, DP, p->storage, workspace, stream);
+  if (int rc = fwd_args(p, a)) return rc;
+  if (p->storage == DFL_STORAGE_STREAM)
+    return fail("the allocation-free forward runs resident storage only (storage=DFL_STORAGE_STREAM given)");
+  // layout in the static array: header, u/v exchange words, then the uint8 bins copies
+  const size_t xch_end = WS_HEADER + (size_t)p->B * p->H * 2 * np32(p->N) * 8;
+  const size_t bins_off = (xch_end + 255) / 256 * 256;
+  const size_t need = bins_off + (p->pos_bins ? bins8_bytes(p->B, p->N) : 0);
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return fail("B=%d, H=%d, N=%d%s needs %zu bytes of scratch; the allocation-free forward holds %zu", p->B, p->H,
+                p->N, p->pos_bins ? " with pos_bins" : "", need, NOALLOC_SCRATCH_BYTES);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= MAX_DEVICES) return fail("device %d outside [0, %d)", dev, MAX_DEVICES);
+  ScratchSlot* slot = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    slot = &g_scratch[dev];
+    if (!slot->ptr) {
+      // The array's address on this device (each GPU holds its own copy); the host-side
+      // name of the array is not a device address and is never passed to a kernel.
+      void* ptr = nullptr;
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+      slot->ptr = static_cast<unsigned char*>(ptr);
+      slot->state = WsState{~(uint64_t)0, 0};  // first use clears the exchange region
+    }
+  }
+  const FwdScratch w{slot->ptr, bins_off, false, &slot->state, false};
+  return run_fwd(a, p->dtype == DFL_BF16, head_dim_pad(p->d), p->storage, w, stream);
 }
 
 int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
@@ -860,7 +943,8 @@ int dfl_balanced_fwd(const dfl_balanced_fwd_params* p, void* workspace, size_t w
   a.x_centroid = p->x_centroid; a.o_avg = p->h_centroid;
   a.log_u = p->log_u; a.log_v = p->log_v; a.log_z = p->log_z;
   a.balanced = 1; a.alpha = p->alpha_h; a.r_h = p->r_h; a.hist = p->hist;
-  return run_fwd(a, false, head_dim_pad(p->d), p->storage, workspace, stream);
+  const FwdScratch w{static_cast<unsigned char*>(workspace), 0, true, nullptr, true};  // no bins
+  return run_fwd(a, false, head_dim_pad(p->d), p->storage, w, stream);
 }
 
 int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {

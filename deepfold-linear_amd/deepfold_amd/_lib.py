@@ -226,6 +226,7 @@ SIGNATURES = [
     ("dfl_pending_error", I32, []),
     ("dfl_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
     ("dfl_sinkhorn_fwd", I32, [ctypes.POINTER(SinkhornFwdParams), P, ctypes.c_size_t, P]),
+    ("dfl_sinkhorn_fwd_noalloc", I32, [ctypes.POINTER(SinkhornFwdParams), P]),
     ("dfl_sinkhorn_bwd", I32, [ctypes.POINTER(SinkhornBwdParams), P, ctypes.c_size_t, P]),
     ("dfl_sinkhorn_unrolled_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
     ("dfl_sinkhorn_unrolled_bwd", I32, [ctypes.POINTER(SinkhornUnrolledBwdParams), P, ctypes.c_size_t, P]),

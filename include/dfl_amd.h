@@ -115,6 +115,19 @@ typedef struct dfl_sinkhorn_fwd_params {
 size_t dfl_sinkhorn_workspace_size(int B, int H, int N);
 int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of dfl_sinkhorn_fwd.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * params, outputs and kernels as dfl_sinkhorn_fwd, resident storage only (AUTO or
+ * RESIDENT; a problem that needs stream storage is rejected).  Instead of a
+ * workspace it uses a static device array of DFL_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends: it needs 256 + 16*B*H*Np bytes (+ 2*B*Np*Np with
+ * pos_bins), Np = N rounded up to 32, and rejects larger problems.  Every call on
+ * one GPU shares that array, so calls that overlap in time on one GPU race.  It
+ * calls no hipMalloc / hipFree and no allocating library routine. */
+#define DFL_NOALLOC_SCRATCH_BYTES (8u << 20)
+int dfl_sinkhorn_fwd_noalloc(const dfl_sinkhorn_fwd_params* p, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Flash-Sinkhorn IFT backward.
  * Replaces FlashSinkhornAttn.backward (flash_sinkhorn_attn.py:246-667).  The linear
