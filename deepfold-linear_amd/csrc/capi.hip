@@ -193,8 +193,9 @@ int cu_count() {
 
 size_t np32(int N) { return (size_t)((N + 31) / 32) * 32; }
 
-// Exchange words per (b,h): u and v for the forward; four vectors for the backward.
-size_t xch_words(int B, int H, int N) { return (size_t)B * H * 4 * np32(N); }
+// Exchange words per (b,h): u and v for the forward, four vectors for the backward,
+// then 32 placement words per (b,h) (after all vector slots).
+size_t xch_words(int B, int H, int N) { return (size_t)B * H * (4 * np32(N) + 32); }
 
 int head_dim_pad(int d) { return d <= 32 ? 32 : (d <= 64 ? 64 : -1); }
 
@@ -427,8 +428,8 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
   a.err = err_ref(ws, w.may_allocate);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
-  // the forward's exchange words: u and v of every (b,h)
-  const size_t xch_end = WS_HEADER + (size_t)a.B * a.H * 2 * np32(a.N) * 8;
+  // the forward's exchange words: u and v of every (b,h), then 32 placement words per (b,h)
+  const size_t xch_end = WS_HEADER + (size_t)a.B * a.H * (2 * np32(a.N) + 32) * 8;
   if (int rc = acquire_salt(ws, xch_end, stream, &a.salt, w.fixed))
     return hip_fail((hipError_t)rc, "workspace clear launch");
   if (a.bins)
@@ -585,8 +586,9 @@ int dfl_sinkhorn_fwd_noalloc(const dfl_sinkhorn_fwd_params* p, void* stream) {
   if (int rc = fwd_args(p, a)) return rc;
   if (p->storage == DFL_STORAGE_STREAM)
     return fail("the allocation-free forward runs resident storage only (storage=DFL_STORAGE_STREAM given)");
-  // layout in the static array: header, u/v exchange words, then the uint8 bins copies
-  const size_t xch_end = WS_HEADER + (size_t)p->B * p->H * 2 * np32(p->N) * 8;
+  // layout in the static array: header, u/v exchange words and placement words, then
+  // the uint8 bins copies
+  const size_t xch_end = WS_HEADER + (size_t)p->B * p->H * (2 * np32(p->N) + 32) * 8;
   const size_t bins_off = (xch_end + 255) / 256 * 256;
   const size_t need = bins_off + (p->pos_bins ? bins8_bytes(p->B, p->N) : 0);
   if (need > NOALLOC_SCRATCH_BYTES)

@@ -159,39 +159,14 @@ __device__ __forceinline__ float block_sum(int n, F f, float* red, int& flip) {
 // (uniformly) if the error flag is raised or a wait expires.
 __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
                                               const unsigned char* valid, ErrRef err, int* s_flag) {
-  const uint32_t salt = tag >> 12;
   const int t = threadIdx.x;
   for (int i = n + t; i < Np; i += BWD_NT) dst[i] = 0.f;
-  bool ok = true;
-  for (int base = 0; base < n && ok; base += 8 * BWD_NT) {
-    uint32_t pending = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (base + t + k * BWD_NT < n) pending |= 1u << k;
-    uint32_t spins = 0;
-    while (pending) {
-      uint64_t w[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (pending & (1u << k))
-          w[k] = __hip_atomic_load(const_cast<uint64_t*>(buf + base + t + k * BWD_NT), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if ((pending & (1u << k)) && (uint32_t)w[k] == tag) {
-          const int i = base + t + k * BWD_NT;
-          dst[i] = valid[i] ? __uint_as_float((uint32_t)(w[k] >> 32)) : 0.f;
-          pending &= ~(1u << k);
-        }
-      }
-      if (pending) {
-        __builtin_amdgcn_s_sleep(1);  // back off: tight polling slows the publishers' stores
-        if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); ok = false; break; }
-        if ((spins & 255u) == 0u && error_raised(err, salt)) { ok = false; break; }
-      }
-    }
-  }
+  const bool ok = poll_vector<BWD_NT>(buf, n, tag, err, [&](int off, uint64_t w) {
+    const int i = off + t;
+    dst[i] = valid[i] ? __uint_as_float((uint32_t)(w >> 32)) : 0.f;
+  });
   if (!ok) *s_flag = 1;
+  // dst may be global memory (stream storage keeps the vectors in the workspace)
   __syncthreads();
   return *s_flag == 0;
 }
@@ -413,7 +388,7 @@ __device__ __forceinline__ void put_grad(void* p, size_t i, float v) {
 }
 
 struct BwdShared {
-  int flag, tmp;
+  int flag, tmp, local;
   float posw[BIN_NONE + 1];
   float red[2 * BWD_NW];
 };
@@ -443,7 +418,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int g = lane >> 4;
-  if (threadIdx.x == 0) sh.flag = 0;
+  if (threadIdx.x == 0) { sh.flag = 0; sh.local = 1; }
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(a.err.ws + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
@@ -560,6 +535,11 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   uint64_t* xbase = a.xch + bh * 4 * (size_t)Np;
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
+  // placement words of the group (after all (b,h)'s four vector slots); plain-store
+  // publishing from the second exchange on if every member is on its XCD
+  uint64_t* xpl = a.xch + (size_t)a.B * a.H * 4 * Np + bh * 32;
+  publish_placement(xpl, member, a.salt);
+  bool local = false;
   constexpr int NC = DP / 16;
 
   // =========================================================================
@@ -721,6 +701,8 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     uint64_t* xg = xbase;  // slot 0: g_v
     for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xg + j, lout[j - r_lo], salt | phase);
     if (!gather_vector(xg, n, Np, salt | phase, gv, valid, a.err, &sh.flag)) return;
+    if (!read_placement(xpl, a.G, n_tiles, a.salt, a.err, &sh.flag, &sh.local)) return;
+    local = sh.local != 0;
   }
 
   // =========================================================================
@@ -784,13 +766,13 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       // z_u_i = kappa sum_j S_col_ij z_v_j   (resident rows: cres = u_i)
       wsum(true, mcl, zvv, uu + r_lo);
       ++phase;
-      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, kappa * lout[i - r_lo], salt | phase);
+      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, kappa * lout[i - r_lo], salt | phase, local);
       if (!gather_vector(xA, n, Np, salt | phase, zu, valid, a.err, &sh.flag)) return;
       // z_v_j = g_v_j + kappa sum_i T_ij z_u_i   (resident cols: cres = v_j)
       wsum(false, a2, zu, vv + r_lo);
       ++phase;
       for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT)
-        xch_put(xB + j, gv[j] + kappa * lout[j - r_lo], salt | phase);
+        xch_put(xB + j, gv[j] + kappa * lout[j - r_lo], salt | phase, local);
       if (!gather_vector(xB, n, Np, salt | phase, zvv, valid, a.err, &sh.flag)) return;
     }
   } else {
@@ -822,12 +804,12 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       // t_i = sum_j W_ij p_j (my rows)
       wsum(true, be, cp, al + r_lo);
       ++phase;
-      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, lout[i - r_lo], salt | phase);
+      for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, lout[i - r_lo], salt | phase, local);
       if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) return;
       // s_j = sum_i W_ij t_i (my cols)
       wsum(false, al, ct, be + r_lo);
       ++phase;
-      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase);
+      for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase, local);
       if (!gather_vector(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag)) return;
       // CG update, identical in every member (utils/cg.py:70-92 with x0 = 0)
       const float pAp = block_sum(Np, [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red, flip);

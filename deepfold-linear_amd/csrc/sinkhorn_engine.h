@@ -178,6 +178,78 @@ __device__ __forceinline__ int mask_setup(const float* mask, int N, unsigned cha
   return n;
 }
 
+// Polls this thread's words i = base + t + k * stride, k < W, of [0, n) until each
+// carries `tag`, calling take(k, word) once per word.  Every word has two loads in
+// flight, issued one sleep unit apart and checked alternately, so a load that still
+// saw the old word costs that stagger rather than a whole round trip (an exchange
+// round of a 16-member group measured 1826 instead of 2285 clocks on MI355X).
+// The loads are unconditional (words past n read word 0 and are ignored), so
+// the compiler can wait for one set with the other still in flight.  Returns
+// false if the error flag is raised or the wait expires (then it raises it).
+template <int W, typename Take>
+__device__ __forceinline__ bool poll_batch(const uint64_t* buf, int base, int n, int stride, uint32_t tag, ErrRef err,
+                                           Take take) {
+  const uint32_t salt = tag >> 12;
+  const int t = threadIdx.x;
+  const uint64_t* addr[W];
+  bool done[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int i = base + t + k * stride;
+    done[k] = i >= n;
+    addr[k] = buf + (done[k] ? 0 : i);
+  }
+  auto all = [&]() {
+    bool r = true;
+#pragma unroll
+    for (int k = 0; k < W; ++k) r = r && done[k];
+    return r;
+  };
+  auto ld = [&](int k) {
+    return __hip_atomic_load(const_cast<uint64_t*>(addr[k]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  uint64_t wa[W], wb[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) wa[k] = ld(k);
+  __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+  for (int k = 0; k < W; ++k) wb[k] = ld(k);
+  uint32_t spins = 0;
+  while (true) {
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+      if (!done[k] && (uint32_t)wa[k] == tag) { take(k, wa[k]); done[k] = true; }
+    if (all()) return true;
+#pragma unroll
+    for (int k = 0; k < W; ++k) wa[k] = ld(k);
+    __builtin_amdgcn_s_sleep(1);  // back off: tight polling slows the publishers' stores
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+      if (!done[k] && (uint32_t)wb[k] == tag) { take(k, wb[k]); done[k] = true; }
+    if (all()) return true;
+#pragma unroll
+    for (int k = 0; k < W; ++k) wb[k] = ld(k);
+    __builtin_amdgcn_s_sleep(1);
+    // Only a scalar counter here: a vector load of the error word on some iterations
+    // would leave the compiler unable to count the loads in flight, and it would then
+    // wait for all of them.  A member that gave up stops publishing, so the others'
+    // waits expire too, within the spin limit (well under a second).
+    if (++spins > SPIN_LIMIT / 2) { raise_error(err, salt, 2u); return false; }
+  }
+}
+
+// All words [0, n) of a vector, NT threads, batches of W = 1, 2 or 4 words a
+// thread (the smallest that covers n, else repeated batches of 4).
+template <int NT, typename Take>
+__device__ __forceinline__ bool poll_vector(const uint64_t* buf, int n, uint32_t tag, ErrRef err, Take take) {
+  if (n <= NT) return poll_batch<1>(buf, 0, n, NT, tag, err, [&](int k, uint64_t w) { take(k * NT, w); });
+  if (n <= 2 * NT) return poll_batch<2>(buf, 0, n, NT, tag, err, [&](int k, uint64_t w) { take(k * NT, w); });
+  for (int base = 0; base < n; base += 4 * NT)
+    if (!poll_batch<4>(buf, base, n, NT, tag, err, [&](int k, uint64_t w) { take(base + k * NT, w); }))
+      return false;
+  return true;
+}
+
 // Gather a published potential vector [0, n) into dst (log2 units), writing
 // NEG_BIG for masked entries, and fold max |new - old| over valid entries into
 // *s_delta (float bits, >= 0; reset by the caller before a barrier that
@@ -188,47 +260,22 @@ __device__ __forceinline__ bool gather_potential(const uint64_t* buf, int n, uin
                                                  const unsigned char* valid, ErrRef err, int* s_flag,
                                                  unsigned* s_delta) {
   const int t = threadIdx.x;
-  const uint32_t salt = tag >> 12;
-  bool ok = true;
   float dmax = 0.f;
-  for (int base = 0; base < n && ok; base += 4 * NT) {
-    // words base + t + k*NT, k < cnt, owned by this thread
-    const int rem = n - base - t;
-    const int cnt = rem <= 0 ? 0 : min(4, (rem + NT - 1) / NT);
-    bool done[4] = {cnt <= 0, cnt <= 1, cnt <= 2, cnt <= 3};
-    uint32_t spins = 0;
-    while (!(done[0] && done[1] && done[2] && done[3])) {
-      uint64_t w[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (!done[k])
-          w[k] = __hip_atomic_load(const_cast<uint64_t*>(buf + base + t + k * NT), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (!done[k] && (uint32_t)w[k] == tag) {
-          const int i = base + t + k * NT;
-          if (valid[i]) {
-            const float nv = __uint_as_float((uint32_t)(w[k] >> 32)) * LOG2E;
-            dmax = fmaxf(dmax, fabsf(nv - dst[i]));
-            dst[i] = nv;
-          } else {
-            dst[i] = NEG_BIG;
-          }
-          done[k] = true;
-        }
-      }
-      if (!(done[0] && done[1] && done[2] && done[3])) {
-        __builtin_amdgcn_s_sleep(1);  // back off: tight polling slows the publishers' stores
-        if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); ok = false; break; }
-        if ((spins & 255u) == 0u && error_raised(err, salt)) { ok = false; break; }
-      }
+  // take(off, w): word i = off + t
+  const bool ok = poll_vector<NT>(buf, n, tag, err, [&](int off, uint64_t w) {
+    const int i = off + t;
+    if (valid[i]) {
+      const float nv = __uint_as_float((uint32_t)(w >> 32)) * LOG2E;
+      dmax = fmaxf(dmax, fabsf(nv - dst[i]));
+      dst[i] = nv;
+    } else {
+      dst[i] = NEG_BIG;
     }
-  }
+  });
   if (!ok) *s_flag = 1;
   // NaN-safe: a NaN delta forces the online path
   block_atomic_max_u32(s_delta, dmax == dmax ? __float_as_uint(dmax) : 0x7f800000u);
-  __syncthreads();
+  lds_barrier();  // dst, the flag and the change word are LDS
   return *s_flag == 0;
 }
 
@@ -376,6 +423,199 @@ __device__ __forceinline__ void lse_sweep(const T* __restrict__ res_lds, const T
 struct NoPublish {
   __device__ __forceinline__ void operator()(int, float) const {}
 };
+
+// ---------------------------------------------------------------------------
+// Fixed-shift LSE sweep of resident storage, the sweep of every Sinkhorn
+// half-iteration after the first.  Same result as lse_sweep<..., ONLINE = false>
+// (lse2[q] = shift2[q] + log2 sum_j exp2(x_qj - shift2[q]), in place), organised
+// for issue rate:
+//  * NR resident tiles per call, known at compile time; their fragments and
+//    shifts are loaded once;
+//  * a wave's streamed tiles st = wave + NW k are read from one base address at
+//    compile-time offsets, SCH per group; slots past the last tile read padding
+//    rows (zero operands) whose column term is NEG_BIG, so no slot is tested
+//    (the caller pads res/str to lean_rows() rows and w2 with NEG_BIG);
+//  * all MFMAs of a group are issued before the exponentials, and each resident
+//    tile's 4 * SCH exponentials are summed as a tree.
+// A sweep-only microbenchmark at the headline member shape (3 resident tiles
+// against 48 streamed tiles, bf16, d = 32) measured 1.80 us against 2.34 us for
+// lse_sweep, and 0.96 against 1.72 us at 2 against 32.
+template <typename T, int DP> constexpr int lean_sch() {
+  return (sizeof(T) == 2 && DP == 32) ? 6 : ((sizeof(T) == 4 && DP == 64) ? 2 : 4);
+}
+// Rows of a resident Q / K array (and entries of a potential vector) that the
+// lean sweep may read: Np rounded up to whole groups of NW * SCH streamed tiles.
+template <int NT> __host__ __device__ inline int lean_rows(int Np, int sch) {
+  const int unit = (NT / WAVE) * sch * 16;
+  return ((Np + unit - 1) / unit) * unit;
+}
+
+template <int N>
+__device__ __forceinline__ float tree_sum(float (&v)[N]) {
+#pragma unroll
+  for (int w = 1; w < N; w *= 2)
+#pragma unroll
+    for (int i = 0; i + w < N; i += 2 * w) v[i] += v[i + w];
+  return v[0];
+}
+
+// One chunk of NR resident tiles (absolute tiles rt0 .. rt0 + NR - 1, local rows
+// q0 .. q0 + 16 NR - 1) against `groups` groups of SCH streamed slots per wave.
+template <int NT, typename T, int DP, int NR, int SCH, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void lean_chunk(const T* __restrict__ res, const T* __restrict__ str,
+                                           const float* __restrict__ w2, int groups, int rt0, int q0, float sc,
+                                           const Bias& bias, float* lse, float* scratch, unsigned* s_reset,
+                                           Pub publish) {
+  using M = Mfma<T, DP>;
+  using Frag = typename M::Frag;
+  constexpr int NW = NT / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int g = lane >> 4;
+  const float isc = 1.f / sc;
+  Frag bf[NR];
+  f32x4 ci[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    M::load(bf[r], res + (size_t)((rt0 + r) * 16 + (lane & 15)) * DP, lane);
+    const float c = -lse[q0 + r * 16 + (lane & 15)] * isc;
+    ci[r] = f32x4{c, c, c, c};
+  }
+  float s[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) s[r] = 0.f;
+  const T* sb = str + (size_t)(wave * 16 + (lane & 15)) * DP;
+  const float* wb = w2 + wave * 16 + 4 * g;
+  for (int kg = 0; kg < groups; ++kg) {
+    Frag af[SCH];
+    f32x4 w[SCH];
+#pragma unroll
+    for (int k = 0; k < SCH; ++k) {
+      M::load(af[k], sb + (size_t)(kg * SCH + k) * NW * 16 * DP, lane);
+      w[k] = *reinterpret_cast<const f32x4*>(wb + (kg * SCH + k) * NW * 16);
+    }
+    f32x4 x[NR][SCH];
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int k = 0; k < SCH; ++k) x[r][k] = M::qk(af[k], bf[r], ci[r]);  // independent MFMAs
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      f32x4 bv[SCH];
+      if (GENERAL) {
+        // padding slots index past the last tile: clamp inside the padded arrays
+        // (their w is NEG_BIG, so the bias value is irrelevant)
+        int s0[SCH];
+#pragma unroll
+        for (int k = 0; k < SCH; ++k) s0[k] = min((wave + NW * (kg * SCH + k)) * 16 + 4 * g, bias.Np - 4);
+        bias.template quads<TRANS>((rt0 + r) * 16 + (lane & 15), s0, bv);
+      }
+      float e[4 * SCH];
+#pragma unroll
+      for (int k = 0; k < SCH; ++k)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float xv = __builtin_fmaf(x[r][k][q], sc, w[k][q]);
+          e[4 * k + q] = fast_exp2(GENERAL ? xv + bv[k][q] : xv);
+        }
+      s[r] += tree_sum(e);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float ss = sum_groups(s[r]);
+    if (lane < 16) scratch[(wave * NR + r) * 16 + lane] = ss;
+  }
+  // the change word of the coming gather is cleared before the barrier, so no
+  // wave's post-barrier atomic can precede the clear
+  if (s_reset && threadIdx.x == 0) *s_reset = 0u;
+  lds_barrier();
+  if ((int)threadIdx.x < NR * 16) {
+    const int q = threadIdx.x, r = q >> 4, l = q & 15;
+    float ss = 0.f;
+#pragma unroll
+    for (int w_ = 0; w_ < NW; ++w_) ss += scratch[(w_ * NR + r) * 16 + l];
+    const float v = lse[q0 + q] + fast_log2(ss);
+    lse[q0 + q] = v;
+    publish(q0 + q, v);
+  }
+  // the published words complete on their own: the coming gather polls them
+  lds_barrier();
+}
+
+// Chunks of at most 4 resident tiles (2 with a bias: its per-element values would
+// not fit in registers beside 4 tiles' accumulators).
+template <int NT, typename T, int DP, int SCH, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void lean_chunks(const T* res, const T* str, const float* w2, int groups, int t0, int nr,
+                                            float sc, const Bias& bias, float* lse, float* scratch,
+                                            unsigned* s_reset, Pub publish) {
+  constexpr int CMAX = GENERAL ? 2 : 4;
+  for (int c0 = 0; c0 < nr; c0 += CMAX) {
+    const int nc = min(CMAX, nr - c0);
+    if (CMAX == 4 && nc == 4)
+      lean_chunk<NT, T, DP, CMAX, SCH, GENERAL, TRANS>(res, str, w2, groups, t0 + c0, c0 * 16, sc, bias, lse, scratch,
+                                                    s_reset, publish);
+    else if (CMAX == 4 && nc == 3)
+      lean_chunk<NT, T, DP, CMAX - 1, SCH, GENERAL, TRANS>(res, str, w2, groups, t0 + c0, c0 * 16, sc, bias, lse, scratch,
+                                                    s_reset, publish);
+    else if (nc == 2)
+      lean_chunk<NT, T, DP, 2, SCH, GENERAL, TRANS>(res, str, w2, groups, t0 + c0, c0 * 16, sc, bias, lse, scratch,
+                                                    s_reset, publish);
+    else
+      lean_chunk<NT, T, DP, 1, SCH, GENERAL, TRANS>(res, str, w2, groups, t0 + c0, c0 * 16, sc, bias, lse, scratch,
+                                                    s_reset, publish);
+  }
+}
+
+// Resident fixed-shift sweep over n_str_tiles streamed tiles for resident tiles
+// [t0, t0 + nr): lse (local rows) holds the shift on entry and the result on exit.
+// For (bf16, DP 32) a wave with at most 4 streamed tiles takes groups of 4 slots,
+// else of 6.  res, str and w2 must hold lean_rows<NT>(Np, lean_sch<T, DP>()) rows.
+template <int NT, typename T, int DP, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void lean_sweep(const T* res, const T* str, const float* w2, int n_str_tiles, int t0,
+                                           int nr, float sc, const Bias& bias, float* lse, float* scratch,
+                                           unsigned* s_reset, Pub publish) {
+  constexpr int NW = NT / WAVE;
+  constexpr int SMAX = lean_sch<T, DP>();
+  const int ks = (n_str_tiles + NW - 1) / NW;  // streamed tiles of the busiest wave
+  if (SMAX == 6 && ks <= 4)
+    lean_chunks<NT, T, DP, 4, GENERAL, TRANS>(res, str, w2, 1, t0, nr, sc, bias, lse, scratch, s_reset, publish);
+  else
+    lean_chunks<NT, T, DP, SMAX, GENERAL, TRANS>(res, str, w2, (ks + SMAX - 1) / SMAX, t0, nr, sc, bias, lse,
+                                                 scratch, s_reset, publish);
+}
+
+// Exchange-placement agreement of a group.  At the start of a launch every member
+// publishes whether it runs on its expected XCD (publish_placement); after the
+// launch's first gather, by when every member has published, each member reads
+// the G words (read_placement): plain-store publishing (xch_put_local) is used
+// only if all members are placed.  The answer is uniform over the block and
+// identical in every member.  Returns false (uniformly) if a wait expires.
+__device__ __forceinline__ void publish_placement(uint64_t* pw, int member, uint32_t salt) {
+  if (threadIdx.x == 0) xch_put(pw + member, xcc_placed() ? 1.f : 0.f, salt << 12);
+}
+// Members that own no tiles (stripe empty: n_tiles < G) return before publishing
+// and are skipped.
+__device__ __forceinline__ bool read_placement(const uint64_t* pw, int G, int n_tiles, uint32_t salt, ErrRef err,
+                                               int* s_flag, int* s_local) {
+  const uint32_t tag = salt << 12;
+  const int t = threadIdx.x;
+  if (t < G && (long long)n_tiles * (t + 1) / G > (long long)n_tiles * t / G) {
+    uint32_t spins = 0;
+    while (true) {
+      const uint64_t w = __hip_atomic_load(const_cast<uint64_t*>(pw + t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((uint32_t)w == tag) {
+        if (__uint_as_float((uint32_t)(w >> 32)) != 1.f) *s_local = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); *s_flag = 1; break; }
+      if ((spins & 255u) == 0u && error_raised(err, salt)) { *s_flag = 1; break; }
+    }
+  }
+  __syncthreads();
+  return *s_flag == 0;
+}
 
 // Workgroup -> (group, member).  Workgroups are dispatched round-robin over the
 // 8 XCDs (id % 8), so the members of one group are taken from a single XCD:

@@ -161,7 +161,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   constexpr bool BAL = MODE == FWD_BALANCED;
   constexpr bool HIST = MODE != FWD_UOT;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_flag, s_tmp;
+  __shared__ int s_flag, s_tmp, s_local;
   __shared__ unsigned s_du, s_dv;
   __shared__ int s_cnt;
   __shared__ float s_posw[BIN_NONE + 1];
@@ -172,20 +172,23 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const int Np = ((N + 31) / 32) * 32;
   constexpr bool bal = BAL;
   const bool has_v = !BAL || (a.v != nullptr && a.o_avg != nullptr);  // UOT mode always has V
-  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; s_cnt = 0; }
+  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; s_cnt = 0; s_local = 1; }
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(a.err.ws + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- LDS carve-up (must match sinkhorn_fwd_lds_bytes)
   const int loc = fwd_local_rows(N, a.G);
-  const int q_rows = STREAM ? loc : Np;
-  const int k_rows = STREAM ? fwd_kregion_rows(N, a.G) : Np;
+  // resident: Q, K and the potentials padded to the lean sweep's row groups
+  // (zero operands, NEG_BIG potentials past the valid tokens)
+  const int rcap = STREAM ? Np : lean_rows<FWD_NT>(Np, lean_sch<T, DP>());
+  const int q_rows = STREAM ? loc : rcap;
+  const int k_rows = STREAM ? fwd_kregion_rows(N, a.G) : rcap;
   unsigned char* valid = smem;
   T* QS = reinterpret_cast<T*>(smem + ((Np + 15) / 16) * 16);     // resident: all rows; stream: my stripe
   T* KS = QS + (size_t)q_rows * DP;
   float* vecU = reinterpret_cast<float*>(KS + (size_t)k_rows * DP);  // u of all rows (log2)
-  float* vecV = vecU + Np;                                          // v of all columns (log2)
-  float* xs = vecV + Np;                                            // resident only: [Np][3]
+  float* vecV = vecU + rcap;                                        // v of all columns (log2)
+  float* xs = vecV + rcap;                                          // resident only: [Np][3]
   float* lse_r = xs + (STREAM ? 0 : 3 * Np);  // row LSE of my rows (log2); shift of the next row sweep
   float* lse_c = lse_r + loc;   // column LSE of my columns (log2)
   float* mx2 = lse_c + loc;     // row maxima of the final sweep
@@ -233,8 +236,8 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     stage_rows<T, DP>(QS, Qp + (size_t)r_lo * DP, DP, nr * 16, DP, loc);
     stage_rows<T, DP>(KS, Kp + (size_t)r_lo * DP, DP, nr * 16, DP, loc);
   } else {
-    stage_rows<T, DP>(QS, Qg, a.sn, n, d, Np);
-    stage_rows<T, DP>(KS, Kg, a.sn, n, d, Np);
+    stage_rows<T, DP>(QS, Qg, a.sn, n, d, rcap);
+    stage_rows<T, DP>(KS, Kg, a.sn, n, d, rcap);
   }
 
   const float eps = a.eps[h];
@@ -254,7 +257,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     lmu_l[q] = i < n ? (bal ? lmarg : a.log_mu[bh * N + i]) : 0.f;
     lnu_l[q] = i < n ? (bal ? lmarg : a.log_nu[bh * N + i]) : 0.f;
   }
-  for (int i = threadIdx.x; i < Np; i += FWD_NT) {
+  for (int i = threadIdx.x; i < rcap; i += FWD_NT) {
     const bool ok = i < n && valid[i];
     vecU[i] = ok ? (a.u_init ? a.u_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
     vecV[i] = ok ? (a.v_init ? a.v_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
@@ -301,12 +304,20 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       const T* res = row ? QS : KS;
       const T* str = row ? KS : QS;
       const float* w2 = row ? vecV : vecU;
-      if (row) {
-        if (general) fwd_sweep<T, DP, true, false>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
-        else fwd_sweep<T, DP, false, false>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+      if (!online) {
+        if (row) {
+          if (general) lean_sweep<FWD_NT, T, DP, true, false>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, scratch, s_reset, pub);
+          else lean_sweep<FWD_NT, T, DP, false, false>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, scratch, s_reset, pub);
+        } else {
+          if (general) lean_sweep<FWD_NT, T, DP, true, true>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, scratch, s_reset, pub);
+          else lean_sweep<FWD_NT, T, DP, false, true>(res, str, w2, n_tiles, t0, nr, sc, bias, lse, scratch, s_reset, pub);
+        }
+      } else if (row) {
+        if (general) fwd_sweep<T, DP, true, false>(true, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+        else fwd_sweep<T, DP, false, false>(true, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
       } else {
-        if (general) fwd_sweep<T, DP, true, true>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
-        else fwd_sweep<T, DP, false, true>(online, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+        if (general) fwd_sweep<T, DP, true, true>(true, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
+        else fwd_sweep<T, DP, false, true>(true, res, str, w2, n_tiles, t0, nr, sc, bias, lse, mx, scratch, s_reset, pub);
       }
     }
   };
@@ -315,6 +326,17 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   uint64_t* xv = xu + Np;                       // v words
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
+  // placement words of the group (after all (b,h)'s u/v words); plain-store
+  // publishing from the second exchange on if every member is on its XCD
+  uint64_t* xpl = a.xch + (size_t)a.B * a.H * 2 * Np + bh * 32;
+  publish_placement(xpl, member, a.salt);
+  bool local = false;
+  auto agree_placement = [&]() __attribute__((always_inline)) -> bool {
+    if (phase != 1) return true;
+    if (!read_placement(xpl, a.G, n_tiles, a.salt, a.err, &s_flag, &s_local)) return false;
+    local = s_local != 0;
+    return true;
+  };
 
   // History for the unrolled backward: this member's stripe of the vector just
   // exchanged, copied from its own words (exact published values), outside the sweep.
@@ -336,10 +358,11 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       const bool online = it == 0 || __uint_as_float(s_dv) > FIXED_SHIFT_MAX_DELTA;
       auto pub = [&](int q, float l2) {
         const int i = r_lo + q;
-        if (i < n) xch_put(xu + i, kappa * (lmu_l[q] - l2 * LN2), tag);
+        if (i < n) xch_put(xu + i, kappa * (lmu_l[q] - l2 * LN2), tag, local);
       };
       sweep(true, online, lse_r, nullptr, &s_du, pub);
       if (!gather_potential<FWD_NT>(xu, n, tag, vecU, valid, a.err, &s_flag, &s_du)) return false;
+      if (!agree_placement()) return false;
       if constexpr (HIST) record(xu, 2 * it + 1);
     }
     return true;
@@ -354,12 +377,13 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       auto pub = [&](int q, float l2) {
         const int j = r_lo + q;
         if (j < n) {
-          xch_put(xv + j, kappa * (lnu_l[q] - l2 * LN2), tag);
+          xch_put(xv + j, kappa * (lnu_l[q] - l2 * LN2), tag, local);
           if (!BAL && last && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
         }
       };
       sweep(false, online, lse_c, nullptr, &s_dv, pub);
       if (!gather_potential<FWD_NT>(xv, n, tag, vecV, valid, a.err, &s_flag, &s_dv)) return false;
+      if (!agree_placement()) return false;
       if constexpr (HIST) record(xv, 2 * it);
     }
     return true;
@@ -547,8 +571,10 @@ inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stre
     bytes += 5 * loc * 4;                                  // lse_r, lse_c, mx2, lmu_l, lnu_l
     bytes += (size_t)stream_scratch<FWD_NT>() * 4;
   } else {
-    bytes += 2 * Np * DP * elem;          // QS, KS
-    bytes += (2 * Np + 3 * Np) * 4;       // vecU, vecV, xs
+    const int sch = (elem == 2 && DP == 32) ? 6 : ((elem == 4 && DP == 64) ? 2 : 4);  // lean_sch<T, DP>()
+    const size_t rcap = lean_rows<FWD_NT>((int)Np, sch);
+    bytes += 2 * rcap * DP * elem;        // QS, KS (padded to the lean sweep's row groups)
+    bytes += (2 * rcap + 3 * Np) * 4;     // vecU, vecV, xs
     bytes += 5 * loc * 4;                 // lse_r, lse_c, mx2, lmu_l, lnu_l
     bytes += (size_t)sweep_scratch<FWD_NT>() * 4;
   }

@@ -121,8 +121,8 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
  * params, outputs and kernels as dfl_sinkhorn_fwd, resident storage only (AUTO or
  * RESIDENT; a problem that needs stream storage is rejected).  Instead of a
  * workspace it uses a static device array of DFL_NOALLOC_SCRATCH_BYTES per GPU,
- * held until the process ends: it needs 256 + 16*B*H*Np bytes (+ 2*B*Np*Np with
- * pos_bins), Np = N rounded up to 32, and rejects larger problems.  Every call on
+ * held until the process ends: it needs 256 + 16*B*H*(Np + 16) bytes (+ 2*B*Np*Np
+ * with pos_bins), Np = N rounded up to 32, and rejects larger problems.  Every call on
  * one GPU shares that array, so calls that overlap in time on one GPU race.  It
  * calls no hipMalloc / hipFree and no allocating library routine. */
 #define DFL_NOALLOC_SCRATCH_BYTES (8u << 20)

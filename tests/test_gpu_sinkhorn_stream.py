@@ -141,7 +141,11 @@ def test_stream_equals_resident():
     gs = run_gpu_bwd(inp, 12, torch.bfloat16, go, gxc, storage="stream", **kw)
     for k in GRADS:
         if k in gr:
-            assert max_rel_err(gs[k], gr[k]) <= 1e-4, k
+            # Q, K, V, G gradients are returned in bf16: the two modes' fp32 sums differ in
+            # order (~1e-7 relative), which can flip a final bf16 rounding, i.e. one bf16 ulp
+            # (2^-8 of the value) on an element; the fp32 gradients are held to 1e-4.
+            tol = 2.0 ** -8 if k in ("Q", "K", "V", "G") else 1e-4
+            assert max_rel_err(gs[k], gr[k]) <= tol, k
 
 
 def test_baseline_config5_full_size():
