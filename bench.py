@@ -37,8 +37,11 @@ sys.path.insert(0, os.path.join(ROOT, "deepfold-linear_amd"))
 # MI355X published peaks (dense): bf16 MFMA 2.5 PFLOP/s, HBM 8 TB/s.
 PEAK_MFMA_BF16 = 2.5e15
 PEAK_HBM = 8.0e12
-# v_exp_f32 issue rate (quarter rate of fp32 FMA) used for the exp roof.
-PEAK_EXP_NOMINAL = 9.8e12
+# Measured on MI355X by `bench.py --workload peaks` (csrc/peaks.hip, two waves per
+# SIMD on all 256 CUs): v_exp_f32 issue rate, and the rate of the fixed-shift sweep's
+# element (fma + exp2 + add), which does not overlap on gfx950.
+PEAK_EXP_MEASURED = 15.5e12
+PEAK_SWEEP_ELEMENT_MEASURED = 9.54e12
 PEAK_MFMA_F32 = 157.3e12
 
 SINKHORN = {
@@ -418,7 +421,7 @@ def bench_sinkhorn(args, name):
     achieved = f_dom / (avg[dom] * 1e-3)
     traffic = profiled_traffic(dom, "sinkhorn_cfg2_bench.md" if name == "cfg2" else f"sinkhorn_{name}_bench.md")
     peak = PEAK_MFMA_BF16  # bf16 inputs: both backwards run their products on the bf16 MFMA
-    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
+    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_SWEEP_ELEMENT_MEASURED)
     metric = ("flash-Sinkhorn fwd+IFT-bwd ms/layer @B2,H8,N768,d32 bf16; % of MFMA/HBM roof" if name == "cfg2"
               else f"flash-Sinkhorn fwd+{'unrolled' if cfg.get('unrolled') else 'IFT'}-bwd ms/layer "
                    f"@B{cfg['B']},H{cfg['H']},N{cfg['N']},d{cfg['d']} bf16")
@@ -444,8 +447,10 @@ def bench_sinkhorn(args, name):
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
                      "peak": peak / 1e12, "unit": "TFLOP/s", "frac": round(achieved / peak, 5),
                      "traffic": traffic},
-        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_NOMINAL,
-                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
+        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_MEASURED,
+                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_MEASURED,
+                         "element_peak": PEAK_SWEEP_ELEMENT_MEASURED,
+                         "element_frac": x_dom / (avg[dom] * 1e-3) / PEAK_SWEEP_ELEMENT_MEASURED,
                          "layer_t_roof_ms": t_roof * 1e3, "layer_frac": t_roof * 1e3 / ms_per_step},
     }
     out["kernel_errors"] = 0  # check_errors passed after the timed steps
@@ -669,7 +674,7 @@ def bench_balanced(args):
     f_dom = f_fwd if dom == "balanced_fwd" else f_bwd
     x_dom = x_fwd if dom == "balanced_fwd" else x_bwd
     achieved = f_dom / (avg[dom] * 1e-3)
-    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_F32, (x_fwd + x_bwd) / PEAK_EXP_NOMINAL)
+    t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_F32, (x_fwd + x_bwd) / PEAK_SWEEP_ELEMENT_MEASURED)
     out = {
         "metric": "balanced Sinkhorn transport (dual) fwd+bwd ms/step @B1,H16,N256,d32 fp32 K20",
         "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -682,8 +687,8 @@ def bench_balanced(args):
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
                      "peak": PEAK_MFMA_F32 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_F32, 5),
                      "traffic": profiled_traffic(dom, "balanced_tokenot_bench.md")},
-        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_NOMINAL,
-                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_NOMINAL,
+        "roofline_exp": {"kernel": dom, "achieved": x_dom / (avg[dom] * 1e-3), "peak": PEAK_EXP_MEASURED,
+                         "unit": "exp/s", "frac": x_dom / (avg[dom] * 1e-3) / PEAK_EXP_MEASURED,
                          "step_t_roof_ms": t_roof * 1e3, "step_frac": t_roof * 1e3 / ms},
     }
     if not args.no_cpu_baseline:
@@ -854,6 +859,49 @@ def tokenot_cpu_baseline(blk, h0, x0, mask, gh, gx, K):
                       "autograd, float32, one full step, median of 3"}
 
 
+def bench_peaks():
+    """Measured issue rates of the instructions the Sinkhorn sweeps are made of, and
+    the exchange round of a 16-member group (csrc/peaks.hip), one JSON line each.
+    Every probe runs one 512-thread workgroup per CU (two waves per SIMD, as the
+    Sinkhorn kernels do) on all 256 CUs; rates come from HIP events around the launch,
+    `clk_per_wave_op` from clock64() (per SIMD, both waves' instructions counted)."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "deepfold-linear_amd", "deepfold_amd", "libdfl_peaks.so"))
+    run = lib.dfl_peak_run
+    run.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_float),
+                    ctypes.POINTER(ctypes.c_longlong)]
+    run.restype = ctypes.c_int
+    blocks, lanes = 256, 512
+
+    def probe(mode, iters):
+        ms, clk = ctypes.c_float(), ctypes.c_longlong()
+        for _ in range(2):  # the first launch loads the code object
+            rc = run(mode, blocks, iters, ctypes.byref(ms), ctypes.byref(clk))
+            if rc:
+                raise SystemExit(f"peaks: probe {mode} failed with code {rc}")
+        return ms.value * 1e-3, clk.value
+
+    rows = [(0, 100000, "v_exp_f32 (exp2) issue rate", "exp/s", 24, 1.0),
+            (1, 100000, "v_fma_f32 issue rate", "FLOP/s", 24, 2.0),
+            (3, 50000, "fixed-shift sweep element: s += exp2(x * a + w) (fma + exp + add)", "elements/s", 24, 1.0)]
+    for mode, iters, what, unit, per, scale in rows:
+        t, clk = probe(mode, iters)
+        n = blocks * lanes * iters * per
+        print(json.dumps({"probe": what, "value": n * scale / t, "unit": unit, "ms": t * 1e3,
+                          "clk_per_wave_op": clk / (iters * per * 2)}), flush=True)
+    t, clk = probe(2, 200000)
+    flops = blocks * 8 * 200000 * 6 * 16 * 16 * 32 * 2
+    print(json.dumps({"probe": "v_mfma_f32_16x16x32_bf16, 6 independent accumulators per wave", "value": flops / t,
+                      "unit": "FLOP/s", "ms": t * 1e3, "frac_of_published": flops / t / PEAK_MFMA_BF16,
+                      "clk_per_wave_op": clk / (200000 * 6 * 2)}), flush=True)
+    rounds = 2000
+    t, clk = probe(4, rounds)
+    print(json.dumps({"probe": "exchange round: 16 workgroups on one XCD each publish 48 tagged words and poll "
+                               "the group's 768 (16 groups)", "value": t * 1e6 / rounds, "unit": "us/round",
+                      "clk_per_round": clk / rounds}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -861,9 +909,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="cfg2",
-                    choices=["cfg2", "cfg5", "cfg2-full", "cfg2-unrolled", "cfg3", "cfg4", "balanced", "tokenot-step"],
+                    choices=["cfg2", "cfg5", "cfg2-full", "cfg2-unrolled", "cfg3", "cfg4", "balanced", "tokenot-step",
+                             "peaks"],
                     help="cfg2 (default): the headline flash-Sinkhorn layer; cfg5: the N=4096 layer; "
-                         "cfg3 / cfg4: attention rows")
+                         "cfg3 / cfg4: attention rows; peaks: the issue-rate and exchange probes "
+                         "(libdfl_peaks.so) behind the roofline figures")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB -> 256 MiB elementwise copy (torch.neg), used to "
                          "calibrate the FETCH_SIZE / WRITE_SIZE counters")
@@ -893,7 +943,9 @@ def main():
         print(json.dumps({"calibrate_copy": {"kernel": "torch.neg", "launches": 5, "read_bytes": 4 * n,
                                              "write_bytes": 4 * n}}), flush=True)
         return
-    if args.workload in SINKHORN:
+    if args.workload == "peaks":
+        bench_peaks()
+    elif args.workload in SINKHORN:
         bench_sinkhorn(args, args.workload)
     elif args.workload == "balanced":
         bench_balanced(args)

@@ -1,4 +1,4 @@
-"""Build libdfl_amd.so in-tree with hipcc for gfx950.
+"""Build libdfl_amd.so (and the probe library libdfl_peaks.so) in-tree with hipcc for gfx950.
 
 Every source compiles to its own object in parallel, then one link step.
 
@@ -19,6 +19,9 @@ SOURCES = ["capi.hip", "sinkhorn_fwd.hip", "sinkhorn_fwd_stream.hip", "sinkhorn_
            "sinkhorn_bwd_stream.hip", "attention.hip", "dense.hip", "balanced_bwd.hip",
            "unrolled_bwd.hip", "trunk_steps.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# issue-rate / exchange probes (bench.py --workload peaks only): a library of its own
+PROBE_SOURCE = "peaks.hip"
+PROBE_OUT = os.path.join(HERE, "deepfold_amd", "libdfl_peaks.so")
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -40,8 +43,13 @@ def build(verbose: bool = True) -> str:
         if verbose:
             print("[build]", " ".join(cmd), flush=True)
         jobs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    probe_obj = os.path.join(OBJ_DIR, "peaks.o")
+    probe_cmd = [HIPCC, *FLAGS, "-c", "-o", probe_obj, os.path.join(CSRC, PROBE_SOURCE)]
+    if verbose:
+        print("[build]", " ".join(probe_cmd), flush=True)
+    probe = subprocess.Popen(probe_cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     errors = []
-    for src, _, proc in jobs:
+    for src, _, proc in jobs + [(PROBE_SOURCE, probe_obj, probe)]:
         out, _ = proc.communicate()
         out = _clean(out)
         if proc.returncode != 0:
@@ -58,6 +66,14 @@ def build(verbose: bool = True) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed ({proc.returncode}):\n{_clean(proc.stdout + proc.stderr)}")
     os.replace(tmp, OUT)
+    tmp = PROBE_OUT + ".tmp"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, probe_obj]
+    if verbose:
+        print("[build]", " ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"probe link failed ({proc.returncode}):\n{_clean(proc.stdout + proc.stderr)}")
+    os.replace(tmp, PROBE_OUT)
     return OUT
 
 

@@ -5,6 +5,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -92,6 +93,33 @@ int hip_fail(hipError_t e, const char* what) {
 // header are cleared (fill kernel, on the call's stream) at its first use in each
 // new epoch.  A workspace never seen before is taken as zero-filled, as the ABI
 // requires of a new workspace.
+int cu_count();
+
+// Launch mode of the persistent kernels, whose group members wait on each other and
+// so must all be resident at once.  A grid of at most one workgroup per CU
+// (dfl::grid_blocks(n_groups, G) <= CU count, which group_size() arranges) is
+// launched as an ordinary launch: on an otherwise idle device every workgroup is
+// resident at once, and a member kept waiting by other work on the device shows up
+// as an expired wait (error 2), not a hang.  A cooperative launch also guarantees
+// residency against concurrent kernels on other streams, at about 12-16 us more per
+// launch on MI355X (measured: cfg2 layer 0.602 vs 0.572 ms).  DFL_AMD_COOP=1 forces
+// cooperative launches (callers that run other kernels concurrently), DFL_AMD_COOP=0
+// forces ordinary ones; grids larger than the CU count are always cooperative (the
+// runtime then checks that they fit).  rocprofv3 ends with SIGSEGV in its exit-time
+// teardown after any cooperative launch, even of a trivial kernel, so the committed
+// profiles use DFL_AMD_COOP=0.
+bool coop_launch(int G, int n_groups) {
+  static const int mode = [] {
+    const char* v = std::getenv("DFL_AMD_COOP");
+    if (v && v[0] == '1' && v[1] == 0) return 1;
+    if (v && v[0] == '0' && v[1] == 0) return 0;
+    return -1;
+  }();
+  if (G <= 1 || mode == 0) return false;
+  if (mode == 1) return true;
+  return dfl::grid_blocks(n_groups, G) > cu_count();
+}
+
 std::atomic<uint64_t> g_salt_counter{1};
 std::mutex g_ws_mu;
 struct WsState {
@@ -434,7 +462,7 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
     return hip_fail((hipError_t)rc, "workspace clear launch");
   if (a.bins)
     if (int rc = prepare_bins8(a.bins, a.B, a.N, workspace, w.bins_off, &a.bins8, &a.bins8t, stream)) return rc;
-  const bool coop = G > 1;  // members wait on each other: all must be co-resident
+  const bool coop = coop_launch(G, a.B * a.H);
   hipError_t e;
   if (stream_mode) {
     const StreamPtrs sp = stream_ptrs(workspace, a.B, a.H, a.N, G);
@@ -686,7 +714,7 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
     if (int rc = prepare_bins8(p->pos_bins, p->B, p->N, workspace, sinkhorn_bins8_offset(p->B, p->H, p->N),
                                &a.bins8, &a.bins8t, stream))
       return rc;
-  const bool coop = G > 1;
+  const bool coop = coop_launch(G, a.B * a.H);
   hipError_t e = dfl::launch_sinkhorn_bwd_prep(a, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward prep launch");
   if (stream_mode) {
@@ -997,7 +1025,7 @@ int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t w
   a.G = G;
   if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
     return hip_fail((hipError_t)rc, "workspace clear launch");
-  e = dfl::launch_balanced_bwd(a, DP, lds, (hipStream_t)stream, G > 1);
+  e = dfl::launch_balanced_bwd(a, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H));
   if (e != hipSuccess) return hip_fail(e, "balanced backward launch");
   e = dfl::launch_balanced_finalize(a, p->dx_res, p->dalpha_h, p->dr_h, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "balanced backward finalize launch");
@@ -1068,7 +1096,7 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
   a.G = G;
   if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
     return hip_fail((hipError_t)rc, "workspace clear launch");
-  e = dfl::launch_unrolled_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, G > 1);
+  e = dfl::launch_unrolled_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H));
   if (e != hipSuccess) return hip_fail(e, "unrolled backward launch");
   e = dfl::launch_unrolled_finalize(a, p->x_res ? p->dx_res : nullptr, p->dpos_weight, p->dw_dist,
                                     (hipStream_t)stream);

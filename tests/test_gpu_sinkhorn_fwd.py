@@ -135,6 +135,12 @@ def test_forward_masked_equals_unpadded(dtype, tol):
                 assert np.all(gv[b, :, n:] == 0)
 
 
+def geometry_rounded(z):
+    """A fixture whose reference distances came from torch.cdist's matmul path (N > 25
+    with a geometry term), which rounds them."""
+    return float(np.max(np.abs(z["w_dist"]))) > 0 and z["Q"].shape[2] > 25
+
+
 def test_forward_golden_vectors():
     """The reference's own outputs (tests/golden/make_golden.py) at fp32."""
     import glob
@@ -148,9 +154,11 @@ def test_forward_golden_vectors():
         inp = {k: torch.from_numpy(z[k]) for k in ("Q", "K", "V", "G", "x_res", "pos_weight", "pos_bins",
                                                    "eps", "w_dist", "log_mu", "log_nu")}
         got = run_gpu(inp, int(z["K_iter"]), torch.float32)
-        # torch.cdist's matmul path (N > 25) rounds the reference's distances; 3e-4 covers it
+        # fp32 bar 1e-4, except where the reference's distances went through torch.cdist's
+        # matmul path (geometry on and N > 25), which rounds them: 3e-4 covers that
+        tol = 3e-4 if geometry_rounded(z) else 1e-4
         for name, gv in zip(("o_flat", "x_centroid", "log_u", "log_v"), got):
-            assert_close_rel(gv, z[name], 3e-4, f"{os.path.basename(f)}:{name}")
+            assert_close_rel(gv, z[name], tol, f"{os.path.basename(f)}:{name}")
 
 
 def test_unbatched_matches_batched():
