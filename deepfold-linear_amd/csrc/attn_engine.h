@@ -202,17 +202,27 @@ __device__ __forceinline__ float bias_value(const uint4* r, int e, const float* 
   return LOG2E * blk_elem<float>(r[e >> 2], e & 3);
 }
 
-// Workgroup -> (resident block, b*H + h).  Hardware dispatches workgroups
-// round-robin over the 8 XCDs; when B*H is a multiple of 8 all blocks of one
-// (b,h) go to one XCD, so its streamed operands are read into one L2.
-__device__ __forceinline__ void block_coords(int nblk, int BH, int& blk, int& bh) {
-  const int L = blockIdx.x;
-  if ((BH & 7) == 0) {
-    const int s = L >> 3;
-    bh = (L & 7) + 8 * (s / nblk);
+// Workgroup -> (block, unit).  A unit is a set of nblk workgroups that stream the
+// same operand (one (b,h), or one (b,h) and query split in the dK/dV pass); units
+// are numbered 0 .. U-1.  Hardware dispatches workgroups round-robin over the 8 XCDs
+// (workgroup id % 8), each with its own L2, so the mapping keeps a unit's streamed
+// operand inside as few L2s as it can:
+//   U % 8 == 0:                 every unit on one XCD;
+//   8 % U == 0, nblk U % 8 == 0: a unit on 8 / U XCDs, each taking a contiguous
+//                               range of its blocks (windows that overlap stay on
+//                               one XCD except at the range ends);
+//   otherwise:                  unit-major order.
+__device__ __forceinline__ void block_coords(int nblk, int U, int& blk, int& unit) {
+  const int L = blockIdx.x, x = L & 7, s = L >> 3;
+  if ((U & 7) == 0) {
+    unit = x + 8 * (s / nblk);
     blk = s % nblk;
+  } else if (8 % U == 0 && (nblk * U) % 8 == 0) {
+    const int per = nblk * U / 8;
+    unit = x % U;
+    blk = (x / U) * per + s;
   } else {
-    bh = L / nblk;
+    unit = L / nblk;
     blk = L % nblk;
   }
 }
@@ -791,9 +801,10 @@ __global__ void __launch_bounds__(512) attn_bwd_kv2_kernel(AttnArgs a) {
   const int rt = wave % RT, ks = wave / RT;
   const int BH = a.B * a.H, Mq = a.Mq, Nk = a.Nk, d = a.d;
   const int nkb = (Nk + K::RK - 1) / K::RK;
-  int blk, bh;
-  block_coords(nkb * a.qsplit, BH, blk, bh);
-  const int kbk = blk % nkb, split = blk / nkb;
+  // units: (b,h) x query split; the key blocks of a unit stream the same queries
+  int kbk, unit;
+  block_coords(nkb, BH * a.qsplit, kbk, unit);
+  const int bh = unit / a.qsplit, split = unit % a.qsplit;
   const int b = bh / a.H, h = bh % a.H;
   const int k0 = kbk * K::RK;
   const int kt = k0 + 16 * rt;

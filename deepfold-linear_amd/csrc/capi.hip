@@ -305,13 +305,20 @@ StreamPtrs stream_ptrs(void* ws, int B, int H, int N, int G) {
   return p;
 }
 
-// Query-range splits of the attention dK/dV pass: enough workgroups to cover the
-// chip when keys are few (token-to-atom: 341 keys, 8192 queries).
+// Query-range splits of the attention dK/dV pass: when keys are few (token-to-atom:
+// 341 keys, 8192 queries), as many splits as keep the grid within one workgroup per
+// CU, preferring a count that makes B*H*splits a multiple of 8, so that the key
+// blocks of one (b,h, split) share an XCD and read its queries into one L2.
 int attn_qsplit(int B, int H, int Mq, int Nk) {
   const int kv_blocks = ((Nk + 63) / 64) * B * H;
-  int s = kv_blocks >= 256 ? 1 : (256 + kv_blocks - 1) / kv_blocks;
+  if (kv_blocks >= cu_count()) return 1;
   const int max_s = (Mq + 63) / 64;
-  return s < 1 ? 1 : (s > max_s ? max_s : s);
+  int s = cu_count() / kv_blocks;
+  if (s > max_s) s = max_s;
+  if (s < 1) s = 1;
+  for (int t = s; t >= (s + 1) / 2 && t > 1; --t)
+    if ((B * H * t) % 8 == 0) return t;
+  return s;
 }
 
 // Attention backward workspace: do_w, D, dK/dV partials, d pos_weight partials.

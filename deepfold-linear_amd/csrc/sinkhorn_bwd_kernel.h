@@ -51,88 +51,116 @@ constexpr int BWD_STREAM_SCRATCH = stream_scratch<BWD_NT>();
 constexpr int BWD_STREAM_VECS = 13 + 6;
 
 // ---------------------------------------------------------------------------
-// light sweep: out[q] = sum_j exp2(sc*<res_q, str_j> + cres[q] + w2_j (+bias)) * z_j
-// Every exponent is <= 0 here (S_col, T and W are bounded by 1), so no shift.
-template <typename T, int DP, bool GENERAL, bool TRANS>
-__device__ __forceinline__ void light_sweep(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
-                            const float* __restrict__ w2, const float* __restrict__ zv, int n_str_tiles, int rt0,
-                            int nr, float sc, const float* __restrict__ cres, const Bias& bias, float* out,
-                            float* scratch) {
+// Weighted sum of resident storage: out[q] = sum_j exp2(sc*<res_q, str_j> + cres[q]
+// + w2_j (+bias)) * z_j over the streamed tiles.  Every exponent is <= 0 here (S_col,
+// T and W are bounded by 1), so no shift.  NR resident tiles known at compile time
+// (the CG and fixed-point matvecs): resident fragments and row constants
+// are loaded once, all NR * SCH MFMAs of a slot group are issued before the
+// exponentials, and each resident tile keeps four independent accumulators (one per
+// accumulator row of a lane) instead of one dependent chain.  Slots past the wave's
+// last streamed tile re-read tile `wave` with w = NEG_BIG and z = 0.
+template <typename T, int DP, int NR, bool GENERAL, bool TRANS>
+__device__ __forceinline__ void lean_wsum_chunk(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
+                                                const float* __restrict__ w2, const float* __restrict__ zv,
+                                                int n_str_tiles, int rt0, int q0, float sc,
+                                                const float* __restrict__ cres, const Bias& bias, float* out,
+                                                float* scratch) {
   using M = Mfma<T, DP>;
   constexpr int SCH = sweep_sch<T, DP>();
   const int lane = threadIdx.x & (WAVE - 1);
-  const int wave = threadIdx.x / WAVE;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int g = lane >> 4;
   const float isc = 1.f / sc;
   const int ks = wave < n_str_tiles ? (n_str_tiles - wave + BWD_NW - 1) / BWD_NW : 0;
-  for (int c0 = 0; c0 < nr; c0 += SK_RT) {
-    const int nc = min(SK_RT, nr - c0);
-    float s[SK_RT];
+  typename M::Frag bf[NR];
+  f32x4 ci[NR];
 #pragma unroll
-    for (int r = 0; r < SK_RT; ++r) s[r] = 0.f;
-    for (int k0 = 0; k0 < ks; k0 += SCH) {
-      // streamed fragments, column terms and weights stay in registers for all
-      // resident tiles; slots past the wave's last tile carry w = NEG_BIG (no
-      // bias lookup, exp2 -> 0) and z = 0
-      typename M::Frag af[SCH];
-      f32x4 w[SCH], z[SCH];
+  for (int r = 0; r < NR; ++r) {
+    M::load(bf[r], res_lds + (size_t)((rt0 + r) * 16 + (lane & 15)) * DP, lane);
+    const float c = cres[q0 + r * 16 + (lane & 15)] * isc;
+    ci[r] = f32x4{c, c, c, c};
+  }
+  float s[NR][4];
 #pragma unroll
-      for (int k = 0; k < SCH; ++k) {
-        const bool live = k0 + k < ks;
-        const int st = live ? wave + BWD_NW * (k0 + k) : wave;
-        M::load(af[k], str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
-        w[k] = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
-        z[k] = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
-        if (!live) {
-          w[k] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
-          z[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      }
+  for (int r = 0; r < NR; ++r)
 #pragma unroll
-      for (int r = 0; r < SK_RT; ++r) {
-        if (r >= nc) continue;
-        typename M::Frag bf;
-        M::load(bf, res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
-        const float ci = cres[(c0 + r) * 16 + (lane & 15)] * isc;
-        const f32x4 cinit = f32x4{ci, ci, ci, ci};
-        f32x4 bv[SCH];
-        if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
-          int s0[SCH];
+    for (int e = 0; e < 4; ++e) s[r][e] = 0.f;
+  for (int k0 = 0; k0 < ks; k0 += SCH) {
+    typename M::Frag af[SCH];
+    f32x4 w[SCH], z[SCH];
 #pragma unroll
-          for (int k = 0; k < SCH; ++k) s0[k] = (k0 + k < ks ? wave + BWD_NW * (k0 + k) : wave) * 16 + 4 * g;
-          bias.template quads<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), s0, bv);
-        }
-        f32x4 x[SCH];
-#pragma unroll
-        for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
-        float acc_s = 0.f;
-#pragma unroll
-        for (int k = 0; k < SCH; ++k) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
-            if (GENERAL) xv += bv[k][e];
-            acc_s = __builtin_fmaf(fast_exp2(xv), z[k][e], acc_s);
-          }
-        }
-        s[r] += acc_s;
+    for (int k = 0; k < SCH; ++k) {
+      const bool live = k0 + k < ks;
+      const int st = live ? wave + BWD_NW * (k0 + k) : wave;
+      M::load(af[k], str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+      w[k] = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+      z[k] = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
+      if (!live) {
+        w[k] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+        z[k] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
+    f32x4 x[NR][SCH];
 #pragma unroll
-    for (int r = 0; r < SK_RT; ++r)
-      if (r < nc) {
-        const float ss = sum_groups(s[r]);
-        if (lane < 16) scratch[(wave * SK_RT + r) * 16 + lane] = ss;
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int k = 0; k < SCH; ++k) x[r][k] = M::qk(af[k], bf[r], ci[r]);  // independent MFMAs
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      f32x4 bv[SCH];
+      if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+        int s0[SCH];
+#pragma unroll
+        for (int k = 0; k < SCH; ++k) s0[k] = (k0 + k < ks ? wave + BWD_NW * (k0 + k) : wave) * 16 + 4 * g;
+        bias.template quads<TRANS>((rt0 + r) * 16 + (lane & 15), s0, bv);
       }
-    __syncthreads();
-    if ((int)threadIdx.x < nc * 16) {
-      const int q = threadIdx.x, r = q >> 4, l = q & 15;
-      float ss = 0.f;
 #pragma unroll
-      for (int w = 0; w < BWD_NW; ++w) ss += scratch[(w * SK_RT + r) * 16 + l];
-      out[c0 * 16 + q] = ss;
+      for (int k = 0; k < SCH; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float xv = __builtin_fmaf(x[r][k][e], sc, w[k][e]);
+          if (GENERAL) xv += bv[k][e];
+          s[r][e] = __builtin_fmaf(fast_exp2(xv), z[k][e], s[r][e]);
+        }
     }
-    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float ss = sum_groups((s[r][0] + s[r][1]) + (s[r][2] + s[r][3]));
+    if (lane < 16) scratch[(wave * NR + r) * 16 + lane] = ss;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < NR * 16) {
+    const int q = threadIdx.x, r = q >> 4, l = q & 15;
+    float ss = 0.f;
+#pragma unroll
+    for (int w_ = 0; w_ < BWD_NW; ++w_) ss += scratch[(w_ * NR + r) * 16 + l];
+    out[q0 + q] = ss;
+  }
+  __syncthreads();
+}
+
+// lean_wsum_chunk over the nr resident tiles [rt0, rt0 + nr), chunks of at most 4
+// tiles (2 with a bias, whose per-element values take the registers of two tiles).
+template <typename T, int DP, bool GENERAL, bool TRANS>
+__device__ __forceinline__ void lean_wsum(const T* res_lds, const T* str_lds, const float* w2, const float* zv,
+                                          int n_str_tiles, int rt0, int nr, float sc, const float* cres,
+                                          const Bias& bias, float* out, float* scratch) {
+  constexpr int CMAX = GENERAL ? 2 : 4;
+  for (int c0 = 0; c0 < nr; c0 += CMAX) {
+    const int nc = min(CMAX, nr - c0);
+    if (CMAX == 4 && nc == 4)
+      lean_wsum_chunk<T, DP, CMAX, GENERAL, TRANS>(res_lds, str_lds, w2, zv, n_str_tiles, rt0 + c0, c0 * 16, sc,
+                                                   cres, bias, out, scratch);
+    else if (CMAX == 4 && nc == 3)
+      lean_wsum_chunk<T, DP, CMAX - 1, GENERAL, TRANS>(res_lds, str_lds, w2, zv, n_str_tiles, rt0 + c0, c0 * 16,
+                                                       sc, cres, bias, out, scratch);
+    else if (nc == 2)
+      lean_wsum_chunk<T, DP, 2, GENERAL, TRANS>(res_lds, str_lds, w2, zv, n_str_tiles, rt0 + c0, c0 * 16, sc, cres,
+                                                bias, out, scratch);
+    else
+      lean_wsum_chunk<T, DP, 1, GENERAL, TRANS>(res_lds, str_lds, w2, zv, n_str_tiles, rt0 + c0, c0 * 16, sc, cres,
+                                                bias, out, scratch);
   }
 }
 
@@ -741,11 +769,11 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       }
     } else {
       if (row) {
-        if (general) light_sweep<T, DP, true, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
-        else light_sweep<T, DP, false, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
+        if (general) lean_wsum<T, DP, true, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
+        else lean_wsum<T, DP, false, false>(QS, KS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
       } else {
-        if (general) light_sweep<T, DP, true, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
-        else light_sweep<T, DP, false, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
+        if (general) lean_wsum<T, DP, true, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
+        else lean_wsum<T, DP, false, true>(KS, QS, w2, z, n_tiles, t0, nr, sc, cres, bias, lout, scratch);
       }
     }
   };
