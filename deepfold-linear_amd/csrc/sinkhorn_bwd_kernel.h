@@ -199,6 +199,37 @@ __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np
   return *s_flag == 0;
 }
 
+// gather_vector followed by block_sum(Np, f) in one barrier: every thread gathers the
+// entries i = t + k BWD_NT (the poll's assignment; the tail [n, Np) too), so after
+// its polls it already holds what f reads of dst and can sum f over its entries; the
+// wave partials then travel through the gather's own barrier.  The sum is the one
+// block_sum gives (same entries, order and reduction).  *dot is uniform on return.
+template <typename F>
+__device__ __forceinline__ bool gather_vector_dot(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
+                                                  const unsigned char* valid, ErrRef err, int* s_flag, F f,
+                                                  float* red, int& flip, float* dot) {
+  const int t = threadIdx.x;
+  for (int i = t; i < Np; i += BWD_NT)
+    if (i >= n) dst[i] = 0.f;
+  const bool ok = poll_vector<BWD_NT>(buf, n, tag, err, [&](int off, uint64_t w) {
+    const int i = off + t;
+    dst[i] = valid[i] ? __uint_as_float((uint32_t)(w >> 32)) : 0.f;
+  });
+  if (!ok) *s_flag = 1;
+  float acc = 0.f;
+  for (int i = t; i < Np; i += BWD_NT) acc += f(i);
+  acc = wave_sum(acc);
+  float* slot = red + flip * BWD_NW;
+  flip ^= 1;
+  if ((t & (WAVE - 1)) == 0) slot[t / WAVE] = acc;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < BWD_NW; ++w) tot += slot[w];
+  *dot = tot;
+  return *s_flag == 0;
+}
+
 // Resident-tile assignment of the heavy passes.  With nr <= BWD_NW resident tiles,
 // each tile gets wpt = BWD_NW / nr waves that take interleaved 32-row pairs of
 // every streamed chunk (all waves busy); the part > 0 waves hand their partial
@@ -838,9 +869,12 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       wsum(false, al, ct, be + r_lo);
       ++phase;
       for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase, local);
-      if (!gather_vector(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag)) return;
-      // CG update, identical in every member (utils/cg.py:70-92 with x0 = 0)
-      const float pAp = block_sum(Np, [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red, flip);
+      // CG update, identical in every member (utils/cg.py:70-92 with x0 = 0); p^T A p
+      // rides on the gather's barrier
+      float pAp;
+      if (!gather_vector_dot(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag,
+                             [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red, flip, &pAp))
+        return;
       if (early_exit && pAp == 0.f) break;
       const float alpha = (pAp != 0.f && rr != 0.f) ? rr / pAp : 0.f;
       // the update and ||r_new||^2 in one pass: each thread squares the entries it wrote
@@ -852,9 +886,20 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
         return ri * ri;
       }, sh.red, flip);
       const float beta = rr != 0.f ? rr_new / rr : 0.f;
-      for (int i = threadIdx.x; i < Np; i += BWD_NT) cp[i] = cr[i] + beta * cp[i];
       rr = rr_new;
-      __syncthreads();
+      if constexpr (STREAM) {
+        for (int i = threadIdx.x; i < Np; i += BWD_NT) cp[i] = cr[i] + beta * cp[i];
+        __syncthreads();
+      } else {
+        // each wave updates the entries of p that its own slots of the next row sweep
+        // read (streamed tiles wave + BWD_NW k, lean_wsum's assignment), so no barrier;
+        // the rest of p ([n_tiles * 16, Np), and r = p = 0 there) stays zero
+        const int wv = threadIdx.x / WAVE, ln = threadIdx.x & (WAVE - 1);
+        for (int e = ln; e < ((n_tiles - wv + BWD_NW - 1) / BWD_NW) * 16; e += WAVE) {
+          const int i = (wv + BWD_NW * (e >> 4)) * 16 + (e & 15);
+          cp[i] = cr[i] + beta * cp[i];
+        }
+      }
     }
     // z_v = D_c^{1/2} y, z_u = kappa D_r^{1/2} (W y)
     for (int i = threadIdx.x; i < Np; i += BWD_NT) {
