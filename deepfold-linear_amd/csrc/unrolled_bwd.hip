@@ -36,6 +36,7 @@ constexpr int UNR_NT = 512;
 constexpr int UNR_NW = UNR_NT / WAVE;
 template <int DP> constexpr int unr_maxt() { return DP <= 32 ? 2 : 1; }
 constexpr int UNR_MAXT_ANY = 2;
+constexpr int UNR_MAX_LOCAL = 16 * UNR_MAXT_ANY * UNR_NW;  // rows of a stripe (unrolled_max_tiles)
 
 __host__ __device__ inline int unr_wpt(int nr) { return nr >= UNR_NW ? 1 : UNR_NW / nr; }
 
@@ -113,13 +114,75 @@ __global__ void __launch_bounds__(256) unrolled_finalize_kernel(UnrBwdArgs a, fl
   }
 }
 
+// gather_vector (sinkhorn_bwd_kernel.h) storing scale * value at valid entries.
+__device__ __forceinline__ bool gather_scaled(const uint64_t* buf, int n, int Np, uint32_t tag, float* dst,
+                                              const unsigned char* valid, ErrRef err, int* s_flag, float scale) {
+  const int t = threadIdx.x;
+  for (int i = n + t; i < Np; i += UNR_NT) dst[i] = 0.f;
+  const bool ok = poll_vector<UNR_NT>(buf, n, tag, err, [&](int off, uint64_t w) {
+    const int i = off + t;
+    dst[i] = valid[i] ? scale * __uint_as_float((uint32_t)(w >> 32)) : 0.f;
+  });
+  if (!ok) *s_flag = 1;
+  __syncthreads();
+  return *s_flag == 0;
+}
+
+// A lane's share of the transposed operand of one dQ / dK product (row l % 16 of the
+// operand, streamed columns 4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3), loaded ahead of
+// the product, and the product itself (Mfma<T, DP>::pv_split with the loads done).
+template <typename T> struct VtQuad;
+template <> struct VtQuad<bf16> { using type = bf16x4; };
+template <> struct VtQuad<float> { using type = f32x4; };
+template <typename T>
+__device__ __forceinline__ void load_vt(const T* vt_row, int lane, typename VtQuad<T>::type& lo,
+                                        typename VtQuad<T>::type& hi) {
+  const int g = lane >> 4;
+  lo = *reinterpret_cast<const typename VtQuad<T>::type*>(vt_row + 4 * g);
+  hi = *reinterpret_cast<const typename VtQuad<T>::type*>(vt_row + 16 + 4 * g);
+}
+__device__ __forceinline__ f32x4 pv_split_regs(const f32x4& p0, const f32x4& p1, const bf16x4& lo, const bf16x4& hi,
+                                               f32x4 acc) {
+  bf16x8 ah, al, b;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bf16 h0 = (bf16)p0[r], h1 = (bf16)p1[r];
+    ah[r] = h0; ah[4 + r] = h1;
+    al[r] = (bf16)(p0[r] - (float)h0); al[4 + r] = (bf16)(p1[r] - (float)h1);
+    b[r] = lo[r];
+    b[4 + r] = hi[r];
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 pv_split_regs(const f32x4& p0, const f32x4& p1, const f32x4& lo, const f32x4& hi,
+                                               f32x4 acc) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p0[r], lo[r], acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[r], hi[r], acc, 0, 0, 0);
+  return acc;
+}
+
 // GEN: the cost may carry position bins or geometry (set by the host when either is
 // passed); GEN = false compiles none of their per-element code.
 // T: the input type.  The cost recompute q.k and the products dQ += W K, dK += W^T Q
 // run on Mfma<T, DP> (bf16 inputs: the bf16 MFMA with exact operands, W as a hi + lo
 // bf16 pair, fp32 accumulation, as the forward); the centroid sweep's products, whose
 // operands (sigma(G) dO) are not bf16-exact, run on the fp32 MFMA.
-template <typename T, int DP, bool GEN>
+// Staged operands (STAGE: bf16 inputs, DP = 32, when LDS has room): a sweep's streamed
+// operand, row-major [Np][DP] and transposed [DP][Np] (the prep kernel's padded copies),
+// is copied into LDS with padded rows (no bank conflicts for the fragment reads),
+// over the part hand-over region.  The copy for the next sweep is issued right after
+// a sweep's combine, so its loads overlap the exchange wait; the main loops then read
+// LDS instead of waiting on L2.
+template <typename T, int DP> constexpr int unr_srs() { return DP + 16 / (int)sizeof(T); }
+__host__ __device__ inline size_t unr_stage_bytes(int Np, int DP, int elem) {
+  const int pad = 16 / elem;
+  return ((size_t)Np * (DP + pad) + (size_t)DP * (Np + pad)) * elem;
+}
+
+template <typename T, int DP, bool GEN, bool STAGE>
 __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   using M = Mfma<float, DP>;
   using MQ = Mfma<T, DP>;
@@ -161,7 +224,15 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   float* STB = STA + Np;  // streamed exponent terms of term 2 (or of P in RS(K-1))
   float* sred = STB + Np;                        // [NW][MAXT][16]
   float* spart = sred + NW * UNR_MAXT_ANY * 16;  // [NW][16*64] part hand-over
-  float* sscal = spart + NW * 16 * 64;           // [NW][2]
+  // part hand-over [NW][16*64], or (STAGE) the staged operands of a sweep
+  constexpr int SRS = unr_srs<T, DP>();          // row stride of the staged row-major operand
+  const int STS = Np + 16 / (int)sizeof(T);      // row stride of the staged transposed operand
+  const int region = STAGE ? max(NW * 16 * 64, (int)(unr_stage_bytes(Np, DP, sizeof(T)) / 4)) : NW * 16 * 64;
+  T* stg_r = reinterpret_cast<T*>(spart);
+  T* stg_t = stg_r + (size_t)Np * SRS;
+  float* sscal = spart + region;                 // [NW]
+  float* ldmu = sscal + NW;                      // d log_mu of my rows, summed over the sweeps
+  float* ldnu = ldmu + UNR_MAX_LOCAL;            // d log_nu of my columns
 
   const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &s_tmp);
   const int n_tiles = (n + 15) / 16;
@@ -197,6 +268,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     GLU[i] = 0.f;
     GLV[i] = 0.f;
   }
+  for (int q = tid; q < UNR_MAX_LOCAL; q += UNR_NT) ldmu[q] = ldnu[q] = 0.f;
   __syncthreads();
   const float eps = a.eps[h];
   const float kappa = a.lam / (a.lam + eps);
@@ -228,6 +300,39 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const float* vp = a.vp + bh * Np * DP;
   const float* gp = a.gp + bh * Np * DP;
   const float* gt = a.gt + bh * DP * Np;
+
+  // Copy of the streamed operand of a sweep of orientation `row` into LDS, batches of
+  // 8 16-byte chunks a thread (all loads of a batch, then its stores).  Loads are
+  // unconditional, from clamped chunk indices.
+  auto stage_operands = [&](bool row) {
+    if constexpr (STAGE) {
+      typedef __attribute__((__vector_size__(16))) int i32x4;
+      const T* srow = row ? kp : qp;  // [Np][DP]
+      const T* scol = row ? kt : qt;  // [DP][Np]
+      constexpr int CPR = DP * (int)sizeof(T) / 16;  // chunks of a row-major row
+      const int cpt = Np * (int)sizeof(T) / 16;      // chunks of a transposed row
+      const int nrm = Np * CPR, ntot = nrm + DP * cpt;
+      for (int e0 = 0; e0 < ntot; e0 += 8 * UNR_NT) {
+        i32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = min(e0 + u * UNR_NT + tid, ntot - 1);
+          const T* src = e < nrm ? srow + (size_t)(e / CPR) * DP + (e % CPR) * 8
+                                 : scol + (size_t)((e - nrm) / cpt) * Np + ((e - nrm) % cpt) * 8;
+          v[u] = *reinterpret_cast<const i32x4*>(src);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = e0 + u * UNR_NT + tid;
+          if (e >= ntot) continue;
+          T* dst = e < nrm ? stg_r + (size_t)(e / CPR) * SRS + (e % CPR) * 8
+                           : stg_t + (size_t)((e - nrm) / cpt) * STS + ((e - nrm) % cpt) * 8;
+          *reinterpret_cast<i32x4*>(dst) = v[u];
+        }
+      }
+    }
+  };
+  stage_operands(false);  // the first sweep (CS_cent) streams Q
 
   f32x4 dQa[MAXT][NC], dKa[MAXT][NC];
   float gbx[MAXT], gby[MAXT], gbz[MAXT], xt0[MAXT], xt1[MAXT], xt2[MAXT], dmu[MAXT], dnu[MAXT];
@@ -295,7 +400,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   // the header comment (CS_cent uses k = K).  USE_C (the recurrence term: all but
   // RS(-1) and CS_cent) and TERM2 (the mirror term: all but RS(K-1) and CS_cent) are
   // compile-time, so the element loop carries no test of them.
-  auto sweep = [&](auto row_tag, auto cent_tag, auto usec_tag, auto term2_tag, int k) -> bool {
+  auto sweep = [&](auto row_tag, auto cent_tag, auto usec_tag, auto term2_tag, int k, bool stage_next) -> bool {
     constexpr bool ROW = decltype(row_tag)::value;
     constexpr bool CENT = decltype(cent_tag)::value;
     constexpr bool use_c = decltype(usec_tag)::value;
@@ -321,14 +426,16 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     }
     __syncthreads();
     const float* STC = ROW ? GLV : GLU;  // streamed recurrence coefficients
-    const T* Sop = ROW ? kp : qp;
-    const T* Sot = ROW ? kt : qt;
+    const T* Sop = STAGE ? stg_r : (ROW ? kp : qp);
+    const T* Sot = STAGE ? stg_t : (ROW ? kt : qt);
+    const int sop_rs = STAGE ? SRS : DP;  // row strides of the streamed operand and its transpose
+    const int sot_rs = STAGE ? STS : Np;
     const T* Rop = ROW ? qp : kp;
 
     typename MQ::Frag bf[MAXT];
     typename M::Frag cbf[MAXT];
     float ra[MAXT], rb[MAXT], dd[MAXT], xr0[MAXT], xr1[MAXT], xr2[MAXT], Dr[MAXT], gr0[MAXT], gr1[MAXT], gr2[MAXT];
-    float red[MAXT];
+    float red[MAXT][4];  // per accumulator row of a lane: independent chains
     f32x4 gVa[MAXT][NC];
 #pragma unroll
     for (int s = 0; s < MAXT; ++s) {
@@ -344,13 +451,13 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           if (use_c) ra[s] = Un(k, ri) * LOG2E;                                             // s^{C,k}
           if (CENT) rb[s] = (a.log_u[bhN + ri] - a.log_z[bhN + ri]) * LOG2E;                // P
           else if (term2) rb[s] = (Un(k + 1, ri) * ik - a.log_mu[bhN + ri]) * LOG2E;        // s^{R,k+1}
-          if (term2) dd[s] = kappa * GLU[ri];
+          if (term2) dd[s] = GLU[ri];
         } else {    // resident columns j
           if (CENT) ra[s] = Vn(K - 1, ri) * LOG2E;                                          // P
           else {
             ra[s] = Vn(k - 1, ri) * LOG2E;                                                  // s^{R,k}
             rb[s] = (Vn(k, ri) * ik - a.log_nu[bhN + ri]) * LOG2E;                          // s^{C,k}
-            dd[s] = kappa * GLV[ri];
+            dd[s] = GLV[ri];
           }
         }
       }
@@ -364,12 +471,41 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
         gr1[s] = gx1[ri];
         gr2[s] = gx2[ri];
       }
-      red[s] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[s][e] = 0.f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) gVa[s][c] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     if (ts < nts) {
+      // The streamed operands of a pair of tiles (Q or K fragments for the cost, the
+      // transposed operand for dQ / dK) come from global memory (L2): they are the same
+      // for every resident slot, so they are loaded once per pair, and one pair ahead:
+      // the loads of pair sp + wpt are issued (unconditionally, from a clamped pair)
+      // before pair sp is computed.
+      using V4 = typename VtQuad<T>::type;
+      typename MQ::Frag afn[2];
+      V4 vln[NC], vhn[NC];
+      auto load_pair = [&](int sp_) {
+        const int spc = min(sp_, n_pairs - 1);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          MQ::load(afn[hh], Sop + (size_t)((2 * spc + hh) * 16 + (lane & 15)) * sop_rs, lane);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const T* vt_row = Sot + (size_t)(c * 16 + (lane & 15)) * sot_rs + spc * 32;
+          load_vt<T>(vt_row, lane, vln[c], vhn[c]);
+        }
+      };
+      load_pair(part);
       for (int sp = part; sp < n_pairs; sp += wpt) {
+        typename MQ::Frag afc[2] = {afn[0], afn[1]};
+        V4 vlc[NC], vhc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          vlc[c] = vln[c];
+          vhc[c] = vhn[c];
+        }
+        load_pair(sp + wpt);
 #pragma unroll
         for (int s = 0; s < MAXT; ++s) {
           const int rt = ts + nts * s;
@@ -380,8 +516,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           for (int hh = 0; hh < 2; ++hh) {
             const int st = 2 * sp + hh;
             const int o = st * 16 + 4 * g;
-            typename MQ::Frag af;
-            MQ::load(af, Sop + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+            const typename MQ::Frag& af = afc[hh];
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
             f32x4 t = zero;
             if (CENT) {
@@ -389,7 +524,12 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
               M::load(cf, (ROW ? vp : gp) + (size_t)(st * 16 + (lane & 15)) * DP, lane);
               t = M::qk(cf, cbf[s], zero);
             }
-            const f32x4 x = MQ::qk(af, bf[s], zero);
+            // exponent arguments sc (q.k + ra / sc) + sa_j and sc (q.k + rb / sc) + sb_j: the
+            // resident terms ride in the accumulator init, one product per term
+            constexpr bool E1 = use_c || (CENT && !ROW), E2 = term2 || (CENT && ROW);
+            const float ca = ra[s] / sc, cb = rb[s] / sc;
+            const f32x4 x1 = E1 ? MQ::qk(af, bf[s], f32x4{ca, ca, ca, ca}) : zero;
+            const f32x4 x2 = E2 ? MQ::qk(af, bf[s], f32x4{cb, cb, cb, cb}) : zero;
             const f32x4 sa = *reinterpret_cast<const f32x4*>(STA + o);
             const f32x4 sb = *reinterpret_cast<const f32x4*>(STB + o);
             const f32x4 scf = use_c ? *reinterpret_cast<const f32x4*>(STC + o) : zero;
@@ -420,14 +560,14 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
                 if (bin < 68) bias += s_pw[bin];
                 else bin = -1;
               }
-              const float lg = __builtin_fmaf(x[e], sc, bsc * bias);
-              const float e1 = (use_c || (CENT && !ROW)) ? fast_exp2(lg + sa[e] + ra[s]) : 0.f;
-              const float e2 = (term2 || (CENT && ROW)) ? fast_exp2(lg + sb[e] + rb[s]) : 0.f;
+              const float bb = GEN ? bsc * bias : 0.f;
+              const float e1 = E1 ? fast_exp2(__builtin_fmaf(x1[e], sc, GEN ? sa[e] + bb : sa[e])) : 0.f;
+              const float e2 = E2 ? fast_exp2(__builtin_fmaf(x2[e], sc, GEN ? sb[e] + bb : sb[e])) : 0.f;
               float W = 0.f;
               if (use_c) {
-                const float t1 = kappa * e1 * scf[e];
+                const float t1 = e1 * scf[e];  // scf holds kappa gl (scaled when gathered)
                 W = t1;
-                red[s] -= t1;
+                red[s][e] -= t1;
               }
               if (term2) W = __builtin_fmaf(e2, dd[s], W);
               if (CENT) {
@@ -438,7 +578,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
                 const float qv = P * (dT - (ROW ? Dr[s] : sD[e]));
                 W -= qv;
                 if (!ROW) {
-                  red[s] += qv;
+                  red[s][e] += qv;
                   xt0[s] = __builtin_fmaf(P, sg0[e], xt0[s]);
                   xt1[s] = __builtin_fmaf(P, sg1[e], xt1[s]);
                   xt2[s] = __builtin_fmaf(P, sg2[e], xt2[s]);
@@ -461,9 +601,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           for (int c = 0; c < NC; ++c) {
             // dQ += W K (dK += W^T Q): for bf16 inputs W is carried as a bf16 hi + lo pair
             // against the exact bf16 operand (two bf16 MFMAs), as the forward's P V
-            const T* vt_row = Sot + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32;
-            if (ROW) dQa[s][c] = MQ::pv_split(wop[0], wop[1], vt_row, lane, dQa[s][c]);
-            else dKa[s][c] = MQ::pv_split(wop[0], wop[1], vt_row, lane, dKa[s][c]);
+            if (ROW) dQa[s][c] = pv_split_regs(wop[0], wop[1], vlc[c], vhc[c], dQa[s][c]);
+            else dKa[s][c] = pv_split_regs(wop[0], wop[1], vlc[c], vhc[c], dKa[s][c]);
             if (CENT && !ROW)
               gVa[s][c] = M::pv(pop[0], pop[1], gt + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, gVa[s][c]);
           }
@@ -474,39 +613,57 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     uint64_t* buf = ROW ? xgu : xgv;
     ++phase;
     const uint32_t tag = salt | phase;
-    combine_rows(red, [&](int q, float v) {
+    float redv[MAXT];
+#pragma unroll
+    for (int s = 0; s < MAXT; ++s) redv[s] = (red[s][0] + red[s][1]) + (red[s][2] + red[s][3]);
+    // the marginal gradients accumulate in LDS (thread q owns row q in every sweep)
+    // and are written once at the end
+    combine_rows(redv, [&](int q, float v) {
       const int i = r_lo + q;
       if (i >= n) return;
       const bool ok = valid[i];
       if (publish) xch_put(buf + i, v, tag);
       if (!ok) return;
       if (ROW) {
-        if (k >= 0) a.dlog_mu[bhN + i] = (k == K - 1 ? 0.f : a.dlog_mu[bhN + i]) + kappa * v;
+        if (k >= 0) ldmu[q] += kappa * v;
       } else if (CENT || k >= 1) {
-        a.dlog_nu[bhN + i] = (CENT ? 0.f : a.dlog_nu[bhN + i]) + kappa * v;
+        ldnu[q] += kappa * v;
       } else if (a.dv_init) {
         a.dv_init[bhN + i] = v;
       }
     });
+    // the next sweep streams the other operand (the sweeps alternate): its copy is
+    // issued now, past the combine's barrier (no wave reads the region any more), so
+    // it overlaps the exchange; CS_cent hands its dV partials over through the same
+    // region and stages after that
+    if (stage_next && !(CENT && !ROW)) stage_operands(!ROW);
     if (publish) {
-      if (!gather_vector(buf, n, Np, tag, ROW ? GLU : GLV, valid, a.err, &s_flag)) return false;
+      // gathered as kappa gl: both readers (the streamed coefficients and the
+      // resident dd) want the kappa multiple
+      if (!gather_scaled(buf, n, Np, tag, ROW ? GLU : GLV, valid, a.err, &s_flag, kappa)) return false;
     } else {
       __syncthreads();
     }
-    if (CENT && !ROW) write_rows(gVa, a.dv, 1.f);
+    if (CENT && !ROW) {
+      write_rows(gVa, a.dv, 1.f);
+      if (stage_next) {
+        __syncthreads();
+        stage_operands(!ROW);
+      }
+    }
     return true;
   };
 
   using TRUE_ = std::integral_constant<bool, true>;
   using FALSE_ = std::integral_constant<bool, false>;
   // (row, cent, use_c, term2)
-  if (!sweep(FALSE_{}, TRUE_{}, FALSE_{}, FALSE_{}, K)) return;
-  if (!sweep(TRUE_{}, TRUE_{}, TRUE_{}, FALSE_{}, K - 1)) return;
+  if (!sweep(FALSE_{}, TRUE_{}, FALSE_{}, FALSE_{}, K, true)) return;
+  if (!sweep(TRUE_{}, TRUE_{}, TRUE_{}, FALSE_{}, K - 1, true)) return;
   for (int k = K - 1; k >= 0; --k) {
-    if (k < K - 1 && !sweep(TRUE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k)) return;
-    if (!sweep(FALSE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k)) return;
+    if (k < K - 1 && !sweep(TRUE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k, true)) return;
+    if (!sweep(FALSE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k, true)) return;
   }
-  if (!sweep(TRUE_{}, FALSE_{}, FALSE_{}, TRUE_{}, -1)) return;
+  if (!sweep(TRUE_{}, FALSE_{}, FALSE_{}, TRUE_{}, -1, false)) return;
 
   // ---- outputs of my stripe
   const float fs = -1.f / (sqrtf((float)d) * eps);
@@ -515,7 +672,11 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   // invalid rows of the stripe: zero marginal gradients
   for (int q = tid; q < nr * 16; q += UNR_NT) {
     const int i = r_lo + q;
-    if (i < N && !(i < n && valid[i])) {
+    if (i >= N) continue;
+    if (i < n && valid[i]) {
+      a.dlog_mu[bhN + i] = ldmu[q];
+      a.dlog_nu[bhN + i] = ldnu[q];
+    } else {
       a.dlog_mu[bhN + i] = 0.f;
       a.dlog_nu[bhN + i] = 0.f;
       if (a.dv_init) a.dv_init[bhN + i] = 0.f;
@@ -555,14 +716,20 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   }
 }
 
-size_t unrolled_bwd_lds_bytes(int N) {
+size_t unrolled_bwd_lds_bytes(int N, int DP, int elem, bool stage) {
   const size_t Np = ((N + 31) / 32) * 32;
   size_t bytes = ((Np + 15) / 16) * 16;
   bytes += 11 * Np * 4;                              // coordinates, grad x_c, D, gathered vectors, STA, STB
   bytes += (size_t)UNR_NW * UNR_MAXT_ANY * 16 * 4;   // recurrence partials
-  bytes += (size_t)UNR_NW * 16 * 64 * 4;             // part hand-over (>= the dx hand-over)
+  // part hand-over (>= the dx hand-over), or a sweep's staged operands (4-byte units)
+  bytes += 4 * std::max((size_t)UNR_NW * 16 * 64, stage ? unr_stage_bytes((int)Np, DP, elem) / 4 : (size_t)0);
   bytes += UNR_NW * 4;
+  bytes += 2 * UNR_MAX_LOCAL * 4;                    // d log_mu, d log_nu of the stripe
   return bytes;
+}
+
+bool unrolled_can_stage(int N, int DP, int elem, size_t limit) {
+  return elem == 2 && DP == 32 && unrolled_bwd_lds_bytes(N, DP, elem, true) <= limit;
 }
 
 int unrolled_max_tiles(int DP) { return (DP <= 32 ? unr_maxt<32>() : unr_maxt<64>()) * UNR_NW; }
@@ -586,9 +753,9 @@ hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipS
   return hipErrorInvalidValue;
 }
 
-template <typename T, int DP, bool GEN>
+template <typename T, int DP, bool GEN, bool STAGE>
 static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  auto kern = unrolled_bwd_kernel<T, DP, GEN>;
+  auto kern = unrolled_bwd_kernel<T, DP, GEN, STAGE>;
   hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(UNR_NT);
@@ -602,17 +769,28 @@ static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stre
 }
 
 template <typename T>
-static hipError_t launch_unr_dt(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop) {
+static hipError_t launch_unr_dt(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop, bool stage) {
   const bool gen = (a.bins8 && a.pos_w) || (a.has_geo && a.w_dist);
+  if constexpr (sizeof(T) == 2) {
+    if (stage && DP == 32)
+      return gen ? launch_unr_t<T, 32, true, true>(a, lds, stream, coop)
+                 : launch_unr_t<T, 32, false, true>(a, lds, stream, coop);
+  }
+  if (stage) return hipErrorInvalidValue;
   if (DP == 32)
-    return gen ? launch_unr_t<T, 32, true>(a, lds, stream, coop) : launch_unr_t<T, 32, false>(a, lds, stream, coop);
+    return gen ? launch_unr_t<T, 32, true, false>(a, lds, stream, coop)
+               : launch_unr_t<T, 32, false, false>(a, lds, stream, coop);
   if (DP == 64)
-    return gen ? launch_unr_t<T, 64, true>(a, lds, stream, coop) : launch_unr_t<T, 64, false>(a, lds, stream, coop);
+    return gen ? launch_unr_t<T, 64, true, false>(a, lds, stream, coop)
+               : launch_unr_t<T, 64, false, false>(a, lds, stream, coop);
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
-  return bf16_in ? launch_unr_dt<bf16>(a, DP, lds, stream, coop) : launch_unr_dt<float>(a, DP, lds, stream, coop);
+// stage: unrolled_can_stage() said yes and lds was sized with it
+hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop,
+                               bool stage) {
+  return bf16_in ? launch_unr_dt<bf16>(a, DP, lds, stream, coop, stage)
+                 : launch_unr_dt<float>(a, DP, lds, stream, coop, stage);
 }
 
 hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream) {

@@ -80,6 +80,9 @@ CASES = [
     (2, 3, 70, 32, 3, [0.5, 1.0, 2.0], [70, 41], True, torch.float32, 1e-4),
     (1, 2, 48, 64, 5, [0.7, 1.3], None, False, torch.bfloat16, 2e-2),
     (1, 2, 300, 32, 4, [0.5, 1.0], [290], False, torch.float32, 1e-4),        # several tiles per member
+    # bf16 with d <= 32: the sweeps stream their operand from LDS copies (staged path)
+    (2, 3, 70, 32, 5, [0.5, 1.0, 2.0], [70, 41], False, torch.bfloat16, 2e-2),
+    (1, 2, 300, 32, 4, [0.5, 1.0], [290], False, torch.bfloat16, 2e-2),
 ]
 
 
@@ -132,3 +135,33 @@ def test_flash_sinkhorn_defaults_to_unrolled():
         ((O * wO.to(DEV)).sum() + (xc * wx.to(DEV)).sum()).backward()
         for k in ("Q", "K", "V", "x", "pw", "wd", "lmu", "lnu"):
             assert_close_rel(L[k].grad.cpu().numpy(), gr[k].numpy(), 1e-4, f"{fn} grad {k}")
+
+
+@pytest.mark.parametrize("B,H,N,d,K,lens", [(2, 4, 96, 32, 6, [96, 61]), (1, 2, 300, 24, 4, [290])])
+def test_unrolled_content_only_bf16(B, H, N, d, K, lens):
+    """The content-only cost (no bins, no geometry: the kernel's GEN = false build, the
+    one the headline workload runs) with bf16 inputs at d <= 32 (staged operands)."""
+    print(f"case content-only B{B} H{H} N{N} d{d} K{K}", flush=True)
+    t, bins, e, mask, wo, wx = _inputs(B, H, N, d, seed=N + 3 * K, eps=[0.5] * H, lens=lens)
+    t["pw"] = torch.zeros_like(t["pw"])
+    t["wd"] = torch.zeros_like(t["wd"])
+    for k in ("Q", "K", "V", "G"):
+        t[k] = t[k].to(torch.bfloat16).float()
+    vr, gr = _oracle(t, torch.zeros_like(bins), e, mask, wo, wx, K)
+    from deepfold_amd import flash_sinkhorn_attn
+
+    L = {k: v.to(DEV) for k, v in t.items()}
+    for k in ("Q", "K", "V", "G"):
+        L[k] = L[k].to(torch.bfloat16)
+    L = {k: v.detach().requires_grad_(True) for k, v in L.items()}
+    # no bins and w_dist = None (the reference's w_dist = 0 without reading x): GEN = false
+    o, xc, lu, lv = flash_sinkhorn_attn(L["Q"], L["K"], L["V"], L["G"], L["x"], L["pw"], None, e.to(DEV), None,
+                                        L["lmu"], L["lnu"], K_iter=K, mask=mask.to(DEV), ift_mode="unrolled")
+    ((o * wo.to(DEV)).sum() + (xc * wx.to(DEV)).sum()).backward()
+    vg = {"o": o, "xc": xc, "lu": lu, "lv": lv}
+    for k in ("o", "xc", "lu", "lv"):
+        assert_close_rel(vg[k].detach().float().cpu().numpy(), vr[k].detach().numpy(), 2e-2, k)
+    for k in ("Q", "K", "V", "G", "lmu", "lnu"):
+        got = L[k].grad.float().cpu().numpy()
+        assert np.isfinite(got).all(), k
+        assert_close_rel(got, gr[k].numpy(), 2e-2, f"grad {k}")
