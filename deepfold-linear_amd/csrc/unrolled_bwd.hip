@@ -38,7 +38,6 @@ template <int DP> constexpr int unr_maxt() { return DP <= 32 ? 2 : 1; }
 constexpr int UNR_MAXT_ANY = 2;
 constexpr int UNR_MAX_LOCAL = 16 * UNR_MAXT_ANY * UNR_NW;  // rows of a stripe (unrolled_max_tiles)
 
-__host__ __device__ inline int unr_wpt(int nr) { return nr >= UNR_NW ? 1 : UNR_NW / nr; }
 
 // Prep: one thread per (b, h, i, c), c < DP.  fp32 copies of Q, K, V, gO and gO^T,
 // D, grad x_c, coordinates; dG = sigma(1 - sigma) O dO (flash_sinkhorn_attn.py:278-292).
@@ -289,9 +288,18 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     return a.v_init ? a.v_init[bhN + j] : 0.f;
   };
 
-  const int wpt = unr_wpt(nr);
-  const int nts = NW / wpt;
-  const int ts = wave / wpt, part = wave % wpt;
+  // Wave -> resident tiles.  nr <= NW: wave takes tile wave % nr as part wave / nr of
+  // the wpt_of(tile) waves of that tile (one slot; every wave busy, and for nr = 3 the
+  // two waves of a SIMD, w and w + 4, take different tiles so that no SIMD carries
+  // two whole shares); nr > NW: wave owns tiles wave and wave + NW (slots 0 and 1).
+  const bool spread = nr <= NW;
+  const int ts = spread ? wave % nr : wave;
+  const int part = spread ? wave / nr : 0;
+  auto wpt_of = [&](int rt) { return spread ? (NW - rt + nr - 1) / nr : 1; };
+  const int wpt = wpt_of(ts);                // this wave's stride over streamed pairs
+  const int nts = spread ? nr : NW;          // slot s holds tile ts + nts s
+  auto wave_of = [&](int rt, int p) { return spread ? rt + p * nr : rt % NW; };  // part p of tile rt
+  auto slot_of = [&](int rt) { return spread ? 0 : rt / NW; };
   const int n_pairs = (n_tiles + 1) / 2;
   const T* qp = static_cast<const T*>(a.qp) + bh * Np * DP;
   const T* kp = static_cast<const T*>(a.kp) + bh * Np * DP;
@@ -351,7 +359,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
 
   auto write_rows = [&](f32x4 (&acc)[MAXT][NC], void* out, float scale) {  // gradients in the input type
     __syncthreads();
-    if (wpt > 1 && part > 0 && ts < nr) {
+    if (part > 0) {
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -368,7 +376,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float v = acc[s][c][r];
-            for (int p = 1; p < wpt; ++p) v += spart[(size_t)(wave + p) * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)];
+            for (int p = 1; p < wpt_of(rt); ++p)
+              v += spart[(size_t)wave_of(rt, p) * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)];
             const int row = (t0 + rt) * 16 + 4 * g + r, col = c * 16 + (lane & 15);
             if (row < N && col < d)
               static_cast<T*>(out)[(bh * N + row) * d + col] = from_f32<T>((row < n && valid[row]) ? scale * v : 0.f);
@@ -388,9 +397,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     __syncthreads();
     for (int q = tid; q < nr * 16; q += UNR_NT) {
       const int rt = q >> 4, l16 = q & 15;
-      const int s = rt / nts, tsl = rt % nts;
       float v = 0.f;
-      for (int p = 0; p < wpt; ++p) v += sred[((tsl * wpt + p) * MAXT + s) * 16 + l16];
+      for (int p = 0; p < wpt_of(rt); ++p) v += sred[(wave_of(rt, p) * MAXT + slot_of(rt)) * 16 + l16];
       dst_fn(q, v);
     }
   };
@@ -698,10 +706,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const float gs = geo ? wd / (eps * r0) : 0.f;
   for (int q = tid; q < nr * 16; q += UNR_NT) {
     const int rt = q >> 4, l16 = q & 15;
-    const int s = rt / nts, tsl = rt % nts;
     float v[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < wpt; ++p)
-      for (int t = 0; t < 6; ++t) v[t] += spart[((size_t)((tsl * wpt + p) * MAXT + s) * 16 + l16) * 6 + t];
+    for (int p = 0; p < wpt_of(rt); ++p)
+      for (int t = 0; t < 6; ++t)
+        v[t] += spart[((size_t)(wave_of(rt, p) * MAXT + slot_of(rt)) * 16 + l16) * 6 + t];
     const int i = r_lo + q;
     if (i < N) {
       const bool ok = i < n && valid[i];
