@@ -140,26 +140,52 @@ __device__ __forceinline__ void load_vt(const T* vt_row, int lane, typename VtQu
   lo = *reinterpret_cast<const typename VtQuad<T>::type*>(vt_row + 4 * g);
   hi = *reinterpret_cast<const typename VtQuad<T>::type*>(vt_row + 16 + 4 * g);
 }
-__device__ __forceinline__ f32x4 pv_split_regs(const f32x4& p0, const f32x4& p1, const bf16x4& lo, const bf16x4& hi,
-                                               f32x4 acc) {
-  bf16x8 ah, al, b;
+// The hi + lo split works on packed pairs: one rounding conversion gives the hi
+// halves of two values, whose fp32 values are bit masks of the packed word (no second
+// conversion), then one conversion packs the two remainders.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hp, uint32_t& lp) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t h = {(bf16)x0, (bf16)x1};
+  hp = __builtin_bit_cast(uint32_t, h);
+  const float h0 = __uint_as_float(hp << 16), h1 = __uint_as_float(hp & 0xffff0000u);
+  const bf16x2_t l = {(bf16)(x0 - h0), (bf16)(x1 - h1)};
+  lp = __builtin_bit_cast(uint32_t, l);
+}
+// W of a lane's two tiles (p0: streamed rows 0..15, p1: 16..31) as the A operand of
+// the dQ / dK product: bf16 inputs carry it as a hi + lo pair of bf16 fragments (split
+// once, used for every output column block), fp32 inputs as the values themselves.
+template <typename T> struct WOperand;
+template <> struct WOperand<bf16> { bf16x8 hi, lo; };
+template <> struct WOperand<float> { f32x4 p0, p1; };
+template <typename T> __device__ __forceinline__ WOperand<T> w_operand(const f32x4& p0, const f32x4& p1);
+template <> __device__ __forceinline__ WOperand<bf16> w_operand<bf16>(const f32x4& p0, const f32x4& p1) {
+  typedef __attribute__((__vector_size__(16))) uint32_t u32x4;
+  uint32_t h[4], l[4];
+  split_pair(p0[0], p0[1], h[0], l[0]);
+  split_pair(p0[2], p0[3], h[1], l[1]);
+  split_pair(p1[0], p1[1], h[2], l[2]);
+  split_pair(p1[2], p1[3], h[3], l[3]);
+  const u32x4 ah = {h[0], h[1], h[2], h[3]}, al = {l[0], l[1], l[2], l[3]};
+  return WOperand<bf16>{__builtin_bit_cast(bf16x8, ah), __builtin_bit_cast(bf16x8, al)};
+}
+template <> __device__ __forceinline__ WOperand<float> w_operand<float>(const f32x4& p0, const f32x4& p1) {
+  return WOperand<float>{p0, p1};
+}
+__device__ __forceinline__ f32x4 pv_regs(const WOperand<bf16>& w, const bf16x4& lo, const bf16x4& hi, f32x4 acc) {
+  bf16x8 b;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const bf16 h0 = (bf16)p0[r], h1 = (bf16)p1[r];
-    ah[r] = h0; ah[4 + r] = h1;
-    al[r] = (bf16)(p0[r] - (float)h0); al[4 + r] = (bf16)(p1[r] - (float)h1);
     b[r] = lo[r];
     b[4 + r] = hi[r];
   }
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w.hi, b, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w.lo, b, acc, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 pv_split_regs(const f32x4& p0, const f32x4& p1, const f32x4& lo, const f32x4& hi,
-                                               f32x4 acc) {
+__device__ __forceinline__ f32x4 pv_regs(const WOperand<float>& w, const f32x4& lo, const f32x4& hi, f32x4 acc) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p0[r], lo[r], acc, 0, 0, 0);
+  for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w.p0[r], lo[r], acc, 0, 0, 0);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[r], hi[r], acc, 0, 0, 0);
+  for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w.p1[r], hi[r], acc, 0, 0, 0);
   return acc;
 }
 
@@ -273,6 +299,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const float kappa = a.lam / (a.lam + eps);
   const float ik = 1.f / kappa;
   const float sc = LOG2E / (sqrtf((float)d) * eps);
+  const float isc = 1.f / sc;
   const float bsc = -LOG2E / eps;  // bias (pw + w d/(r0 + d)) -> log2 logit
   const float wd = a.w_dist ? a.w_dist[h] : 0.f;
   const bool geo = GEN && a.has_geo != 0 && wd != 0.f;
@@ -310,8 +337,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const float* gt = a.gt + bh * DP * Np;
 
   // Copy of the streamed operand of a sweep of orientation `row` into LDS, batches of
-  // 8 16-byte chunks a thread (all loads of a batch, then its stores).  Loads are
-  // unconditional, from clamped chunk indices.
+  // 8 16-byte chunks a thread (all loads of a batch, then its stores; 16 would spill).
+  // Loads are unconditional, from clamped chunk indices.
   auto stage_operands = [&](bool row) {
     if constexpr (STAGE) {
       typedef __attribute__((__vector_size__(16))) int i32x4;
@@ -320,17 +347,18 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       constexpr int CPR = DP * (int)sizeof(T) / 16;  // chunks of a row-major row
       const int cpt = Np * (int)sizeof(T) / 16;      // chunks of a transposed row
       const int nrm = Np * CPR, ntot = nrm + DP * cpt;
-      for (int e0 = 0; e0 < ntot; e0 += 8 * UNR_NT) {
-        i32x4 v[8];
+      constexpr int SB = 8;
+      for (int e0 = 0; e0 < ntot; e0 += SB * UNR_NT) {
+        i32x4 v[SB];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < SB; ++u) {
           const int e = min(e0 + u * UNR_NT + tid, ntot - 1);
           const T* src = e < nrm ? srow + (size_t)(e / CPR) * DP + (e % CPR) * 8
                                  : scol + (size_t)((e - nrm) / cpt) * Np + ((e - nrm) % cpt) * 8;
           v[u] = *reinterpret_cast<const i32x4*>(src);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < SB; ++u) {
           const int e = e0 + u * UNR_NT + tid;
           if (e >= ntot) continue;
           T* dst = e < nrm ? stg_r + (size_t)(e / CPR) * SRS + (e % CPR) * 8
@@ -408,31 +436,37 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   // the header comment (CS_cent uses k = K).  USE_C (the recurrence term: all but
   // RS(-1) and CS_cent) and TERM2 (the mirror term: all but RS(K-1) and CS_cent) are
   // compile-time, so the element loop carries no test of them.
-  auto sweep = [&](auto row_tag, auto cent_tag, auto usec_tag, auto term2_tag, int k, bool stage_next) -> bool {
-    constexpr bool ROW = decltype(row_tag)::value;
-    constexpr bool CENT = decltype(cent_tag)::value;
-    constexpr bool use_c = decltype(usec_tag)::value;
-    constexpr bool term2 = decltype(term2_tag)::value;
-    const bool publish = ROW ? k >= 0 : (CENT || k >= 1);
-    __syncthreads();  // readers of STA / STB and of the gathered vectors are done
+  // Streamed exponent terms STA / STB of a sweep (flags and k as the sweep's).  Filled
+  // for the next sweep right after a sweep's combine (its main loop is done with them),
+  // so the hist loads share the wait of the exchange and of the operand copy.
+  struct SweepDesc { bool valid, row, cent, use_c, term2; int k; };
+  auto fill_streamed = [&](const SweepDesc& nx) {
     for (int i = tid; i < Np; i += UNR_NT) {
       float sa = NEG_BIG, sb = NEG_BIG;
       if (i < n && valid[i]) {
-        if (ROW) {  // streamed columns j
-          if (use_c) sa = (Vn(k, i) * ik - a.log_nu[bhN + i]) * LOG2E;  // s^{C,k}
-          if (term2 || CENT) sb = Vn(k, i) * LOG2E;                       // s^{R,k+1} or P
-        } else {    // streamed rows i
-          if (CENT) sa = (a.log_u[bhN + i] - a.log_z[bhN + i]) * LOG2E;   // P
+        if (nx.row) {  // streamed columns j
+          if (nx.use_c) sa = (Vn(nx.k, i) * ik - a.log_nu[bhN + i]) * LOG2E;  // s^{C,k}
+          if (nx.term2 || nx.cent) sb = Vn(nx.k, i) * LOG2E;                  // s^{R,k+1} or P
+        } else {       // streamed rows i
+          if (nx.cent) sa = (a.log_u[bhN + i] - a.log_z[bhN + i]) * LOG2E;   // P
           else {
-            sa = (Un(k, i) * ik - a.log_mu[bhN + i]) * LOG2E;             // s^{R,k}
-            sb = Un(k, i) * LOG2E;                                         // s^{C,k}
+            sa = (Un(nx.k, i) * ik - a.log_mu[bhN + i]) * LOG2E;             // s^{R,k}
+            sb = Un(nx.k, i) * LOG2E;                                         // s^{C,k}
           }
         }
       }
       STA[i] = sa;
       STB[i] = sb;
     }
-    __syncthreads();
+  };
+
+  auto sweep = [&](auto row_tag, auto cent_tag, auto usec_tag, auto term2_tag, int k, SweepDesc next) -> bool {
+    constexpr bool ROW = decltype(row_tag)::value;
+    constexpr bool CENT = decltype(cent_tag)::value;
+    constexpr bool use_c = decltype(usec_tag)::value;
+    constexpr bool term2 = decltype(term2_tag)::value;
+    const bool publish = ROW ? k >= 0 : (CENT || k >= 1);
+    __syncthreads();  // STA / STB, the staged operand and the gathered vectors are complete
     const float* STC = ROW ? GLV : GLU;  // streamed recurrence coefficients
     const T* Sop = STAGE ? stg_r : (ROW ? kp : qp);
     const T* Sot = STAGE ? stg_t : (ROW ? kt : qt);
@@ -444,6 +478,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     typename M::Frag cbf[MAXT];
     float ra[MAXT], rb[MAXT], dd[MAXT], xr0[MAXT], xr1[MAXT], xr2[MAXT], Dr[MAXT], gr0[MAXT], gr1[MAXT], gr2[MAXT];
     float red[MAXT][4];  // per accumulator row of a lane: independent chains
+    float cra[MAXT], crb[MAXT];  // ra / sc, rb / sc: the accumulator inits of the cost products
     f32x4 gVa[MAXT][NC];
 #pragma unroll
     for (int s = 0; s < MAXT; ++s) {
@@ -469,6 +504,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           }
         }
       }
+      cra[s] = ra[s] * isc;
+      crb[s] = rb[s] * isc;
       xr0[s] = xs0[ri];
       xr1[s] = xs1[ri];
       xr2[s] = xs2[ri];
@@ -504,8 +541,11 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           load_vt<T>(vt_row, lane, vln[c], vhn[c]);
         }
       };
-      load_pair(part);
+      // staged operands come from LDS: loaded in the iteration itself (a register copy of
+      // a prefetch would cost more than the LDS latency it hides)
+      if (!STAGE) load_pair(part);
       for (int sp = part; sp < n_pairs; sp += wpt) {
+        if (STAGE) load_pair(sp);
         typename MQ::Frag afc[2] = {afn[0], afn[1]};
         V4 vlc[NC], vhc[NC];
 #pragma unroll
@@ -513,7 +553,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           vlc[c] = vln[c];
           vhc[c] = vhn[c];
         }
-        load_pair(sp + wpt);
+        if (!STAGE) load_pair(sp + wpt);
 #pragma unroll
         for (int s = 0; s < MAXT; ++s) {
           const int rt = ts + nts * s;
@@ -535,9 +575,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
             // exponent arguments sc (q.k + ra / sc) + sa_j and sc (q.k + rb / sc) + sb_j: the
             // resident terms ride in the accumulator init, one product per term
             constexpr bool E1 = use_c || (CENT && !ROW), E2 = term2 || (CENT && ROW);
-            const float ca = ra[s] / sc, cb = rb[s] / sc;
-            const f32x4 x1 = E1 ? MQ::qk(af, bf[s], f32x4{ca, ca, ca, ca}) : zero;
-            const f32x4 x2 = E2 ? MQ::qk(af, bf[s], f32x4{cb, cb, cb, cb}) : zero;
+            const f32x4 x1 = E1 ? MQ::qk(af, bf[s], f32x4{cra[s], cra[s], cra[s], cra[s]}) : zero;
+            const f32x4 x2 = E2 ? MQ::qk(af, bf[s], f32x4{crb[s], crb[s], crb[s], crb[s]}) : zero;
             const f32x4 sa = *reinterpret_cast<const f32x4*>(STA + o);
             const f32x4 sb = *reinterpret_cast<const f32x4*>(STB + o);
             const f32x4 scf = use_c ? *reinterpret_cast<const f32x4*>(STC + o) : zero;
@@ -605,12 +644,13 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
               if (ROW && bin >= 0 && W != 0.f) atomicAdd(&s_dpw[bin], W);
             }
           }
+          // dQ += W K (dK += W^T Q): for bf16 inputs W is carried as a bf16 hi + lo pair
+          // against the exact bf16 operand (two bf16 MFMAs), as the forward's P V
+          const WOperand<T> wsp = w_operand<T>(wop[0], wop[1]);
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
-            // dQ += W K (dK += W^T Q): for bf16 inputs W is carried as a bf16 hi + lo pair
-            // against the exact bf16 operand (two bf16 MFMAs), as the forward's P V
-            if (ROW) dQa[s][c] = pv_split_regs(wop[0], wop[1], vlc[c], vhc[c], dQa[s][c]);
-            else dKa[s][c] = pv_split_regs(wop[0], wop[1], vlc[c], vhc[c], dKa[s][c]);
+            if (ROW) dQa[s][c] = pv_regs(wsp, vlc[c], vhc[c], dQa[s][c]);
+            else dKa[s][c] = pv_regs(wsp, vlc[c], vhc[c], dKa[s][c]);
             if (CENT && !ROW)
               gVa[s][c] = M::pv(pop[0], pop[1], gt + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, gVa[s][c]);
           }
@@ -644,7 +684,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     // issued now, past the combine's barrier (no wave reads the region any more), so
     // it overlaps the exchange; CS_cent hands its dV partials over through the same
     // region and stages after that
-    if (stage_next && !(CENT && !ROW)) stage_operands(!ROW);
+    if (next.valid && !(CENT && !ROW)) {
+      stage_operands(next.row);
+      fill_streamed(next);
+    }
     if (publish) {
       // gathered as kappa gl: both readers (the streamed coefficients and the
       // resident dd) want the kappa multiple
@@ -654,9 +697,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     }
     if (CENT && !ROW) {
       write_rows(gVa, a.dv, 1.f);
-      if (stage_next) {
+      if (next.valid) {
         __syncthreads();
-        stage_operands(!ROW);
+        stage_operands(next.row);
+        fill_streamed(next);
       }
     }
     return true;
@@ -665,13 +709,19 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   using TRUE_ = std::integral_constant<bool, true>;
   using FALSE_ = std::integral_constant<bool, false>;
   // (row, cent, use_c, term2)
-  if (!sweep(FALSE_{}, TRUE_{}, FALSE_{}, FALSE_{}, K, true)) return;
-  if (!sweep(TRUE_{}, TRUE_{}, TRUE_{}, FALSE_{}, K - 1, true)) return;
+  // (valid, row, cent, use_c, term2, k) of each sweep, for the fill that precedes it
+  const SweepDesc cs_cent{true, false, true, false, false, K}, rs_cent{true, true, true, true, false, K - 1};
+  auto rs_d = [&](int k) { return SweepDesc{true, true, false, true, true, k}; };
+  auto cs_d = [&](int k) { return SweepDesc{true, false, false, true, true, k}; };
+  const SweepDesc rs_last{true, true, false, false, true, -1}, none{false, false, false, false, false, 0};
+  fill_streamed(cs_cent);
+  if (!sweep(FALSE_{}, TRUE_{}, FALSE_{}, FALSE_{}, K, rs_cent)) return;
+  if (!sweep(TRUE_{}, TRUE_{}, TRUE_{}, FALSE_{}, K - 1, cs_d(K - 1))) return;
   for (int k = K - 1; k >= 0; --k) {
-    if (k < K - 1 && !sweep(TRUE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k, true)) return;
-    if (!sweep(FALSE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k, true)) return;
+    if (k < K - 1 && !sweep(TRUE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k, cs_d(k))) return;
+    if (!sweep(FALSE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k, k >= 1 ? rs_d(k - 1) : rs_last)) return;
   }
-  if (!sweep(TRUE_{}, FALSE_{}, FALSE_{}, TRUE_{}, -1, false)) return;
+  if (!sweep(TRUE_{}, FALSE_{}, FALSE_{}, TRUE_{}, -1, none)) return;
 
   // ---- outputs of my stripe
   const float fs = -1.f / (sqrtf((float)d) * eps);
