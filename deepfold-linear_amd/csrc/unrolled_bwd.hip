@@ -336,35 +336,41 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const float* gp = a.gp + bh * Np * DP;
   const float* gt = a.gt + bh * DP * Np;
 
-  // Copy of the streamed operand of a sweep of orientation `row` into LDS, batches of
-  // 8 16-byte chunks a thread (all loads of a batch, then its stores; 16 would spill).
-  // Loads are unconditional, from clamped chunk indices.
+  // Copy of the streamed operand of a sweep of orientation `row` into LDS: the
+  // row-major copy from L2 (batches of 8 16-byte chunks a thread, all loads of a batch
+  // before its stores; one batch up to Np = 1024), then, after a barrier, the
+  // transposed copy built from it inside LDS (8 bf16 of one column per 16-byte chunk).
+  // Loads are unconditional, from clamped chunk indices.  Every thread calls it.
   auto stage_operands = [&](bool row) {
     if constexpr (STAGE) {
       typedef __attribute__((__vector_size__(16))) int i32x4;
       const T* srow = row ? kp : qp;  // [Np][DP]
-      const T* scol = row ? kt : qt;  // [DP][Np]
       constexpr int CPR = DP * (int)sizeof(T) / 16;  // chunks of a row-major row
-      const int cpt = Np * (int)sizeof(T) / 16;      // chunks of a transposed row
-      const int nrm = Np * CPR, ntot = nrm + DP * cpt;
+      const int nrm = Np * CPR;
       constexpr int SB = 8;
-      for (int e0 = 0; e0 < ntot; e0 += SB * UNR_NT) {
+      for (int e0 = 0; e0 < nrm; e0 += SB * UNR_NT) {
         i32x4 v[SB];
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
-          const int e = min(e0 + u * UNR_NT + tid, ntot - 1);
-          const T* src = e < nrm ? srow + (size_t)(e / CPR) * DP + (e % CPR) * 8
-                                 : scol + (size_t)((e - nrm) / cpt) * Np + ((e - nrm) % cpt) * 8;
-          v[u] = *reinterpret_cast<const i32x4*>(src);
+          const int e = min(e0 + u * UNR_NT + tid, nrm - 1);
+          v[u] = *reinterpret_cast<const i32x4*>(srow + (size_t)(e / CPR) * DP + (e % CPR) * 8);
         }
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
           const int e = e0 + u * UNR_NT + tid;
-          if (e >= ntot) continue;
-          T* dst = e < nrm ? stg_r + (size_t)(e / CPR) * SRS + (e % CPR) * 8
-                           : stg_t + (size_t)((e - nrm) / cpt) * STS + ((e - nrm) % cpt) * 8;
-          *reinterpret_cast<i32x4*>(dst) = v[u];
+          if (e < nrm) *reinterpret_cast<i32x4*>(stg_r + (size_t)(e / CPR) * SRS + (e % CPR) * 8) = v[u];
         }
+      }
+      __syncthreads();
+      // lanes take consecutive columns c of one block of 8 rows: the 2-byte reads of a
+      // wave hit distinct banks (a lane-per-row order would put them all in two)
+      const int cpt = Np / 8;  // 8-element chunks of a transposed row
+      for (int e = tid; e < DP * cpt; e += UNR_NT) {
+        const int c = e % DP, j0 = (e / DP) * 8;
+        T col[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) col[r] = stg_r[(size_t)(j0 + r) * SRS + c];
+        *reinterpret_cast<i32x4*>(stg_t + (size_t)c * STS + j0) = *reinterpret_cast<const i32x4*>(col);
       }
     }
   };
