@@ -341,9 +341,32 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   // before its stores; one batch up to Np = 1024), then, after a barrier, the
   // transposed copy built from it inside LDS (8 bf16 of one column per 16-byte chunk).
   // Loads are unconditional, from clamped chunk indices.  Every thread calls it.
-  auto stage_operands = [&](bool row) {
+  // (valid, row, cent, use_c, term2, k) of a sweep: the fill of its streamed terms
+  // (fill_streamed, or with the operand copy) precedes it
+  struct SweepDesc { bool valid, row, cent, use_c, term2; int k; };
+  // With the operand copy go the next sweep's streamed terms (fill_streamed's values
+  // for this thread's entries i = tid, tid + UNR_NT, which cover Np <= 1024): their raw
+  // loads are issued first, then the copy's, so the two share one wait.
+  auto stage_operands = [&](bool row, const SweepDesc* nx) {
     if constexpr (STAGE) {
       typedef __attribute__((__vector_size__(16))) int i32x4;
+      float f0[2] = {0.f, 0.f}, f1[2] = {0.f, 0.f};
+      if (nx) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int ic = min(tid + u * UNR_NT, N - 1);  // clamped: the loads are unconditional
+          if (nx->row) {
+            f0[u] = Vn(nx->k, ic);
+            f1[u] = a.log_nu[bhN + ic];
+          } else if (nx->cent) {
+            f0[u] = a.log_u[bhN + ic];
+            f1[u] = a.log_z[bhN + ic];
+          } else {
+            f0[u] = Un(nx->k, ic);
+            f1[u] = a.log_mu[bhN + ic];
+          }
+        }
+      }
       const T* srow = row ? kp : qp;  // [Np][DP]
       constexpr int CPR = DP * (int)sizeof(T) / 16;  // chunks of a row-major row
       const int nrm = Np * CPR;
@@ -354,6 +377,27 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
         for (int u = 0; u < SB; ++u) {
           const int e = min(e0 + u * UNR_NT + tid, nrm - 1);
           v[u] = *reinterpret_cast<const i32x4*>(srow + (size_t)(e / CPR) * DP + (e % CPR) * 8);
+        }
+        if (nx && e0 == 0) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int i = tid + u * UNR_NT;
+            if (i >= Np) continue;
+            float sa = NEG_BIG, sb = NEG_BIG;
+            if (i < n && valid[i]) {
+              if (nx->row) {
+                if (nx->use_c) sa = (f0[u] * ik - f1[u]) * LOG2E;
+                if (nx->term2 || nx->cent) sb = f0[u] * LOG2E;
+              } else if (nx->cent) {
+                sa = (f0[u] - f1[u]) * LOG2E;
+              } else {
+                sa = (f0[u] * ik - f1[u]) * LOG2E;
+                sb = f0[u] * LOG2E;
+              }
+            }
+            STA[i] = sa;
+            STB[i] = sb;
+          }
         }
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
@@ -374,7 +418,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       }
     }
   };
-  stage_operands(false);  // the first sweep (CS_cent) streams Q
+  stage_operands(false, nullptr);  // the first sweep (CS_cent) streams Q
 
   f32x4 dQa[MAXT][NC], dKa[MAXT][NC];
   float gbx[MAXT], gby[MAXT], gbz[MAXT], xt0[MAXT], xt1[MAXT], xt2[MAXT], dmu[MAXT], dnu[MAXT];
@@ -445,7 +489,6 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   // Streamed exponent terms STA / STB of a sweep (flags and k as the sweep's).  Filled
   // for the next sweep right after a sweep's combine (its main loop is done with them),
   // so the hist loads share the wait of the exchange and of the operand copy.
-  struct SweepDesc { bool valid, row, cent, use_c, term2; int k; };
   auto fill_streamed = [&](const SweepDesc& nx) {
     for (int i = tid; i < Np; i += UNR_NT) {
       float sa = NEG_BIG, sb = NEG_BIG;
@@ -691,8 +734,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     // it overlaps the exchange; CS_cent hands its dV partials over through the same
     // region and stages after that
     if (next.valid && !(CENT && !ROW)) {
-      stage_operands(next.row);
-      fill_streamed(next);
+      if (STAGE) stage_operands(next.row, &next);
+      else fill_streamed(next);
     }
     if (publish) {
       // gathered as kappa gl: both readers (the streamed coefficients and the
@@ -705,8 +748,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       write_rows(gVa, a.dv, 1.f);
       if (next.valid) {
         __syncthreads();
-        stage_operands(next.row);
-        fill_streamed(next);
+        if (STAGE) stage_operands(next.row, &next);
+        else fill_streamed(next);
       }
     }
     return true;
