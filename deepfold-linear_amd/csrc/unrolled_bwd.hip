@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   constexpr int NW = UNR_NW;
   constexpr int MAXT = unr_maxt<DP>();
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_flag, s_tmp;
+  __shared__ int s_flag, s_tmp, s_local;
   __shared__ float s_pw[68];   // pos_weight of this head (natural units)
   __shared__ float s_dpw[68];  // d pos_weight partial of this workgroup (times eps)
   int grp, member;
@@ -226,7 +226,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   const int BH = a.B * a.H;
   const size_t bh = (size_t)grp;
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, g = lane >> 4;
-  if (tid == 0) s_flag = 0;
+  if (tid == 0) {
+    s_flag = 0;
+    s_local = 1;
+  }
   if (tid < 68) {
     s_pw[tid] = a.pos_w ? a.pos_w[h * 68 + tid] : 0.f;
     s_dpw[tid] = 0.f;
@@ -434,6 +437,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   uint64_t* xgv = xgu + Np;
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
+  // placement words of the group (after all (b,h)'s exchange words): plain-store
+  // publishing from the second exchange on if every member runs on its XCD
+  uint64_t* xpl = a.xch + (size_t)BH * 4 * Np + bh * 32;
+  bool local = false;
 
   auto write_rows = [&](f32x4 (&acc)[MAXT][NC], void* out, float scale) {  // gradients in the input type
     __syncthreads();
@@ -719,7 +726,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       const int i = r_lo + q;
       if (i >= n) return;
       const bool ok = valid[i];
-      if (publish) xch_put(buf + i, v, tag);
+      if (publish) xch_put(buf + i, v, tag, local);
       if (!ok) return;
       if (ROW) {
         if (k >= 0) ldmu[q] += kappa * v;
@@ -763,8 +770,12 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   auto rs_d = [&](int k) { return SweepDesc{true, true, false, true, true, k}; };
   auto cs_d = [&](int k) { return SweepDesc{true, false, false, true, true, k}; };
   const SweepDesc rs_last{true, true, false, false, true, -1}, none{false, false, false, false, false, 0};
+  publish_placement(xpl, member, a.salt);
   fill_streamed(cs_cent);
   if (!sweep(FALSE_{}, TRUE_{}, FALSE_{}, FALSE_{}, K, rs_cent)) return;
+  // every member published its placement before its words of the first exchange
+  if (!read_placement(xpl, a.G, n_tiles, a.salt, a.err, &s_flag, &s_local)) return;
+  local = s_local != 0;
   if (!sweep(TRUE_{}, TRUE_{}, TRUE_{}, FALSE_{}, K - 1, cs_d(K - 1))) return;
   for (int k = K - 1; k >= 0; --k) {
     if (k < K - 1 && !sweep(TRUE_{}, FALSE_{}, TRUE_{}, TRUE_{}, k, cs_d(k))) return;
