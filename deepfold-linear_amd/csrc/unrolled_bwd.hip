@@ -318,19 +318,48 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     return a.v_init ? a.v_init[bhN + j] : 0.f;
   };
 
-  // Wave -> resident tiles.  nr <= NW: wave takes tile wave % nr as part wave / nr of
-  // the wpt_of(tile) waves of that tile (one slot; every wave busy, and for nr = 3 the
-  // two waves of a SIMD, w and w + 4, take different tiles so that no SIMD carries
-  // two whole shares); nr > NW: wave owns tiles wave and wave + NW (slots 0 and 1).
+  // Wave -> resident tiles and streamed pairs.  Waves w and w + 4 of a workgroup share
+  // a SIMD, and a SIMD's main-loop time follows the work of its two waves together
+  // (one wave alone issues as fast as two), so the work is balanced per SIMD:
+  //  - nr <= 4: the nr * n_pairs (tile, pair) units are cut into four equal ranges in
+  //    SIMD order; a SIMD's range is split between its two waves at the tile boundary
+  //    it contains, else at its middle, so that every wave takes one tile and a
+  //    contiguous pair range of it;
+  //  - 4 < nr <= NW: wave takes tile wave % nr, and of its pairs every
+  //    (NW - tile + nr - 1) / nr-th from wave / nr (the waves of a tile interleave);
+  //  - nr > NW: wave owns tiles wave and wave + NW (slots 0 and 1), all pairs.
+  // Each tile's partial sums are then combined over the waves of tile_mask(tile).
   const bool spread = nr <= NW;
-  const int ts = spread ? wave % nr : wave;
-  const int part = spread ? wave / nr : 0;
-  auto wpt_of = [&](int rt) { return spread ? (NW - rt + nr - 1) / nr : 1; };
-  const int wpt = wpt_of(ts);                // this wave's stride over streamed pairs
-  const int nts = spread ? nr : NW;          // slot s holds tile ts + nts s
-  auto wave_of = [&](int rt, int p) { return spread ? rt + p * nr : rt % NW; };  // part p of tile rt
-  auto slot_of = [&](int rt) { return spread ? 0 : rt / NW; };
   const int n_pairs = (n_tiles + 1) / 2;
+  auto work_of = [&](int w, int& tile, int& p0, int& p1, int& step) {
+    if (!spread) {
+      tile = w; p0 = 0; p1 = n_pairs; step = 1;
+    } else if (nr <= 4) {
+      const int U = nr * n_pairs, o = 2 * (w & 3) + (w >> 2);
+      const int sb = (o >> 1) * U / 4, se = ((o >> 1) + 1) * U / 4;
+      const int tb = (sb / n_pairs + 1) * n_pairs;  // first tile boundary after sb
+      const int cut = tb < se ? tb : (sb + se) / 2;
+      const int ub = (o & 1) ? cut : sb, ue = (o & 1) ? se : cut;
+      tile = min(ub / n_pairs, nr - 1);
+      p0 = ub - tile * n_pairs; p1 = ue - tile * n_pairs; step = 1;
+    } else {
+      tile = w % nr; p0 = w / nr; p1 = n_pairs; step = (NW - tile + nr - 1) / nr;
+    }
+  };
+  int ts, wp0, wp1, wstep;
+  work_of(wave, ts, wp0, wp1, wstep);
+  uint64_t tmasks = 0;  // byte rt: the waves holding partials of tile rt (spread)
+  if (spread)
+    for (int w = 0; w < NW; ++w) {
+      int t_, a_, b_, c_;
+      work_of(w, t_, a_, b_, c_);
+      tmasks |= 1ull << (8 * t_ + w);
+    }
+  auto tile_mask = [&](int rt) -> unsigned { return spread ? (unsigned)(tmasks >> (8 * rt)) & 0xffu : 1u << (rt % NW); };
+  const int nts = spread ? nr : NW;  // slot s holds tile ts + nts s
+  auto slot_of = [&](int rt) { return spread ? 0 : rt / NW; };
+  // the wave that writes tile ts's rows (the lowest of its tile's waves)
+  const bool lead = (tile_mask(ts) & ((1u << wave) - 1u)) == 0u;
   const T* qp = static_cast<const T*>(a.qp) + bh * Np * DP;
   const T* kp = static_cast<const T*>(a.kp) + bh * Np * DP;
   const T* qt = static_cast<const T*>(a.qt) + bh * DP * Np;
@@ -444,14 +473,14 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
 
   auto write_rows = [&](f32x4 (&acc)[MAXT][NC], void* out, float scale) {  // gradients in the input type
     __syncthreads();
-    if (part > 0) {
+    if (!lead) {
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int r = 0; r < 4; ++r) spart[(size_t)wave * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)] = acc[0][c][r];
     }
     __syncthreads();
-    if (part == 0) {
+    if (lead) {
 #pragma unroll
       for (int s = 0; s < MAXT; ++s) {
         const int rt = ts + nts * s;
@@ -461,8 +490,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float v = acc[s][c][r];
-            for (int p = 1; p < wpt_of(rt); ++p)
-              v += spart[(size_t)wave_of(rt, p) * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)];
+            for (unsigned m = tile_mask(rt) & ~(1u << wave); m; m &= m - 1u)
+              v += spart[(size_t)__builtin_ctz(m) * 16 * DP + (4 * g + r) * DP + c * 16 + (lane & 15)];
             const int row = (t0 + rt) * 16 + 4 * g + r, col = c * 16 + (lane & 15);
             if (row < N && col < d)
               static_cast<T*>(out)[(bh * N + row) * d + col] = from_f32<T>((row < n && valid[row]) ? scale * v : 0.f);
@@ -483,7 +512,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     for (int q = tid; q < nr * 16; q += UNR_NT) {
       const int rt = q >> 4, l16 = q & 15;
       float v = 0.f;
-      for (int p = 0; p < wpt_of(rt); ++p) v += sred[(wave_of(rt, p) * MAXT + slot_of(rt)) * 16 + l16];
+      for (unsigned m = tile_mask(rt); m; m &= m - 1u) v += sred[(__builtin_ctz(m) * MAXT + slot_of(rt)) * 16 + l16];
       dst_fn(q, v);
     }
   };
@@ -581,7 +610,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       // The streamed operands of a pair of tiles (Q or K fragments for the cost, the
       // transposed operand for dQ / dK) come from global memory (L2): they are the same
       // for every resident slot, so they are loaded once per pair, and one pair ahead:
-      // the loads of pair sp + wpt are issued (unconditionally, from a clamped pair)
+      // the loads of pair sp + wstep are issued (unconditionally, from a clamped pair)
       // before pair sp is computed.
       using V4 = typename VtQuad<T>::type;
       typename MQ::Frag afn[2];
@@ -599,8 +628,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       };
       // staged operands come from LDS: loaded in the iteration itself (a register copy of
       // a prefetch would cost more than the LDS latency it hides)
-      if (!STAGE) load_pair(part);
-      for (int sp = part; sp < n_pairs; sp += wpt) {
+      if (!STAGE) load_pair(wp0);
+      for (int sp = wp0; sp < wp1; sp += wstep) {
         if (STAGE) load_pair(sp);
         typename MQ::Frag afc[2] = {afn[0], afn[1]};
         V4 vlc[NC], vhc[NC];
@@ -609,7 +638,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           vlc[c] = vln[c];
           vhc[c] = vhn[c];
         }
-        if (!STAGE) load_pair(sp + wpt);
+        if (!STAGE) load_pair(sp + wstep);
 #pragma unroll
         for (int s = 0; s < MAXT; ++s) {
           const int rt = ts + nts * s;
@@ -817,9 +846,9 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   for (int q = tid; q < nr * 16; q += UNR_NT) {
     const int rt = q >> 4, l16 = q & 15;
     float v[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < wpt_of(rt); ++p)
+    for (unsigned m = tile_mask(rt); m; m &= m - 1u)
       for (int t = 0; t < 6; ++t)
-        v[t] += spart[((size_t)(wave_of(rt, p) * MAXT + slot_of(rt)) * 16 + l16) * 6 + t];
+        v[t] += spart[((size_t)(__builtin_ctz(m) * MAXT + slot_of(rt)) * 16 + l16) * 6 + t];
     const int i = r_lo + q;
     if (i < N) {
       const bool ok = i < n && valid[i];
