@@ -54,12 +54,12 @@ int balanced_max_tiles(int DP);
 hipError_t launch_balanced_prep(const BalPrepArgs& p, int DP, hipStream_t stream);
 hipError_t launch_balanced_bwd(const BalBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop);
 hipError_t launch_balanced_finalize(const BalBwdArgs& a, float* dx, float* dalpha, float* dr, hipStream_t stream);
-size_t unrolled_bwd_lds_bytes(int N, int DP, int elem, bool stage);
-bool unrolled_can_stage(int N, int DP, int elem, size_t limit);
+size_t unrolled_bwd_lds_bytes(int N, int DP, int elem, int ops);
+int unrolled_operand_mode(int N, int DP, int elem, size_t limit);
 int unrolled_max_tiles(int DP);
 hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipStream_t stream);
 hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop,
-                               bool stage);
+                               int ops);
 hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream);
 }  // namespace dfl
 
@@ -1069,8 +1069,8 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
     return fail("unrolled backward: N=%d over %d workgroups per (b,h) exceeds %d tiles of 16 rows each", p->N, G,
                 dfl::unrolled_max_tiles(DP));
   const int elem = p->dtype == DFL_BF16 ? 2 : 4;
-  const bool stage = dfl::unrolled_can_stage(p->N, DP, elem, LDS_LIMIT);
-  const size_t lds = dfl::unrolled_bwd_lds_bytes(p->N, DP, elem, stage);
+  const int ops = dfl::unrolled_operand_mode(p->N, DP, elem, LDS_LIMIT);
+  const size_t lds = dfl::unrolled_bwd_lds_bytes(p->N, DP, elem, ops);
   if (lds > LDS_LIMIT)
     return fail("unrolled backward: N=%d needs %zu bytes of LDS per workgroup (limit %zu)", p->N, lds, LDS_LIMIT);
   unsigned char* ws = static_cast<unsigned char*>(workspace);
@@ -1108,7 +1108,7 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
   if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
     return hip_fail((hipError_t)rc, "workspace clear launch");
   e = dfl::launch_unrolled_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H),
-                               stage);
+                               ops);
   if (e != hipSuccess) return hip_fail(e, "unrolled backward launch");
   e = dfl::launch_unrolled_finalize(a, p->x_res ? p->dx_res : nullptr, p->dpos_weight, p->dw_dist,
                                     (hipStream_t)stream);

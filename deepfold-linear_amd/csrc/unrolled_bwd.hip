@@ -201,14 +201,59 @@ __device__ __forceinline__ f32x4 pv_regs(const WOperand<float>& w, const f32x4& 
 // over the part hand-over region.  The copy for the next sweep is issued right after
 // a sweep's combine, so its loads overlap the exchange wait; the main loops then read
 // LDS instead of waiting on L2.
+// Operand modes of the kernel: streamed operands read from L2 (GLOBAL), a sweep's
+// streamed operand staged in LDS (STAGE), or Q and K resident in LDS (RES).
+constexpr int UNR_OPS_GLOBAL = 0, UNR_OPS_STAGE = 1, UNR_OPS_RES = 2;
 template <typename T, int DP> constexpr int unr_srs() { return DP + 16 / (int)sizeof(T); }
 __host__ __device__ inline size_t unr_stage_bytes(int Np, int DP, int elem) {
   const int pad = 16 / elem;
   return ((size_t)Np * (DP + pad) + (size_t)DP * (Np + pad)) * elem;
 }
+// Floats of the part hand-over region: the write_rows hand-over [NW][16][64] (which
+// also holds the dx hand-over [NW][2][16][6]), [NW][16][32] with resident operands,
+// or (STAGE) a sweep's staged operands if larger.
+__host__ __device__ inline int unr_region_floats(int Np, int DP, int elem, int ops) {
+  if (ops == UNR_OPS_RES) return UNR_NW * 16 * DP;
+  const int base = UNR_NW * 16 * 64;
+  if (ops == UNR_OPS_STAGE) {
+    const int st = (int)(unr_stage_bytes(Np, DP, elem) / 4);
+    return base > st ? base : st;
+  }
+  return base;
+}
 
-template <typename T, int DP, bool GEN, bool STAGE>
+// Resident operands (OPS = UNR_OPS_RES: bf16 inputs, DP = 32, when LDS has room): Q and
+// K stay in LDS for the whole launch, row-major [Np][32] bf16 without padding, under a
+// swizzle that keeps both of their readers free of bank conflicts (64 banks of 4 bytes):
+//   row j lies in 256-byte line L = j / 4, at 64-byte window (j + L) mod 4 of it, and its
+//   16-byte chunk q (columns 8q .. 8q + 7) at chunk position q ^ sw(L),
+//   sw(L) = 2 (L mod 2) + (L / 2 mod 2).
+// Readers: the cost products' fragments (a lane reads 16 bytes of row l % 16 of a 16-row
+// tile, chunk l / 16) and the transposed reads of the dQ / dK products
+// (ds_read_b64_tr_b16: in each 16-lane block, source lane 4i + s reads 4 columns 4s ..
+// 4s + 3 of row i of a 4-row block, and output lane t receives column t of the block's
+// rows 0..3 -- the B operand of the 16x16x32 MFMA for 4 consecutive streamed rows).
+__device__ __forceinline__ int res_off(int j, int c) {  // element offset of (row j, column c)
+  const int L = j >> 2;
+  const int sw = ((L & 1) << 1) | ((L >> 1) & 1);
+  return L * 128 + ((j + L) & 3) * 32 + (((c >> 3) ^ sw) << 3) + (c & 7);
+}
+// 4 consecutive rows j0 + 4 (l / 16) .. + 3 of column cb * 16 + l % 16 (a lane's share of
+// the B operand for streamed rows j0 + 4 (l / 16) + i, i = 0..3)
+__device__ __forceinline__ bf16x4 res_tr4(const bf16* op, int j0, int cb, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4* lds_s16x4;
+  const int g = lane >> 4, t = lane & 15;
+  const bf16* src = op + res_off(j0 + 4 * g + (t >> 2), cb * 16 + 4 * (t & 3));
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(src));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+template <typename T, int DP, bool GEN, int OPS>
 __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
+  constexpr bool STAGE = OPS == UNR_OPS_STAGE;
+  constexpr bool RES = OPS == UNR_OPS_RES;
+  static_assert(!RES || (sizeof(T) == 2 && DP == 32), "resident operands: bf16, DP = 32");
   using M = Mfma<float, DP>;
   using MQ = Mfma<T, DP>;
   constexpr int NC = DP / 16;
@@ -216,6 +261,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   constexpr int MAXT = unr_maxt<DP>();
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_flag, s_tmp, s_local;
+  __shared__ int s_exact;  // number of a sweep whose factors are out of range (exact path)
   __shared__ float s_pw[68];   // pos_weight of this head (natural units)
   __shared__ float s_dpw[68];  // d pos_weight partial of this workgroup (times eps)
   int grp, member;
@@ -229,6 +275,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   if (tid == 0) {
     s_flag = 0;
     s_local = 1;
+    s_exact = -1;
   }
   if (tid < 68) {
     s_pw[tid] = a.pos_w ? a.pos_w[h * 68 + tid] : 0.f;
@@ -250,17 +297,20 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   float* GLV = GLU + Np;
   float* STA = GLV + Np;  // streamed exponent terms of term 1 (or of P in CS_cent)
   float* STB = STA + Np;  // streamed exponent terms of term 2 (or of P in RS(K-1))
-  float* sred = STB + Np;                        // [NW][MAXT][16]
+  float* STG = STB + Np;  // exp2(STB - STA) of a sweep with both terms (the column factor)
+  float* sred = STG + Np;                        // [NW][MAXT][16]
   float* spart = sred + NW * UNR_MAXT_ANY * 16;  // [NW][16*64] part hand-over
   // part hand-over [NW][16*64], or (STAGE) the staged operands of a sweep
   constexpr int SRS = unr_srs<T, DP>();          // row stride of the staged row-major operand
   const int STS = Np + 16 / (int)sizeof(T);      // row stride of the staged transposed operand
-  const int region = STAGE ? max(NW * 16 * 64, (int)(unr_stage_bytes(Np, DP, sizeof(T)) / 4)) : NW * 16 * 64;
+  const int region = unr_region_floats(Np, DP, (int)sizeof(T), OPS);
   T* stg_r = reinterpret_cast<T*>(spart);
   T* stg_t = stg_r + (size_t)Np * SRS;
   float* sscal = spart + region;                 // [NW]
   float* ldmu = sscal + NW;                      // d log_mu of my rows, summed over the sweeps
   float* ldnu = ldmu + UNR_MAX_LOCAL;            // d log_nu of my columns
+  T* opq = reinterpret_cast<T*>(ldnu + UNR_MAX_LOCAL);  // RES: Q, then K, swizzled [Np][32]
+  T* opk = opq + (size_t)Np * DP;
 
   const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &s_tmp);
   const int n_tiles = (n + 15) / 16;
@@ -297,6 +347,18 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     GLV[i] = 0.f;
   }
   for (int q = tid; q < UNR_MAX_LOCAL; q += UNR_NT) ldmu[q] = ldnu[q] = 0.f;
+  if constexpr (RES) {  // Q and K into LDS, swizzled (16-byte chunks)
+    typedef __attribute__((__vector_size__(16))) int i32x4;
+    const T* gq = static_cast<const T*>(a.qp) + bh * Np * DP;
+    const T* gk = static_cast<const T*>(a.kp) + bh * Np * DP;
+    for (int e = tid; e < Np * 4; e += UNR_NT) {
+      const int j = e >> 2, q = e & 3;
+      const i32x4 vq = *reinterpret_cast<const i32x4*>(gq + (size_t)j * DP + 8 * q);
+      const i32x4 vk = *reinterpret_cast<const i32x4*>(gk + (size_t)j * DP + 8 * q);
+      *reinterpret_cast<i32x4*>(opq + res_off(j, 8 * q)) = vq;
+      *reinterpret_cast<i32x4*>(opk + res_off(j, 8 * q)) = vk;
+    }
+  }
   __syncthreads();
   const float eps = a.eps[h];
   const float kappa = a.lam / (a.lam + eps);
@@ -379,6 +441,22 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   // With the operand copy go the next sweep's streamed terms (fill_streamed's values
   // for this thread's entries i = tid, tid + UNR_NT, which cover Np <= 1024): their raw
   // loads are issued first, then the copy's, so the two share one wait.
+  // Sweeps with both terms (use_c and term2, no centroid): the two exponentials of an
+  // element differ by a row factor times a column factor,
+  //   exp2(x sc + sb_j) = exp2(x sc + sa_j) * exp2(sb_j - sa_j) * exp2(rb_i - ra_i)
+  // (the cost and the bias are common), so such a sweep takes one exponential an
+  // element and no second cost product.  The column factors exp2(sb_j - sa_j) are
+  // kept in STG; a sweep with a factor outside [2^-FLIM, 2^FLIM] (row or column) takes
+  // the exact two-exponential path instead (s_exact holds its number, rows are checked
+  // per wave), so that no factor product can overflow or hide a term.
+  constexpr float FLIM = 40.f;
+  int sweep_no = 0;  // number of the running sweep (1, 2, ...); the fills are for the next
+  auto both_factor = [&](const SweepDesc& nx, bool ok, float sa, float sb) -> float {
+    if (!(nx.use_c && nx.term2 && !nx.cent) || !ok) return 0.f;
+    const float dl = sb - sa;
+    if (!(fabsf(dl) <= FLIM)) s_exact = sweep_no + 1;
+    return fast_exp2(fminf(fmaxf(dl, -FLIM), FLIM));
+  };
   auto stage_operands = [&](bool row, const SweepDesc* nx) {
     if constexpr (STAGE) {
       typedef __attribute__((__vector_size__(16))) int i32x4;
@@ -429,6 +507,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
             }
             STA[i] = sa;
             STB[i] = sb;
+            STG[i] = both_factor(*nx, i < n && valid[i], sa, sb);
           }
         }
 #pragma unroll
@@ -542,6 +621,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       }
       STA[i] = sa;
       STB[i] = sb;
+      STG[i] = both_factor(nx, i < n && valid[i], sa, sb);
     }
   };
 
@@ -551,6 +631,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     constexpr bool use_c = decltype(usec_tag)::value;
     constexpr bool term2 = decltype(term2_tag)::value;
     const bool publish = ROW ? k >= 0 : (CENT || k >= 1);
+    constexpr bool BOTH = use_c && term2 && !CENT;  // one exponential an element (see STG)
+    ++sweep_no;
     __syncthreads();  // STA / STB, the staged operand and the gathered vectors are complete
     const float* STC = ROW ? GLV : GLU;  // streamed recurrence coefficients
     const T* Sop = STAGE ? stg_r : (ROW ? kp : qp);
@@ -564,13 +646,16 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     float ra[MAXT], rb[MAXT], dd[MAXT], xr0[MAXT], xr1[MAXT], xr2[MAXT], Dr[MAXT], gr0[MAXT], gr1[MAXT], gr2[MAXT];
     float red[MAXT][4];  // per accumulator row of a lane: independent chains
     float cra[MAXT], crb[MAXT];  // ra / sc, rb / sc: the accumulator inits of the cost products
+    float gam[MAXT];             // BOTH: row factor exp2(rb - ra) times dd
+    bool row_out = false;        // BOTH: a row factor of this wave is out of range
     f32x4 gVa[MAXT][NC];
 #pragma unroll
     for (int s = 0; s < MAXT; ++s) {
       const int rt = ts + nts * s;
       const int ri = (t0 + min(rt, nr - 1)) * 16 + (lane & 15);
       const bool ok = rt < nr && ri < n && valid[ri];
-      MQ::load(bf[s], Rop + (size_t)ri * DP, lane);
+      if constexpr (RES) bf[s].v[0] = *reinterpret_cast<const bf16x8*>((ROW ? opq : opk) + res_off(ri, 8 * (lane >> 4)));
+      else MQ::load(bf[s], Rop + (size_t)ri * DP, lane);
       if (CENT) M::load(cbf[s], (ROW ? gp : vp) + (size_t)ri * DP, lane);
       ra[s] = rb[s] = NEG_BIG;
       dd[s] = 0.f;
@@ -591,6 +676,12 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       }
       cra[s] = ra[s] * isc;
       crb[s] = rb[s] * isc;
+      gam[s] = 0.f;
+      if (BOTH && ok) {
+        const float dl = rb[s] - ra[s];
+        row_out |= !(fabsf(dl) <= FLIM);
+        gam[s] = fast_exp2(fminf(fmaxf(dl, -FLIM), FLIM)) * dd[s];
+      }
       xr0[s] = xs0[ri];
       xr1[s] = xs1[ri];
       xr2[s] = xs2[ri];
@@ -617,6 +708,18 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       V4 vln[NC], vhn[NC];
       auto load_pair = [&](int sp_) {
         const int spc = min(sp_, n_pairs - 1);
+        if constexpr (RES) {
+          const T* so = ROW ? opk : opq;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+            afn[hh].v[0] = *reinterpret_cast<const bf16x8*>(so + res_off((2 * spc + hh) * 16 + (lane & 15), 8 * (lane >> 4)));
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            vln[c] = res_tr4(so, 32 * spc, c, lane);
+            vhn[c] = res_tr4(so, 32 * spc + 16, c, lane);
+          }
+          return;
+        }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
           MQ::load(afn[hh], Sop + (size_t)((2 * spc + hh) * 16 + (lane & 15)) * sop_rs, lane);
@@ -628,9 +731,12 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       };
       // staged operands come from LDS: loaded in the iteration itself (a register copy of
       // a prefetch would cost more than the LDS latency it hides)
-      if (!STAGE) load_pair(wp0);
+      auto main_loop = [&](auto fast_tag) {
+      // FAST (BOTH sweeps with factors in range): e2 = e1 * STG_j * exp2(rb - ra)
+      constexpr bool FAST = decltype(fast_tag)::value;
+      if (!STAGE && !RES) load_pair(wp0);
       for (int sp = wp0; sp < wp1; sp += wstep) {
-        if (STAGE) load_pair(sp);
+        if (STAGE || RES) load_pair(sp);
         typename MQ::Frag afc[2] = {afn[0], afn[1]};
         V4 vlc[NC], vhc[NC];
 #pragma unroll
@@ -638,7 +744,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           vlc[c] = vln[c];
           vhc[c] = vhn[c];
         }
-        if (!STAGE) load_pair(sp + wstep);
+        if (!STAGE && !RES) load_pair(sp + wstep);
 #pragma unroll
         for (int s = 0; s < MAXT; ++s) {
           const int rt = ts + nts * s;
@@ -661,9 +767,9 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
             // resident terms ride in the accumulator init, one product per term
             constexpr bool E1 = use_c || (CENT && !ROW), E2 = term2 || (CENT && ROW);
             const f32x4 x1 = E1 ? MQ::qk(af, bf[s], f32x4{cra[s], cra[s], cra[s], cra[s]}) : zero;
-            const f32x4 x2 = E2 ? MQ::qk(af, bf[s], f32x4{crb[s], crb[s], crb[s], crb[s]}) : zero;
+            const f32x4 x2 = (E2 && !FAST) ? MQ::qk(af, bf[s], f32x4{crb[s], crb[s], crb[s], crb[s]}) : zero;
             const f32x4 sa = *reinterpret_cast<const f32x4*>(STA + o);
-            const f32x4 sb = *reinterpret_cast<const f32x4*>(STB + o);
+            const f32x4 sb = *reinterpret_cast<const f32x4*>((FAST ? STG : STB) + o);  // FAST: column factors
             const f32x4 scf = use_c ? *reinterpret_cast<const f32x4*>(STC + o) : zero;
             const f32x4 sx0 = *reinterpret_cast<const f32x4*>(xs0 + o);
             const f32x4 sx1 = *reinterpret_cast<const f32x4*>(xs1 + o);
@@ -694,14 +800,20 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
               }
               const float bb = GEN ? bsc * bias : 0.f;
               const float e1 = E1 ? fast_exp2(__builtin_fmaf(x1[e], sc, GEN ? sa[e] + bb : sa[e])) : 0.f;
-              const float e2 = E2 ? fast_exp2(__builtin_fmaf(x2[e], sc, GEN ? sb[e] + bb : sb[e])) : 0.f;
+              const float e2 = (E2 && !FAST) ? fast_exp2(__builtin_fmaf(x2[e], sc, GEN ? sb[e] + bb : sb[e])) : 0.f;
               float W = 0.f;
-              if (use_c) {
-                const float t1 = e1 * scf[e];  // scf holds kappa gl (scaled when gathered)
-                W = t1;
-                red[s][e] -= t1;
+              if (FAST) {
+                // W = e1 scf_j + e2 dd_i = e1 (scf_j + STG_j exp2(rb_i - ra_i) dd_i)
+                W = e1 * __builtin_fmaf(gam[s], sb[e], scf[e]);
+                red[s][e] = __builtin_fmaf(-e1, scf[e], red[s][e]);
+              } else {
+                if (use_c) {
+                  const float t1 = e1 * scf[e];  // scf holds kappa gl (scaled when gathered)
+                  W = t1;
+                  red[s][e] -= t1;
+                }
+                if (term2) W = __builtin_fmaf(e2, dd[s], W);
               }
-              if (term2) W = __builtin_fmaf(e2, dd[s], W);
               if (CENT) {
                 const float P = ROW ? e2 : e1;
                 float dT = t[e];
@@ -740,6 +852,13 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
               gVa[s][c] = M::pv(pop[0], pop[1], gt + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, gVa[s][c]);
           }
         }
+      }
+      };
+      if constexpr (BOTH) {
+        if (s_exact != sweep_no && !__any(row_out)) main_loop(std::integral_constant<bool, true>{});
+        else main_loop(std::integral_constant<bool, false>{});
+      } else {
+        main_loop(std::integral_constant<bool, false>{});
       }
     }
     // recurrence output (gl_u^k for RS, gl_v^{k-1} or g_v for CS) of my rows
@@ -863,20 +982,25 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   }
 }
 
-size_t unrolled_bwd_lds_bytes(int N, int DP, int elem, bool stage) {
+size_t unrolled_bwd_lds_bytes(int N, int DP, int elem, int ops) {
   const size_t Np = ((N + 31) / 32) * 32;
   size_t bytes = ((Np + 15) / 16) * 16;
-  bytes += 11 * Np * 4;                              // coordinates, grad x_c, D, gathered vectors, STA, STB
+  bytes += 12 * Np * 4;                              // coordinates, grad x_c, D, gathered vectors, STA, STB, STG
   bytes += (size_t)UNR_NW * UNR_MAXT_ANY * 16 * 4;   // recurrence partials
-  // part hand-over (>= the dx hand-over), or a sweep's staged operands (4-byte units)
-  bytes += 4 * std::max((size_t)UNR_NW * 16 * 64, stage ? unr_stage_bytes((int)Np, DP, elem) / 4 : (size_t)0);
+  bytes += 4 * (size_t)unr_region_floats((int)Np, DP, elem, ops);  // part hand-over / staged operand
   bytes += UNR_NW * 4;
   bytes += 2 * UNR_MAX_LOCAL * 4;                    // d log_mu, d log_nu of the stripe
+  if (ops == UNR_OPS_RES) bytes += 2 * Np * DP * (size_t)elem;  // resident Q and K
   return bytes;
 }
 
-bool unrolled_can_stage(int N, int DP, int elem, size_t limit) {
-  return elem == 2 && DP == 32 && unrolled_bwd_lds_bytes(N, DP, elem, true) <= limit;
+// Resident operands if they fit, else a staged streamed operand if that fits (bf16,
+// DP = 32), else operands from L2.
+int unrolled_operand_mode(int N, int DP, int elem, size_t limit) {
+  if (elem != 2 || DP != 32) return UNR_OPS_GLOBAL;
+  if (unrolled_bwd_lds_bytes(N, DP, elem, UNR_OPS_RES) <= limit) return UNR_OPS_RES;
+  if (unrolled_bwd_lds_bytes(N, DP, elem, UNR_OPS_STAGE) <= limit) return UNR_OPS_STAGE;
+  return UNR_OPS_GLOBAL;
 }
 
 int unrolled_max_tiles(int DP) { return (DP <= 32 ? unr_maxt<32>() : unr_maxt<64>()) * UNR_NW; }
@@ -900,9 +1024,9 @@ hipError_t launch_unrolled_prep(const UnrPrepArgs& p, bool bf16_in, int DP, hipS
   return hipErrorInvalidValue;
 }
 
-template <typename T, int DP, bool GEN, bool STAGE>
+template <typename T, int DP, bool GEN, int OPS>
 static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  auto kern = unrolled_bwd_kernel<T, DP, GEN, STAGE>;
+  auto kern = unrolled_bwd_kernel<T, DP, GEN, OPS>;
   hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   dim3 grid(grid_blocks(a.B * a.H, a.G)), block(UNR_NT);
@@ -916,28 +1040,28 @@ static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stre
 }
 
 template <typename T>
-static hipError_t launch_unr_dt(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop, bool stage) {
+static hipError_t launch_unr_dt(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop, int ops) {
   const bool gen = (a.bins8 && a.pos_w) || (a.has_geo && a.w_dist);
+  constexpr int G0 = UNR_OPS_GLOBAL, ST = UNR_OPS_STAGE, RS = UNR_OPS_RES;
   if constexpr (sizeof(T) == 2) {
-    if (stage && DP == 32)
-      return gen ? launch_unr_t<T, 32, true, true>(a, lds, stream, coop)
-                 : launch_unr_t<T, 32, false, true>(a, lds, stream, coop);
+    if (ops == RS && DP == 32)
+      return gen ? launch_unr_t<T, 32, true, RS>(a, lds, stream, coop) : launch_unr_t<T, 32, false, RS>(a, lds, stream, coop);
+    if (ops == ST && DP == 32)
+      return gen ? launch_unr_t<T, 32, true, ST>(a, lds, stream, coop) : launch_unr_t<T, 32, false, ST>(a, lds, stream, coop);
   }
-  if (stage) return hipErrorInvalidValue;
+  if (ops != G0) return hipErrorInvalidValue;
   if (DP == 32)
-    return gen ? launch_unr_t<T, 32, true, false>(a, lds, stream, coop)
-               : launch_unr_t<T, 32, false, false>(a, lds, stream, coop);
+    return gen ? launch_unr_t<T, 32, true, G0>(a, lds, stream, coop) : launch_unr_t<T, 32, false, G0>(a, lds, stream, coop);
   if (DP == 64)
-    return gen ? launch_unr_t<T, 64, true, false>(a, lds, stream, coop)
-               : launch_unr_t<T, 64, false, false>(a, lds, stream, coop);
+    return gen ? launch_unr_t<T, 64, true, G0>(a, lds, stream, coop) : launch_unr_t<T, 64, false, G0>(a, lds, stream, coop);
   return hipErrorInvalidValue;
 }
 
-// stage: unrolled_can_stage() said yes and lds was sized with it
+// ops: from unrolled_operand_mode(), with lds sized for it
 hipError_t launch_unrolled_bwd(const UnrBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop,
-                               bool stage) {
-  return bf16_in ? launch_unr_dt<bf16>(a, DP, lds, stream, coop, stage)
-                 : launch_unr_dt<float>(a, DP, lds, stream, coop, stage);
+                               int ops) {
+  return bf16_in ? launch_unr_dt<bf16>(a, DP, lds, stream, coop, ops)
+                 : launch_unr_dt<float>(a, DP, lds, stream, coop, ops);
 }
 
 hipError_t launch_unrolled_finalize(const UnrBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream) {
