@@ -381,12 +381,13 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   };
 
   // Wave -> resident tiles and streamed pairs.  Waves w and w + 4 of a workgroup share
-  // a SIMD, and a SIMD's main-loop time follows the work of its two waves together
-  // (one wave alone issues as fast as two), so the work is balanced per SIMD:
+  // a SIMD, and a SIMD's main-loop time follows the work of its two waves together, so
+  // the work is balanced per SIMD:
   //  - nr <= 4: the nr * n_pairs (tile, pair) units are cut into four equal ranges in
   //    SIMD order; a SIMD's range is split between its two waves at the tile boundary
   //    it contains, else at its middle, so that every wave takes one tile and a
-  //    contiguous pair range of it;
+  //    contiguous pair range of it (the larger part to the older wave, which the SIMD
+  //    issues for first);
   //  - 4 < nr <= NW: wave takes tile wave % nr, and of its pairs every
   //    (NW - tile + nr - 1) / nr-th from wave / nr (the waves of a tile interleave);
   //  - nr > NW: wave owns tiles wave and wave + NW (slots 0 and 1), all pairs.
@@ -401,7 +402,9 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       const int sb = (o >> 1) * U / 4, se = ((o >> 1) + 1) * U / 4;
       const int tb = (sb / n_pairs + 1) * n_pairs;  // first tile boundary after sb
       const int cut = tb < se ? tb : (sb + se) / 2;
-      const int ub = (o & 1) ? cut : sb, ue = (o & 1) ? se : cut;
+      // the SIMD issues for its older wave (w < 4) first: that wave takes the larger part
+      const bool first = ((o & 1) == 0) == (cut - sb >= se - cut);
+      const int ub = first ? sb : cut, ue = first ? cut : se;
       tile = min(ub / n_pairs, nr - 1);
       p0 = ub - tile * n_pairs; p1 = ue - tile * n_pairs; step = 1;
     } else {
