@@ -195,32 +195,13 @@ __device__ __forceinline__ f32x4 pv_regs(const WOperand<float>& w, const f32x4& 
 // run on Mfma<T, DP> (bf16 inputs: the bf16 MFMA with exact operands, W as a hi + lo
 // bf16 pair, fp32 accumulation, as the forward); the centroid sweep's products, whose
 // operands (sigma(G) dO) are not bf16-exact, run on the fp32 MFMA.
-// Staged operands (STAGE: bf16 inputs, DP = 32, when LDS has room): a sweep's streamed
-// operand, row-major [Np][DP] and transposed [DP][Np] (the prep kernel's padded copies),
-// is copied into LDS with padded rows (no bank conflicts for the fragment reads),
-// over the part hand-over region.  The copy for the next sweep is issued right after
-// a sweep's combine, so its loads overlap the exchange wait; the main loops then read
-// LDS instead of waiting on L2.
-// Operand modes of the kernel: streamed operands read from L2 (GLOBAL), a sweep's
-// streamed operand staged in LDS (STAGE), or Q and K resident in LDS (RES).
-constexpr int UNR_OPS_GLOBAL = 0, UNR_OPS_STAGE = 1, UNR_OPS_RES = 2;
-template <typename T, int DP> constexpr int unr_srs() { return DP + 16 / (int)sizeof(T); }
-__host__ __device__ inline size_t unr_stage_bytes(int Np, int DP, int elem) {
-  const int pad = 16 / elem;
-  return ((size_t)Np * (DP + pad) + (size_t)DP * (Np + pad)) * elem;
-}
-// Floats of the part hand-over region: the write_rows hand-over [NW][16][64] (which
-// also holds the dx hand-over [NW][2][16][6]), [NW][16][32] with resident operands,
-// or (STAGE) a sweep's staged operands if larger.
-__host__ __device__ inline int unr_region_floats(int Np, int DP, int elem, int ops) {
-  if (ops == UNR_OPS_RES) return UNR_NW * 16 * DP;
-  const int base = UNR_NW * 16 * 64;
-  if (ops == UNR_OPS_STAGE) {
-    const int st = (int)(unr_stage_bytes(Np, DP, elem) / 4);
-    return base > st ? base : st;
-  }
-  return base;
-}
+// Operand modes of the kernel: streamed operands read from L2 (their padded copies
+// [Np][DP] and transposed [DP][Np] written by the prep kernel: GLOBAL), or Q and K
+// resident in LDS (RES).
+constexpr int UNR_OPS_GLOBAL = 0, UNR_OPS_RES = 2;
+// Floats of the part hand-over region: the write_rows hand-over [NW][16][DP] (which
+// also holds the dx hand-over [NW][2][16][6]).
+__host__ __device__ inline int unr_region_floats(int DP) { return UNR_NW * 16 * DP; }
 
 // Resident operands (OPS = UNR_OPS_RES: bf16 inputs, DP = 32, when LDS has room): Q and
 // K stay in LDS for the whole launch, row-major [Np][32] bf16 without padding, under a
@@ -251,7 +232,6 @@ __device__ __forceinline__ bf16x4 res_tr4(const bf16* op, int j0, int cb, int la
 
 template <typename T, int DP, bool GEN, int OPS>
 __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
-  constexpr bool STAGE = OPS == UNR_OPS_STAGE;
   constexpr bool RES = OPS == UNR_OPS_RES;
   static_assert(!RES || (sizeof(T) == 2 && DP == 32), "resident operands: bf16, DP = 32");
   using M = Mfma<float, DP>;
@@ -299,14 +279,8 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   float* STB = STA + Np;  // streamed exponent terms of term 2 (or of P in RS(K-1))
   float* STG = STB + Np;  // exp2(STB - STA) of a sweep with both terms (the column factor)
   float* sred = STG + Np;                        // [NW][MAXT][16]
-  float* spart = sred + NW * UNR_MAXT_ANY * 16;  // [NW][16*64] part hand-over
-  // part hand-over [NW][16*64], or (STAGE) the staged operands of a sweep
-  constexpr int SRS = unr_srs<T, DP>();          // row stride of the staged row-major operand
-  const int STS = Np + 16 / (int)sizeof(T);      // row stride of the staged transposed operand
-  const int region = unr_region_floats(Np, DP, (int)sizeof(T), OPS);
-  T* stg_r = reinterpret_cast<T*>(spart);
-  T* stg_t = stg_r + (size_t)Np * SRS;
-  float* sscal = spart + region;                 // [NW]
+  float* spart = sred + NW * UNR_MAXT_ANY * 16;  // [NW][16][DP] part hand-over
+  float* sscal = spart + unr_region_floats(DP);  // [NW]
   float* ldmu = sscal + NW;                      // d log_mu of my rows, summed over the sweeps
   float* ldnu = ldmu + UNR_MAX_LOCAL;            // d log_nu of my columns
   T* opq = reinterpret_cast<T*>(ldnu + UNR_MAX_LOCAL);  // RES: Q, then K, swizzled [Np][32]
@@ -460,79 +434,6 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     if (!(fabsf(dl) <= FLIM)) s_exact = sweep_no + 1;
     return fast_exp2(fminf(fmaxf(dl, -FLIM), FLIM));
   };
-  auto stage_operands = [&](bool row, const SweepDesc* nx) {
-    if constexpr (STAGE) {
-      typedef __attribute__((__vector_size__(16))) int i32x4;
-      float f0[2] = {0.f, 0.f}, f1[2] = {0.f, 0.f};
-      if (nx) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int ic = min(tid + u * UNR_NT, N - 1);  // clamped: the loads are unconditional
-          if (nx->row) {
-            f0[u] = Vn(nx->k, ic);
-            f1[u] = a.log_nu[bhN + ic];
-          } else if (nx->cent) {
-            f0[u] = a.log_u[bhN + ic];
-            f1[u] = a.log_z[bhN + ic];
-          } else {
-            f0[u] = Un(nx->k, ic);
-            f1[u] = a.log_mu[bhN + ic];
-          }
-        }
-      }
-      const T* srow = row ? kp : qp;  // [Np][DP]
-      constexpr int CPR = DP * (int)sizeof(T) / 16;  // chunks of a row-major row
-      const int nrm = Np * CPR;
-      constexpr int SB = 8;
-      for (int e0 = 0; e0 < nrm; e0 += SB * UNR_NT) {
-        i32x4 v[SB];
-#pragma unroll
-        for (int u = 0; u < SB; ++u) {
-          const int e = min(e0 + u * UNR_NT + tid, nrm - 1);
-          v[u] = *reinterpret_cast<const i32x4*>(srow + (size_t)(e / CPR) * DP + (e % CPR) * 8);
-        }
-        if (nx && e0 == 0) {
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int i = tid + u * UNR_NT;
-            if (i >= Np) continue;
-            float sa = NEG_BIG, sb = NEG_BIG;
-            if (i < n && valid[i]) {
-              if (nx->row) {
-                if (nx->use_c) sa = (f0[u] * ik - f1[u]) * LOG2E;
-                if (nx->term2 || nx->cent) sb = f0[u] * LOG2E;
-              } else if (nx->cent) {
-                sa = (f0[u] - f1[u]) * LOG2E;
-              } else {
-                sa = (f0[u] * ik - f1[u]) * LOG2E;
-                sb = f0[u] * LOG2E;
-              }
-            }
-            STA[i] = sa;
-            STB[i] = sb;
-            STG[i] = both_factor(*nx, i < n && valid[i], sa, sb);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < SB; ++u) {
-          const int e = e0 + u * UNR_NT + tid;
-          if (e < nrm) *reinterpret_cast<i32x4*>(stg_r + (size_t)(e / CPR) * SRS + (e % CPR) * 8) = v[u];
-        }
-      }
-      __syncthreads();
-      // lanes take consecutive columns c of one block of 8 rows: the 2-byte reads of a
-      // wave hit distinct banks (a lane-per-row order would put them all in two)
-      const int cpt = Np / 8;  // 8-element chunks of a transposed row
-      for (int e = tid; e < DP * cpt; e += UNR_NT) {
-        const int c = e % DP, j0 = (e / DP) * 8;
-        T col[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) col[r] = stg_r[(size_t)(j0 + r) * SRS + c];
-        *reinterpret_cast<i32x4*>(stg_t + (size_t)c * STS + j0) = *reinterpret_cast<const i32x4*>(col);
-      }
-    }
-  };
-  stage_operands(false, nullptr);  // the first sweep (CS_cent) streams Q
 
   f32x4 dQa[MAXT][NC], dKa[MAXT][NC];
   float gbx[MAXT], gby[MAXT], gbz[MAXT], xt0[MAXT], xt1[MAXT], xt2[MAXT], dmu[MAXT], dnu[MAXT];
@@ -636,12 +537,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     const bool publish = ROW ? k >= 0 : (CENT || k >= 1);
     constexpr bool BOTH = use_c && term2 && !CENT;  // one exponential an element (see STG)
     ++sweep_no;
-    __syncthreads();  // STA / STB, the staged operand and the gathered vectors are complete
+    __syncthreads();  // STA / STB / STG and the gathered vectors are complete
     const float* STC = ROW ? GLV : GLU;  // streamed recurrence coefficients
-    const T* Sop = STAGE ? stg_r : (ROW ? kp : qp);
-    const T* Sot = STAGE ? stg_t : (ROW ? kt : qt);
-    const int sop_rs = STAGE ? SRS : DP;  // row strides of the streamed operand and its transpose
-    const int sot_rs = STAGE ? STS : Np;
+    const T* Sop = ROW ? kp : qp;  // GLOBAL: the streamed operand and its transpose in L2
+    const T* Sot = ROW ? kt : qt;
     const T* Rop = ROW ? qp : kp;
 
     typename MQ::Frag bf[MAXT];
@@ -702,10 +601,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     }
     if (ts < nts) {
       // The streamed operands of a pair of tiles (Q or K fragments for the cost, the
-      // transposed operand for dQ / dK) come from global memory (L2): they are the same
-      // for every resident slot, so they are loaded once per pair, and one pair ahead:
-      // the loads of pair sp + wstep are issued (unconditionally, from a clamped pair)
-      // before pair sp is computed.
+      // transposed operand for dQ / dK) are the same for every resident slot, so they are
+      // loaded once per pair: from LDS in the iteration itself (RES), or from L2 one pair
+      // ahead (GLOBAL: the loads of pair sp + wstep are issued, unconditionally from a
+      // clamped pair, before pair sp is computed).
       using V4 = typename VtQuad<T>::type;
       typename MQ::Frag afn[2];
       V4 vln[NC], vhn[NC];
@@ -725,21 +624,21 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
         }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
-          MQ::load(afn[hh], Sop + (size_t)((2 * spc + hh) * 16 + (lane & 15)) * sop_rs, lane);
+          MQ::load(afn[hh], Sop + (size_t)((2 * spc + hh) * 16 + (lane & 15)) * DP, lane);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const T* vt_row = Sot + (size_t)(c * 16 + (lane & 15)) * sot_rs + spc * 32;
+          const T* vt_row = Sot + (size_t)(c * 16 + (lane & 15)) * Np + spc * 32;
           load_vt<T>(vt_row, lane, vln[c], vhn[c]);
         }
       };
-      // staged operands come from LDS: loaded in the iteration itself (a register copy of
-      // a prefetch would cost more than the LDS latency it hides)
+      // resident operands come from LDS: loaded in the iteration itself (a register copy
+      // of a prefetch would cost more than the LDS latency it hides)
       auto main_loop = [&](auto fast_tag) {
       // FAST (BOTH sweeps with factors in range): e2 = e1 * STG_j * exp2(rb - ra)
       constexpr bool FAST = decltype(fast_tag)::value;
-      if (!STAGE && !RES) load_pair(wp0);
+      if (!RES) load_pair(wp0);
       for (int sp = wp0; sp < wp1; sp += wstep) {
-        if (STAGE || RES) load_pair(sp);
+        if (RES) load_pair(sp);
         typename MQ::Frag afc[2] = {afn[0], afn[1]};
         V4 vlc[NC], vhc[NC];
 #pragma unroll
@@ -747,7 +646,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
           vlc[c] = vln[c];
           vhc[c] = vhn[c];
         }
-        if (!STAGE && !RES) load_pair(sp + wstep);
+        if (!RES) load_pair(sp + wstep);
 #pragma unroll
         for (int s = 0; s < MAXT; ++s) {
           const int rt = ts + nts * s;
@@ -887,14 +786,9 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
         a.dv_init[bhN + i] = v;
       }
     });
-    // the next sweep streams the other operand (the sweeps alternate): its copy is
-    // issued now, past the combine's barrier (no wave reads the region any more), so
-    // it overlaps the exchange; CS_cent hands its dV partials over through the same
-    // region and stages after that
-    if (next.valid && !(CENT && !ROW)) {
-      if (STAGE) stage_operands(next.row, &next);
-      else fill_streamed(next);
-    }
+    // the next sweep's streamed terms, past the combine's barrier (no wave reads
+    // STA / STB / STG any more): their loads share the exchange's wait
+    if (next.valid) fill_streamed(next);
     if (publish) {
       // gathered as kappa gl: both readers (the streamed coefficients and the
       // resident dd) want the kappa multiple
@@ -902,14 +796,7 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     } else {
       __syncthreads();
     }
-    if (CENT && !ROW) {
-      write_rows(gVa, a.dv, 1.f);
-      if (next.valid) {
-        __syncthreads();
-        if (STAGE) stage_operands(next.row, &next);
-        else fill_streamed(next);
-      }
-    }
+    if (CENT && !ROW) write_rows(gVa, a.dv, 1.f);
     return true;
   };
 
@@ -990,19 +877,16 @@ size_t unrolled_bwd_lds_bytes(int N, int DP, int elem, int ops) {
   size_t bytes = ((Np + 15) / 16) * 16;
   bytes += 12 * Np * 4;                              // coordinates, grad x_c, D, gathered vectors, STA, STB, STG
   bytes += (size_t)UNR_NW * UNR_MAXT_ANY * 16 * 4;   // recurrence partials
-  bytes += 4 * (size_t)unr_region_floats((int)Np, DP, elem, ops);  // part hand-over / staged operand
+  bytes += 4 * (size_t)unr_region_floats(DP);       // part hand-over
   bytes += UNR_NW * 4;
   bytes += 2 * UNR_MAX_LOCAL * 4;                    // d log_mu, d log_nu of the stripe
   if (ops == UNR_OPS_RES) bytes += 2 * Np * DP * (size_t)elem;  // resident Q and K
   return bytes;
 }
 
-// Resident operands if they fit, else a staged streamed operand if that fits (bf16,
-// DP = 32), else operands from L2.
+// Resident operands if they fit (bf16, DP = 32), else operands from L2.
 int unrolled_operand_mode(int N, int DP, int elem, size_t limit) {
-  if (elem != 2 || DP != 32) return UNR_OPS_GLOBAL;
-  if (unrolled_bwd_lds_bytes(N, DP, elem, UNR_OPS_RES) <= limit) return UNR_OPS_RES;
-  if (unrolled_bwd_lds_bytes(N, DP, elem, UNR_OPS_STAGE) <= limit) return UNR_OPS_STAGE;
+  if (elem == 2 && DP == 32 && unrolled_bwd_lds_bytes(N, DP, elem, UNR_OPS_RES) <= limit) return UNR_OPS_RES;
   return UNR_OPS_GLOBAL;
 }
 
@@ -1045,12 +929,10 @@ static hipError_t launch_unr_t(const UnrBwdArgs& a, size_t lds, hipStream_t stre
 template <typename T>
 static hipError_t launch_unr_dt(const UnrBwdArgs& a, int DP, size_t lds, hipStream_t stream, bool coop, int ops) {
   const bool gen = (a.bins8 && a.pos_w) || (a.has_geo && a.w_dist);
-  constexpr int G0 = UNR_OPS_GLOBAL, ST = UNR_OPS_STAGE, RS = UNR_OPS_RES;
+  constexpr int G0 = UNR_OPS_GLOBAL, RS = UNR_OPS_RES;
   if constexpr (sizeof(T) == 2) {
     if (ops == RS && DP == 32)
       return gen ? launch_unr_t<T, 32, true, RS>(a, lds, stream, coop) : launch_unr_t<T, 32, false, RS>(a, lds, stream, coop);
-    if (ops == ST && DP == 32)
-      return gen ? launch_unr_t<T, 32, true, ST>(a, lds, stream, coop) : launch_unr_t<T, 32, false, ST>(a, lds, stream, coop);
   }
   if (ops != G0) return hipErrorInvalidValue;
   if (DP == 32)

@@ -80,7 +80,7 @@ CASES = [
     (2, 3, 70, 32, 3, [0.5, 1.0, 2.0], [70, 41], True, torch.float32, 1e-4),
     (1, 2, 48, 64, 5, [0.7, 1.3], None, False, torch.bfloat16, 2e-2),
     (1, 2, 300, 32, 4, [0.5, 1.0], [290], False, torch.float32, 1e-4),        # several tiles per member
-    # bf16 with d <= 32: the sweeps stream their operand from LDS copies (staged path)
+    # bf16 with d <= 32: Q and K resident in LDS (swizzled, transposed reads)
     (2, 3, 70, 32, 5, [0.5, 1.0, 2.0], [70, 41], False, torch.bfloat16, 2e-2),
     (1, 2, 300, 32, 4, [0.5, 1.0], [290], False, torch.bfloat16, 2e-2),
 ]
@@ -137,31 +137,56 @@ def test_flash_sinkhorn_defaults_to_unrolled():
             assert_close_rel(L[k].grad.cpu().numpy(), gr[k].numpy(), 1e-4, f"{fn} grad {k}")
 
 
-@pytest.mark.parametrize("B,H,N,d,K,lens", [(2, 4, 96, 32, 6, [96, 61]), (1, 2, 300, 24, 4, [290])])
-def test_unrolled_content_only_bf16(B, H, N, d, K, lens):
-    """The content-only cost (no bins, no geometry: the kernel's GEN = false build, the
-    one the headline workload runs) with bf16 inputs at d <= 32 (staged operands)."""
-    print(f"case content-only B{B} H{H} N{N} d{d} K{K}", flush=True)
+def _content_only(B, H, N, d, K, lens, dtype, extreme=False):
+    """Oracle and GPU results of the content-only cost (no bins, no geometry: the
+    kernel's GEN = false build).  extreme: a few log-marginals at -70, which puts the
+    ratio of a sweep's two exponentials outside the kernel's factored range (2^+-40),
+    so those sweeps take the exact two-exponential path."""
     t, bins, e, mask, wo, wx = _inputs(B, H, N, d, seed=N + 3 * K, eps=[0.5] * H, lens=lens)
     t["pw"] = torch.zeros_like(t["pw"])
     t["wd"] = torch.zeros_like(t["wd"])
-    for k in ("Q", "K", "V", "G"):
-        t[k] = t[k].to(torch.bfloat16).float()
+    if extreme:
+        t["lmu"][..., :3] = -70.0
+        t["lnu"][..., 5:8] = -70.0
+    if dtype == torch.bfloat16:
+        for k in ("Q", "K", "V", "G"):
+            t[k] = t[k].to(torch.bfloat16).float()
     vr, gr = _oracle(t, torch.zeros_like(bins), e, mask, wo, wx, K)
     from deepfold_amd import flash_sinkhorn_attn
 
     L = {k: v.to(DEV) for k, v in t.items()}
     for k in ("Q", "K", "V", "G"):
-        L[k] = L[k].to(torch.bfloat16)
+        L[k] = L[k].to(dtype)
     L = {k: v.detach().requires_grad_(True) for k, v in L.items()}
     # no bins and w_dist = None (the reference's w_dist = 0 without reading x): GEN = false
     o, xc, lu, lv = flash_sinkhorn_attn(L["Q"], L["K"], L["V"], L["G"], L["x"], L["pw"], None, e.to(DEV), None,
                                         L["lmu"], L["lnu"], K_iter=K, mask=mask.to(DEV), ift_mode="unrolled")
     ((o * wo.to(DEV)).sum() + (xc * wx.to(DEV)).sum()).backward()
-    vg = {"o": o, "xc": xc, "lu": lu, "lv": lv}
+    return {"o": o, "xc": xc, "lu": lu, "lv": lv}, L, vr, gr
+
+
+def _check(vg, L, vr, gr, tol):
     for k in ("o", "xc", "lu", "lv"):
-        assert_close_rel(vg[k].detach().float().cpu().numpy(), vr[k].detach().numpy(), 2e-2, k)
+        assert_close_rel(vg[k].detach().float().cpu().numpy(), vr[k].detach().numpy(), tol, k)
     for k in ("Q", "K", "V", "G", "lmu", "lnu"):
         got = L[k].grad.float().cpu().numpy()
         assert np.isfinite(got).all(), k
-        assert_close_rel(got, gr[k].numpy(), 2e-2, f"grad {k}")
+        assert_close_rel(got, gr[k].numpy(), tol, f"grad {k}")
+
+
+# the last case is the headline layout (B2 H8 N768, n_b = [501, 759]: two and three
+# resident tiles per member, Q and K resident in LDS)
+@pytest.mark.parametrize("B,H,N,d,K,lens", [(2, 4, 96, 32, 6, [96, 61]), (1, 2, 300, 24, 4, [290]),
+                                             (2, 8, 768, 32, 3, [501, 759])])
+def test_unrolled_content_only_bf16(B, H, N, d, K, lens):
+    """The content-only cost (the build the headline workload runs) with bf16 inputs
+    at d <= 32 (Q and K resident in LDS)."""
+    print(f"case content-only B{B} H{H} N{N} d{d} K{K}", flush=True)
+    _check(*_content_only(B, H, N, d, K, lens, torch.bfloat16), 2e-2)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_unrolled_exact_factor_path(dtype, tol):
+    """Sweeps whose exponential ratio leaves the factored range take the exact path."""
+    print(f"case extreme marginals {dtype}", flush=True)
+    _check(*_content_only(2, 2, 96, 32, 4, [96, 61], dtype, extreme=True), tol)
