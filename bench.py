@@ -210,15 +210,15 @@ def algorithmic_counts(cfg, lengths):
     return E, f_fwd, f_bwd, x_fwd, x_bwd
 
 
-def profiled_traffic(kernel, profile="sinkhorn_cfg2_bench.md"):
-    """HBM bytes per launch of ``kernel`` from a committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (calibrated against a copy kernel), or None."""
+def profiled_traffic(kernel, profile="sinkhorn_cfg2_bench.md", key="hbm_bytes_per_launch"):
+    """HBM bytes per launch of ``kernel`` (or per step, key "hbm_bytes") from a committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy kernel), or None."""
     import re
 
     path = os.path.join(ROOT, "profiles", profile)
     if not os.path.exists(path):
         return None
-    m = re.search(rf"^\s*{kernel} hbm_bytes_per_launch = (\d+)", open(path).read(), flags=re.M)
+    m = re.search(rf"^\s*{kernel} {key} = (\d+)", open(path).read(), flags=re.M)
     return int(m.group(1)) if m else None
 
 
@@ -419,7 +419,8 @@ def bench_sinkhorn(args, name):
     f_dom = f_fwd if dom == "sinkhorn_fwd" else f_bwd
     x_dom = x_fwd if dom == "sinkhorn_fwd" else x_bwd
     achieved = f_dom / (avg[dom] * 1e-3)
-    traffic = profiled_traffic(dom, "sinkhorn_cfg2_bench.md" if name == "cfg2" else f"sinkhorn_{name}_bench.md")
+    traffic = profiled_traffic(dom, {"cfg2": "sinkhorn_cfg2_bench.md", "cfg2-unrolled": "unrolled_cfg2_bench.md"}
+                               .get(name, f"sinkhorn_{name}_bench.md"))
     peak = PEAK_MFMA_BF16  # bf16 inputs: both backwards run their products on the bf16 MFMA
     t_roof = max((f_fwd + f_bwd) / PEAK_MFMA_BF16, (x_fwd + x_bwd) / PEAK_SWEEP_ELEMENT_MEASURED)
     metric = ("flash-Sinkhorn fwd+IFT-bwd ms/layer @B2,H8,N768,d32 bf16; % of MFMA/HBM roof" if name == "cfg2"
@@ -578,7 +579,8 @@ def bench_attention(args, which):
         "config": info, "kernel_ms_per_step": {k: round(v, 4) for k, v in kernel_ms.items()},
         "roofline": {"bound": "hbm", "achieved": round(bytes_alg / (dev_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": round(bytes_alg / (dev_ms * 1e-3) / PEAK_HBM, 4),
-                     "traffic": None, "algorithmic_bytes": bytes_alg},
+                     "traffic": profiled_traffic("attention_step", f"attention_{which}_bench.md", "hbm_bytes"),
+                     "traffic_per": "step (sum over the step's kernels)", "algorithmic_bytes": bytes_alg},
         "mfma": {"achieved_tflops": round(flops / (dev_ms * 1e-3) / 1e12, 2), "peak_tflops": PEAK_MFMA_BF16 / 1e12},
     }
     print(json.dumps(out), flush=True)
