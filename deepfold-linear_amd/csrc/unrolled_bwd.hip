@@ -353,6 +353,14 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
     if (k >= 0) return hist[((size_t)(2 * k) * BH + bh) * N + j];
     return a.v_init ? a.v_init[bhN + j] : 0.f;
   };
+  // Prefetch loads: relaxed atomic loads, which the compiler issues where they stand
+  // (it may not sink them to their first use past the main loop).
+  auto pld = [&](const float* p_) { return __hip_atomic_load(const_cast<float*>(p_), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  auto UnP = [&](int k, int i) { return pld(hist + ((size_t)(2 * k + 1) * BH + bh) * N + i); };
+  auto VnP = [&](int k, int j) {
+    if (k >= 0) return pld(hist + ((size_t)(2 * k) * BH + bh) * N + j);
+    return a.v_init ? pld(a.v_init + bhN + j) : 0.f;
+  };
 
   // Wave -> resident tiles and streamed pairs.  Waves w and w + 4 of a workgroup share
   // a SIMD, and a SIMD's main-loop time follows the work of its two waves together, so
@@ -508,7 +516,77 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
   // Streamed exponent terms STA / STB of a sweep (flags and k as the sweep's).  Filled
   // for the next sweep right after a sweep's combine (its main loop is done with them),
   // so the hist loads share the wait of the exchange and of the operand copy.
+  // RES: the next sweep's history values, loaded at the start of a sweep (its main
+  // loop issues no global loads, so they arrive under it instead of at the fill and
+  // at the next sweep's start): the streamed terms' raw values (entries tid and
+  // tid + UNR_NT; Np <= 1024 with resident operands) and the resident slots' terms.
+  float pf0[2] = {0.f, 0.f}, pf1[2] = {0.f, 0.f};
+  float pra[MAXT], prb[MAXT];
+  bool pf_have = false;
+  auto stream_terms = [&](const SweepDesc& nx, float f0, float f1, float& sa, float& sb) {
+    sa = sb = NEG_BIG;
+    if (nx.row) {  // streamed columns j: f0 = v^k_j, f1 = log nu_j
+      if (nx.use_c) sa = (f0 * ik - f1) * LOG2E;  // s^{C,k}
+      if (nx.term2 || nx.cent) sb = f0 * LOG2E;  // s^{R,k+1} or P
+    } else if (nx.cent) {  // streamed rows i: f0 = log u_i, f1 = log Z_i
+      sa = (f0 - f1) * LOG2E;  // P
+    } else {  // f0 = u^k_i, f1 = log mu_i
+      sa = (f0 * ik - f1) * LOG2E;  // s^{R,k}
+      sb = f0 * LOG2E;             // s^{C,k}
+    }
+  };
+  auto prefetch = [&](const SweepDesc& nx) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int ic = min(tid + u * UNR_NT, N - 1);  // clamped: the loads are unconditional
+      if (nx.row) {
+        pf0[u] = VnP(nx.k, ic);
+        pf1[u] = pld(a.log_nu + bhN + ic);
+      } else if (nx.cent) {
+        pf0[u] = pld(a.log_u + bhN + ic);
+        pf1[u] = pld(a.log_z + bhN + ic);
+      } else {
+        pf0[u] = UnP(nx.k, ic);
+        pf1[u] = pld(a.log_mu + bhN + ic);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < MAXT; ++s) {
+      const int rt = ts + nts * s;
+      const int ri = (t0 + min(rt, nr - 1)) * 16 + (lane & 15);
+      const bool ok = rt < nr && ri < n && valid[ri];
+      float ra = NEG_BIG, rb = NEG_BIG;
+      if (ok) {
+        if (nx.row) {
+          if (nx.use_c) ra = UnP(nx.k, ri) * LOG2E;
+          if (nx.cent) rb = (pld(a.log_u + bhN + ri) - pld(a.log_z + bhN + ri)) * LOG2E;
+          else if (nx.term2) rb = (UnP(nx.k + 1, ri) * ik - pld(a.log_mu + bhN + ri)) * LOG2E;
+        } else if (nx.cent) {
+          ra = VnP(K - 1, ri) * LOG2E;
+        } else {
+          ra = VnP(nx.k - 1, ri) * LOG2E;
+          rb = (VnP(nx.k, ri) * ik - pld(a.log_nu + bhN + ri)) * LOG2E;
+        }
+      }
+      pra[s] = ra;
+      prb[s] = rb;
+    }
+  };
   auto fill_streamed = [&](const SweepDesc& nx) {
+    if (RES && pf_have) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * UNR_NT;
+        if (i >= Np) continue;
+        const bool ok = i < n && valid[i];
+        float sa = NEG_BIG, sb = NEG_BIG;
+        if (ok) stream_terms(nx, pf0[u], pf1[u], sa, sb);
+        STA[i] = sa;
+        STB[i] = sb;
+        STG[i] = both_factor(nx, ok, sa, sb);
+      }
+      return;
+    }
     for (int i = tid; i < Np; i += UNR_NT) {
       float sa = NEG_BIG, sb = NEG_BIG;
       if (i < n && valid[i]) {
@@ -561,7 +639,11 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       if (CENT) M::load(cbf[s], (ROW ? gp : vp) + (size_t)ri * DP, lane);
       ra[s] = rb[s] = NEG_BIG;
       dd[s] = 0.f;
-      if (ok) {
+      if (RES && pf_have) {  // prefetched during the previous sweep (the same formulas)
+        ra[s] = pra[s];
+        rb[s] = prb[s];
+        if (ok && ((ROW && term2) || (!ROW && !CENT))) dd[s] = ROW ? GLU[ri] : GLV[ri];
+      } else if (ok) {
         if (ROW) {  // resident rows i
           if (use_c) ra[s] = Un(k, ri) * LOG2E;                                             // s^{C,k}
           if (CENT) rb[s] = (a.log_u[bhN + ri] - a.log_z[bhN + ri]) * LOG2E;                // P
@@ -598,6 +680,10 @@ __global__ void __launch_bounds__(UNR_NT) unrolled_bwd_kernel(UnrBwdArgs a) {
       for (int e = 0; e < 4; ++e) red[s][e] = 0.f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) gVa[s][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if constexpr (RES) {  // the next sweep's history values, under this sweep's main loop
+      if (next.valid) prefetch(next);
+      pf_have = next.valid;
     }
     if (ts < nts) {
       // The streamed operands of a pair of tiles (Q or K fragments for the cost, the
