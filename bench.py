@@ -38,9 +38,10 @@ sys.path.insert(0, os.path.join(ROOT, "deepfold-linear_amd"))
 PEAK_MFMA_BF16 = 2.5e15
 PEAK_HBM = 8.0e12
 # Measured on MI355X by `bench.py --workload peaks` (csrc/peaks.hip, two waves per
-# SIMD on all 256 CUs): v_exp_f32 issue rate, and the rate of the fixed-shift sweep's
-# element (fma + exp2 + add), which does not overlap on gfx950.
-PEAK_EXP_MEASURED = 15.5e12
+# SIMD on all 256 CUs): v_exp_f32 issue rate (15.5-17.8 T/s on two boxes: the higher),
+# and the rate of the fixed-shift sweep's element (fma + exp2 + add), which does not
+# overlap on gfx950 (9.54 and 9.53 T/s).
+PEAK_EXP_MEASURED = 17.8e12
 PEAK_SWEEP_ELEMENT_MEASURED = 9.54e12
 PEAK_MFMA_F32 = 157.3e12
 
