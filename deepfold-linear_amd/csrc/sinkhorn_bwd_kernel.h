@@ -140,13 +140,106 @@ __device__ __forceinline__ void lean_wsum_chunk(const T* __restrict__ res_lds, c
   __syncthreads();
 }
 
+// The weighted sum with a bias (position bins or geometry): out[q] = sum_j exp2(sc*<res_q,
+// str_j> + cres[q] + w2_j + bias_qj) * z_j, one pass over a wave's streamed slots for up to
+// SK_RT resident tiles, the tiles in a runtime loop that computes one tile's biases at a
+// time (the compile-time chunks of lean_wsum_chunk hold two tiles' biases at most, and
+// their second pass over the streamed slots made the full-cost backward 9% slower).
+// Every exponent is <= 0 here (S_col, T and W are bounded by 1), so no shift.
+template <typename T, int DP, bool GENERAL, bool TRANS>
+__device__ __forceinline__ void bias_wsum(const T* __restrict__ res_lds, const T* __restrict__ str_lds,
+                            const float* __restrict__ w2, const float* __restrict__ zv, int n_str_tiles, int rt0,
+                            int nr, float sc, const float* __restrict__ cres, const Bias& bias, float* out,
+                            float* scratch) {
+  using M = Mfma<T, DP>;
+  constexpr int SCH = sweep_sch<T, DP>();
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  const int g = lane >> 4;
+  const float isc = 1.f / sc;
+  const int ks = wave < n_str_tiles ? (n_str_tiles - wave + BWD_NW - 1) / BWD_NW : 0;
+  for (int c0 = 0; c0 < nr; c0 += SK_RT) {
+    const int nc = min(SK_RT, nr - c0);
+    float s[SK_RT];
+#pragma unroll
+    for (int r = 0; r < SK_RT; ++r) s[r] = 0.f;
+    for (int k0 = 0; k0 < ks; k0 += SCH) {
+      // streamed fragments, column terms and weights stay in registers for all
+      // resident tiles; slots past the wave's last tile carry w = NEG_BIG (no
+      // bias lookup, exp2 -> 0) and z = 0
+      typename M::Frag af[SCH];
+      f32x4 w[SCH], z[SCH];
+#pragma unroll
+      for (int k = 0; k < SCH; ++k) {
+        const bool live = k0 + k < ks;
+        const int st = live ? wave + BWD_NW * (k0 + k) : wave;
+        M::load(af[k], str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+        w[k] = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+        z[k] = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
+        if (!live) {
+          w[k] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+          z[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < SK_RT; ++r) {
+        if (r >= nc) continue;
+        typename M::Frag bf;
+        M::load(bf, res_lds + (size_t)((rt0 + c0 + r) * 16 + (lane & 15)) * DP, lane);
+        const float ci = cres[(c0 + r) * 16 + (lane & 15)] * isc;
+        const f32x4 cinit = f32x4{ci, ci, ci, ci};
+        f32x4 bv[SCH];
+        if (GENERAL) {  // dead slots repeat tile `wave` (their w is NEG_BIG)
+          int s0[SCH];
+#pragma unroll
+          for (int k = 0; k < SCH; ++k) s0[k] = (k0 + k < ks ? wave + BWD_NW * (k0 + k) : wave) * 16 + 4 * g;
+          bias.template quads<TRANS>((rt0 + c0 + r) * 16 + (lane & 15), s0, bv);
+        }
+        f32x4 x[SCH];
+#pragma unroll
+        for (int k = 0; k < SCH; ++k) x[k] = M::qk(af[k], bf, cinit);  // independent MFMAs
+        float acc_s = 0.f;
+#pragma unroll
+        for (int k = 0; k < SCH; ++k) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float xv = __builtin_fmaf(x[k][e], sc, w[k][e]);
+            if (GENERAL) xv += bv[k][e];
+            acc_s = __builtin_fmaf(fast_exp2(xv), z[k][e], acc_s);
+          }
+        }
+        s[r] += acc_s;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < SK_RT; ++r)
+      if (r < nc) {
+        const float ss = sum_groups(s[r]);
+        if (lane < 16) scratch[(wave * SK_RT + r) * 16 + lane] = ss;
+      }
+    __syncthreads();
+    if ((int)threadIdx.x < nc * 16) {
+      const int q = threadIdx.x, r = q >> 4, l = q & 15;
+      float ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < BWD_NW; ++w) ss += scratch[(w * SK_RT + r) * 16 + l];
+      out[c0 * 16 + q] = ss;
+    }
+    __syncthreads();
+  }
+}
+
 // lean_wsum_chunk over the nr resident tiles [rt0, rt0 + nr), chunks of at most 4
-// tiles (2 with a bias, whose per-element values take the registers of two tiles).
+// tiles; with a bias, bias_wsum.
 template <typename T, int DP, bool GENERAL, bool TRANS>
 __device__ __forceinline__ void lean_wsum(const T* res_lds, const T* str_lds, const float* w2, const float* zv,
                                           int n_str_tiles, int rt0, int nr, float sc, const float* cres,
                                           const Bias& bias, float* out, float* scratch) {
-  constexpr int CMAX = GENERAL ? 2 : 4;
+  if constexpr (GENERAL) {
+    bias_wsum<T, DP, GENERAL, TRANS>(res_lds, str_lds, w2, zv, n_str_tiles, rt0, nr, sc, cres, bias, out, scratch);
+    return;
+  }
+  constexpr int CMAX = 4;
   for (int c0 = 0; c0 < nr; c0 += CMAX) {
     const int nc = min(CMAX, nr - c0);
     if (CMAX == 4 && nc == 4)
