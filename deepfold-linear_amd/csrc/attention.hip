@@ -7,10 +7,11 @@
 //
 // The first three run on the streaming engine of attn_engine.h: forward, a
 // query-resident pass for dQ and the bias gradients, and a key-resident pass for
-// dK / dV (optionally split over query ranges with fp32 partials).  This file
-// holds the backward prep (D_i = dO_i.O_i, sigma(G) dO, dG), the finalize of the
-// partial sums, the atom-to-token kernels and the launchers.  No atomics in HBM
-// except in the atom-to-token backward, whose atom ranges may overlap.
+// dK / dV (optionally split over query ranges with fp32 partials); the dQ pass runs
+// first and also does the backward prep of its rows (D_i = dO_i.O_i, sigma(G) dO, dG).
+// This file holds the finalize of the partial sums, the atom-to-token kernels and
+// the launchers.  No atomics in HBM except in the atom-to-token backward, whose
+// atom ranges may overlap.
 #include "attn_args.h"
 #include "attn_engine.h"
 #include "common.h"
@@ -18,39 +19,6 @@
 #include <algorithm>
 
 namespace dfl {
-
-__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
-
-// ===========================================================================
-// Backward prep: one thread per (b,h,i,c), the DP lanes of a row contiguous in a wave.
-//   do_w = sigma(G) dO (or dO), D_i = sum_c dO_ic O_ic, dG = (1 - sigma) O dO  (O is the gated output)
-template <typename T, int DP>
-__global__ void __launch_bounds__(256) attn_bwd_prep_kernel(AttnArgs a) {
-  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t rows = (size_t)a.B * a.H * a.Mq;
-  const size_t row = e / DP;
-  const int c = (int)(e % DP);
-  const bool in = row < rows;
-  const int bh = in ? (int)(row / a.Mq) : 0, i = in ? (int)(row % a.Mq) : 0;
-  const int b = bh / a.H, h = bh % a.H;
-  const bool ok = in && (!a.qmask || a.qmask[(size_t)b * a.Mq + i] > 0.5f);
-  float dov = 0.f, ov = 0.f, s = 1.f;
-  if (ok && c < a.d) {
-    dov = to_f32(reinterpret_cast<const T*>(a.dout)[row * a.d + c]);
-    ov = to_f32(reinterpret_cast<const T*>(a.o)[row * a.d + c]);
-    if (a.g) {
-      s = sigm(to_f32(reinterpret_cast<const T*>(a.g)[(size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)i * a.qsn + c]));
-      if (a.dg) reinterpret_cast<T*>(a.dg)[row * a.d + c] = from_f32<T>((1.f - s) * ov * dov);
-    }
-  } else if (in && a.g && a.dg && c < a.d) {
-    reinterpret_cast<T*>(a.dg)[row * a.d + c] = from_f32<T>(0.f);
-  }
-  if (in) reinterpret_cast<T*>(a.do_w)[row * DP + c] = from_f32<T>(s * dov);
-  float part = dov * ov;
-#pragma unroll
-  for (int o = DP / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, WAVE);
-  if (in && c == 0) a.dcoef[row] = part;
-}
 
 // dK / dV from query-split partials; d pos_weight from per-workgroup partials (fixed order).
 template <typename T, int DP>
@@ -216,8 +184,9 @@ __global__ void __launch_bounds__(256) a2t_bwd_finalize_kernel(A2TArgs a) {
 
 // ===========================================================================
 // Launchers
-// Fast staging: 16-byte aligned key / value rows and bias rows, head dim a multiple
-// of the 16-byte element count, key count a multiple of 8 when a bias is read.
+// Fast staging: 16-byte aligned key / value rows and bias rows (and query, dO, O and
+// gate rows when with_q), head dim a multiple of the 16-byte element count, key
+// count a multiple of 8 when a bias is read.
 template <typename T>
 static bool attn_fast(const AttnArgs& a, bool with_q) {
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -225,6 +194,7 @@ static bool attn_fast(const AttnArgs& a, bool with_q) {
   auto st = [](long long s) { return ((s * (long long)sizeof(T)) & 15) == 0; };
   bool ok = a.d % VEC == 0 && al(a.k) && al(a.v) && st(a.ksb) && st(a.ksh) && st(a.ksn);
   if (with_q) ok = ok && al(a.q) && st(a.qsb) && st(a.qsh) && st(a.qsn);
+  if (with_q) ok = ok && al(a.dout) && al(a.o) && (!a.g || al(a.g));  // row loads of the forward and dQ pass
   if (a.bias_mode == ATTN_BIAS_DENSE || a.bias_mode == ATTN_BIAS_WINDOW)
     ok = ok && al(a.bias) && (!a.dbias || al(a.dbias)) && a.Nk % 8 == 0;
   if (a.bias_mode == ATTN_BIAS_BINS) ok = ok && al(a.bins) && a.Nk % 8 == 0;
@@ -244,7 +214,7 @@ static hipError_t attn_fwd_f(const AttnArgs& a, hipStream_t s) {
 }
 template <typename T, int DP, int BIAS, bool WIN>
 static hipError_t attn_fwd_w(const AttnArgs& a, hipStream_t s) {
-  return attn_fast<T>(a, false) ? attn_fwd_f<T, DP, BIAS, WIN, true>(a, s) : attn_fwd_f<T, DP, BIAS, WIN, false>(a, s);
+  return attn_fast<T>(a, true) ? attn_fwd_f<T, DP, BIAS, WIN, true>(a, s) : attn_fwd_f<T, DP, BIAS, WIN, false>(a, s);
 }
 template <typename T, int DP, int BIAS>
 static hipError_t attn_fwd_t(const AttnArgs& a, hipStream_t s) {
@@ -276,15 +246,13 @@ static hipError_t attn_bwd_f(const AttnArgs& a, hipStream_t s) {
                                                                              : set_lds_limit((const void*)kq, lq);
   if (attr != hipSuccess) return attr;
   const int BH = a.B * a.H;
-  const size_t rows = (size_t)BH * a.Mq;
-  hipLaunchKernelGGL((attn_bwd_prep_kernel<T, DP>), dim3((unsigned)((rows * DP + 255) / 256)), dim3(256), 0, s, a);
+  // the dQ pass first: it also writes do_w and D of every query, which the dK/dV pass streams
+  const int nqb = (a.Mq + E::RQ - 1) / E::RQ;
+  hipLaunchKernelGGL(kq, dim3((unsigned)(nqb * BH)), dim3(E::NT), lq, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int nkb = (a.Nk + K::RK - 1) / K::RK;
   hipLaunchKernelGGL(kkv, dim3((unsigned)(nkb * a.qsplit * BH)), dim3(K::NT), lkv, s, a);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  const int nqb = (a.Mq + E::RQ - 1) / E::RQ;
-  hipLaunchKernelGGL(kq, dim3((unsigned)(nqb * BH)), dim3(E::NT), lq, s, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (a.qsplit > 1 || (BIAS == ATTN_BIAS_BINS && a.dpos_w)) {
     const size_t n = std::max((size_t)BH * a.Nk * a.d, (size_t)a.H * 68);

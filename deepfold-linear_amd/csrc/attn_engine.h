@@ -311,9 +311,20 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_fwd2_kernel(AttnAr
     constexpr int RUN = M::RUN;
     T tmp[RUN];
     const int c0 = g * RUN;
+    if constexpr (FAST) {
+      // 16-byte blocks from a clamped row and block start; validity applied after
+      static_assert(RUN % VEC == 0, "whole 16-byte blocks per lane");
 #pragma unroll
-    for (int e = 0; e < RUN; ++e)
-      tmp[e] = (qrow && c0 + e < d) ? Qg[(size_t)qi * a.qsn + c0 + e] : from_f32<T>(0.f);
+      for (int k = 0; k < RUN / VEC; ++k)
+        *reinterpret_cast<uint4*>(tmp + VEC * k) =
+            *reinterpret_cast<const uint4*>(Qg + (size_t)qc * a.qsn + min(c0 + VEC * k, d - VEC));
+#pragma unroll
+      for (int e = 0; e < RUN; ++e) tmp[e] = (qrow && c0 + e < d) ? tmp[e] : from_f32<T>(0.f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < RUN; ++e)
+        tmp[e] = (qrow && c0 + e < d) ? Qg[(size_t)qi * a.qsn + c0 + e] : from_f32<T>(0.f);
+    }
     M::from_run(qf, tmp);
   }
 
@@ -509,7 +520,6 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_bwd_q2_kernel(Attn
   const T* Qg = reinterpret_cast<const T*>(a.q) + (size_t)b * a.qsb + (size_t)h * a.qsh;
   const T* Kg = reinterpret_cast<const T*>(a.k) + (size_t)b * a.ksb + (size_t)h * a.ksh;
   const T* Vg = reinterpret_cast<const T*>(a.v) + (size_t)b * a.ksb + (size_t)h * a.ksh;
-  const T* dOw = reinterpret_cast<const T*>(a.do_w) + (size_t)bh * Mq * DP;
   const float* kmask = a.kmask ? a.kmask + (size_t)b * Nk : nullptr;
   const float sc = a.scale * LOG2E;
   int k_lo = 0, k_hi = Nk;
@@ -537,26 +547,6 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_bwd_q2_kernel(Attn
     br.row = reinterpret_cast<const typename BR::BT*>(a.bins + ((size_t)b * Mq + qc) * Nk);
   }
 
-  typename M::Frag qf, df;
-  {
-    constexpr int RUN = M::RUN;
-    T tq[RUN], td[RUN];
-    const int c0 = g * RUN;
-#pragma unroll
-    for (int e = 0; e < RUN; ++e) {
-      tq[e] = (qrow && c0 + e < d) ? Qg[(size_t)qi * a.qsn + c0 + e] : from_f32<T>(0.f);
-      td[e] = qrow ? dOw[(size_t)qi * DP + c0 + e] : from_f32<T>(0.f);
-    }
-    M::from_run(qf, tq);
-    M::from_run(df, td);
-  }
-  // P = exp2(sc * (qk - l2 / sc) + bias): the -lse term rides in the MFMA accumulator
-  const float l2 = qok ? a.lse[(size_t)bh * Mq + qi] * LOG2E : POS_BIG;
-  const float Di = qok ? a.dcoef[(size_t)bh * Mq + qi] : 0.f;
-  const float ci = -l2 / sc;
-  const f32x4 cinit = {ci, ci, ci, ci};
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-
   Flight<T, LD, FAST> kfl, vfl;
   float kmraw;
   uint4 bcur[SPW][BW], bnxt[SPW][BW];
@@ -574,11 +564,87 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_bwd_q2_kernel(Attn
     }
   };
 
+  // Backward prep of the resident rows, for this pass and the dK/dV pass that runs
+  // after it: do_w = sigma(G) dO (zero for masked rows and padded columns),
+  // D_i = sum_c dO_ic O_ic, dG = (1 - sigma) O dO (O is the gated output).  The four
+  // lanes of a row (g = 0..3) own RUN columns each; waves ks = 0 write.  The row's
+  // operands are loaded from clamped addresses before chunk 0's prefetch is issued,
+  // so both round trips overlap.
+  constexpr int RUN = M::RUN;
+  const int c0r = g * RUN;
+  const size_t row = (size_t)bh * Mq + qc;
+  T rq[RUN], rdo[RUN], ro[RUN], rg[RUN];
+  {
+    const T* Qr = Qg + (size_t)qc * a.qsn;
+    const T* dO = reinterpret_cast<const T*>(a.dout) + row * d;
+    const T* Or = reinterpret_cast<const T*>(a.o) + row * d;
+    const T* Gr = a.g ? reinterpret_cast<const T*>(a.g) + (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)qc * a.qsn
+                      : Or;
+    if constexpr (FAST) {
+      // 16-byte blocks; d is a multiple of VEC, so a block is wholly inside or
+      // wholly outside the row (outside: a clamped block, zeroed below by c < d)
+      static_assert(RUN % VEC == 0, "whole 16-byte blocks per lane");
+#pragma unroll
+      for (int k = 0; k < RUN / VEC; ++k) {
+        const int cb = min(c0r + VEC * k, d - VEC);
+        *reinterpret_cast<uint4*>(rq + VEC * k) = *reinterpret_cast<const uint4*>(Qr + cb);
+        *reinterpret_cast<uint4*>(rdo + VEC * k) = *reinterpret_cast<const uint4*>(dO + cb);
+        *reinterpret_cast<uint4*>(ro + VEC * k) = *reinterpret_cast<const uint4*>(Or + cb);
+        *reinterpret_cast<uint4*>(rg + VEC * k) = *reinterpret_cast<const uint4*>(Gr + cb);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < RUN; ++e) {
+        const int c = min(c0r + e, d - 1);
+        rq[e] = Qr[c];
+        rdo[e] = dO[c];
+        ro[e] = Or[c];
+        rg[e] = Gr[c];
+      }
+    }
+  }
+  prefetch(k_lo);
+
+  typename M::Frag qf, df;
+  float Di;
+  {
+    T tq[RUN], td[RUN];
+    T* dGr = (a.g && a.dg && ks == 0 && qrow) ? reinterpret_cast<T*>(a.dg) + row * d : nullptr;
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < RUN; ++e) {
+      const int c = c0r + e;
+      const bool in = c < d;
+      tq[e] = (qrow && in) ? rq[e] : from_f32<T>(0.f);
+      const float dov = (qok && in) ? to_f32(rdo[e]) : 0.f;
+      const float ov = (qok && in) ? to_f32(ro[e]) : 0.f;
+      const float s = (qok && in && a.g) ? 1.f / (1.f + __expf(-to_f32(rg[e]))) : 1.f;
+      if (dGr && in) dGr[c] = from_f32<T>((1.f - s) * ov * dov);
+      td[e] = from_f32<T>(s * dov);
+      part += dov * ov;
+    }
+    part += __shfl_xor(part, 16, WAVE);
+    part += __shfl_xor(part, 32, WAVE);
+    Di = part;
+    if (ks == 0 && qrow) {
+      T* dst = reinterpret_cast<T*>(a.do_w) + row * DP + c0r;
+#pragma unroll
+      for (int e = 0; e < RUN; ++e) dst[e] = td[e];
+      if (g == 0) a.dcoef[row] = part;
+    }
+    M::from_run(qf, tq);
+    M::from_run(df, td);
+  }
+  // P = exp2(sc * (qk - l2 / sc) + bias): the -lse term rides in the MFMA accumulator
+  const float l2 = qok ? a.lse[(size_t)bh * Mq + qi] * LOG2E : POS_BIG;
+  const float ci = -l2 / sc;
+  const f32x4 cinit = {ci, ci, ci, ci};
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+
   f32x4 dq[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) dq[c] = zero;
 
-  prefetch(k_lo);
   int buf = 0;
   for (int c0 = k_lo; c0 < k_hi; c0 += CH, buf ^= 1) {
     unsigned char* base = smem + buf * BUF;
@@ -719,7 +785,9 @@ template <typename T, int DP>
 struct EngKV {
   using E = Eng<T, DP, false>;
   static constexpr int RK = 64, RT = 4, KS = 2, NT = 512;
-  static constexpr int CH = E::CH, RS = E::RS, TS = E::TS, VEC = E::VEC, CB = E::CB, LD = E::LD, SPW = E::SPW;
+  static constexpr int CH = E::CH, RS = E::RS, TS = E::TS, VEC = E::VEC, CB = E::CB;
+  static constexpr int LD = CH * CB / NT, SPW = CH / 32 / KS;
+  static_assert(SPW >= 1 && CH * CB % NT == 0 && LD >= 1, "dK/dV pass geometry");
 };
 template <typename T, int DP>
 constexpr int attn_bwdkv_lds() {
@@ -842,10 +910,28 @@ __global__ void __launch_bounds__(512) attn_bwd_kv2_kernel(AttnArgs a) {
     T tk[RUN], tv[RUN];
     const int c0 = g * RUN;
     const bool krow = kj < Nk;
+    if constexpr (FAST) {
+      // 16-byte blocks from a clamped row and block start; validity applied after
+      static_assert(RUN % VEC == 0, "whole 16-byte blocks per lane");
+      const size_t ro = (size_t)min(kj, Nk - 1) * a.ksn;
 #pragma unroll
-    for (int e = 0; e < RUN; ++e) {
-      tk[e] = (krow && c0 + e < d) ? Kg[(size_t)kj * a.ksn + c0 + e] : from_f32<T>(0.f);
-      tv[e] = (krow && c0 + e < d) ? Vg[(size_t)kj * a.ksn + c0 + e] : from_f32<T>(0.f);
+      for (int k = 0; k < RUN / VEC; ++k) {
+        const int cb = min(c0 + VEC * k, d - VEC);
+        *reinterpret_cast<uint4*>(tk + VEC * k) = *reinterpret_cast<const uint4*>(Kg + ro + cb);
+        *reinterpret_cast<uint4*>(tv + VEC * k) = *reinterpret_cast<const uint4*>(Vg + ro + cb);
+      }
+#pragma unroll
+      for (int e = 0; e < RUN; ++e) {
+        const bool in = krow && c0 + e < d;
+        tk[e] = in ? tk[e] : from_f32<T>(0.f);
+        tv[e] = in ? tv[e] : from_f32<T>(0.f);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < RUN; ++e) {
+        tk[e] = (krow && c0 + e < d) ? Kg[(size_t)kj * a.ksn + c0 + e] : from_f32<T>(0.f);
+        tv[e] = (krow && c0 + e < d) ? Vg[(size_t)kj * a.ksn + c0 + e] : from_f32<T>(0.f);
+      }
     }
     M::from_run(kf, tk);
     M::from_run(vf, tv);

@@ -85,11 +85,14 @@ def test_diffusion_forward_backward(B, H, N, D, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_diffusion_pair_bias_and_gate(dtype):
-    """cfg3-shaped extension (smaller N): dense pair bias + sigmoid gate, D = 24."""
+@pytest.mark.parametrize("N,D", [(160, 24), (150, 20)])
+def test_diffusion_pair_bias_and_gate(N, D, dtype):
+    """cfg3-shaped extension (smaller N): dense pair bias + sigmoid gate.  N = 150 is not
+    a multiple of 8, so the kernels take their element-load staging (and D = 20 is not a
+    whole number of 16-byte bf16 blocks)."""
     from deepfold_amd import flash_diffusion_attn
 
-    B, H, N, D = 1, 4, 160, 24
+    B, H = 1, 4
     Q, K, V, G = (rnd(B, H, N, D, seed=s, dtype=dtype) for s in (11, 12, 13, 14))
     bias = rnd(B, H, N, N, seed=15, dtype=dtype)
     go = rnd(B, H, N, D, seed=16, dtype=dtype)

@@ -174,10 +174,11 @@ def _check(vg, L, vr, gr, tol):
         assert_close_rel(got, gr[k].numpy(), tol, f"grad {k}")
 
 
-# the last case is the headline layout (B2 H8 N768, n_b = [501, 759]: two and three
-# resident tiles per member, Q and K resident in LDS)
+# (2, 8, 768, ...) is the headline layout (B2 H8 N768, n_b = [501, 759]: two and three
+# resident tiles per member, Q and K resident in LDS); at N = 832 resident operands would
+# need 166752 bytes of LDS (over 160 KiB), so that case reads Q and K from L2
 @pytest.mark.parametrize("B,H,N,d,K,lens", [(2, 4, 96, 32, 6, [96, 61]), (1, 2, 300, 24, 4, [290]),
-                                             (2, 8, 768, 32, 3, [501, 759])])
+                                             (2, 8, 768, 32, 3, [501, 759]), (1, 2, 832, 32, 3, [829])])
 def test_unrolled_content_only_bf16(B, H, N, d, K, lens):
     """The content-only cost (the build the headline workload runs) with bf16 inputs
     at d <= 32 (Q and K resident in LDS)."""
