@@ -204,7 +204,7 @@ static bool attn_fast(const AttnArgs& a, bool with_q) {
 template <typename T, int DP, int BIAS, bool WIN, bool FAST>
 static hipError_t attn_fwd_f(const AttnArgs& a, hipStream_t s) {
   using E = Eng<T, DP, WIN>;
-  constexpr int lds = attn_fwd_lds<T, DP, WIN>();
+  const int lds = attn_fwd_lds<T, DP, WIN>() + (a.g ? attn_fwd_gate_lds<T, DP, WIN>() : 0);
   auto kern = attn_fwd2_kernel<T, DP, BIAS, WIN, FAST>;
   const hipError_t attr = set_lds_limit((const void*)kern, lds);
   if (attr != hipSuccess) return attr;

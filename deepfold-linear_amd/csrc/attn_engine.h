@@ -255,6 +255,12 @@ constexpr int attn_fwd_lds() {
   using E = Eng<T, DP, WIN>;
   return 2 * lds_align(E::CH * E::RS * (int)sizeof(T) + DP * E::TS * (int)sizeof(T) + E::CH * 4) + 68 * 4;
 }
+// LDS of the gate rows a gated forward parks after attn_fwd_lds (launched only with a gate,
+// so that ungated launches keep their occupancy)
+template <typename T, int DP, bool WIN>
+constexpr int attn_fwd_gate_lds() {
+  return Eng<T, DP, WIN>::RQ * DP * (int)sizeof(T);
+}
 
 template <typename T, int DP, int BIAS, bool WIN, bool FAST>
 __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_fwd2_kernel(AttnArgs a) {
@@ -270,6 +276,7 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_fwd2_kernel(AttnAr
   constexpr int BUF = lds_align(BOFF + CH * 4);
   extern __shared__ __align__(16) unsigned char smem[];
   float* s_pw = reinterpret_cast<float*>(smem + 2 * BUF);
+  T* s_g = reinterpret_cast<T*>(smem + 2 * BUF + 68 * 4);  // [RQ][DP] gate rows (gated launches only)
 
   const int t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE, g = lane >> 4;
   const int rt = wave % RT, ks = wave / RT;
@@ -290,6 +297,22 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_fwd2_kernel(AttnAr
   const float sc = a.scale * LOG2E;
   int k_lo = 0, k_hi = Nk;
   if (WIN) window_keys2(q0, Nk, k_lo, k_hi);
+
+  // The gate rows of the workgroup (gated launches) are loaded now, from clamped
+  // addresses, and parked in LDS once chunk 0's prefetch is in flight, so the
+  // epilogue reads them without a global round trip.
+  constexpr int GPT = E::RQ * DP / NT;  // gate elements per thread
+  static_assert(E::RQ * DP % NT == 0, "gate staging geometry");
+  const bool hasg = a.g != nullptr;
+  T gpre[GPT];
+  if (hasg) {
+    const T* Gb = reinterpret_cast<const T*>(a.g) + (size_t)b * a.qsb + (size_t)h * a.qsh;
+#pragma unroll
+    for (int u = 0; u < GPT; ++u) {
+      const int e = t + NT * u;
+      gpre[u] = Gb[(size_t)min(q0 + e / DP, Mq - 1) * a.qsn + min(e % DP, d - 1)];
+    }
+  }
 
   if (BIAS == ATTN_BIAS_BINS)
     for (int k = t; k < 68; k += NT) s_pw[k] = LOG2E * a.pos_w[h * 68 + k];
@@ -353,6 +376,10 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_fwd2_kernel(AttnAr
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 
   prefetch(k_lo);
+  if (hasg) {
+#pragma unroll
+    for (int u = 0; u < GPT; ++u) s_g[t + NT * u] = gpre[u];
+  }
   int buf = 0;
   for (int c0 = k_lo; c0 < k_hi; c0 += CH, buf ^= 1) {
     unsigned char* base = smem + buf * BUF;
@@ -460,8 +487,7 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_fwd2_kernel(AttnAr
   const float inv = qok ? 1.f / lsum : 0.f;
   if (!qrow) return;
   T* O = reinterpret_cast<T*>(a.o) + ((size_t)bh * Mq + qi) * d;
-  const T* Gr = a.g ? reinterpret_cast<const T*>(a.g) + (size_t)b * a.qsb + (size_t)h * a.qsh + (size_t)qi * a.qsn
-                    : nullptr;
+  const T* Gr = s_g + (size_t)(qi - q0) * DP;  // staged gate row (LDS)
   // lane holds O^T[col = c*16 + 4g + r][query qi]
 #pragma unroll
   for (int c = 0; c < NC; ++c)
@@ -470,7 +496,7 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_fwd2_kernel(AttnAr
       const int col = c * 16 + 4 * g + r;
       if (col < d) {
         float o = oacc[c][r] * inv;
-        if (Gr) o *= 1.f / (1.f + __expf(-to_f32(Gr[col])));
+        if (hasg) o *= 1.f / (1.f + __expf(-to_f32(Gr[col])));
         O[col] = from_f32<T>(o);
       }
     }
