@@ -568,7 +568,21 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_bwd_q2_kernel(Attn
     const size_t off = (((size_t)w * a.H + h) * ATTN_WQ + (qc - ATTN_WQ * w)) * ATTN_WK;
     const int kofs = ATTN_WQ * w - ATTN_WOFF;
     br.row = reinterpret_cast<const typename BR::BT*>(reinterpret_cast<const T*>(a.bias) + off - kofs);
-    if (a.dbias) drow = reinterpret_cast<T*>(a.dbias) + off - kofs;
+    if (a.dbias) {
+      drow = reinterpret_cast<T*>(a.dbias) + off - kofs;
+      // The main loop writes the window's keys [k_lo, k_hi) of its rows < Mq; the rest of
+      // the (32, 128) slab (keys clipped at the sequence ends, rows past Mq) is zeroed
+      // here, so the caller need not clear the gradient.  The window bias has no batch
+      // dimension: the C ABI admits its gradient only for B = 1.
+      // (only windows at the sequence ends have such entries: a uniform test)
+      if (k_lo > kofs || k_hi < kofs + ATTN_WK || q0 + ATTN_WQ > Mq) {
+        T* slab = reinterpret_cast<T*>(a.dbias) + ((size_t)w * a.H + h) * ATTN_WQ * ATTN_WK;
+        for (int e = t; e < ATTN_WQ * ATTN_WK; e += NT) {
+          const int key = kofs + (e % ATTN_WK);
+          if (q0 + e / ATTN_WK >= Mq || key < k_lo || key >= k_hi) slab[e] = from_f32<T>(0.f);
+        }
+      }
+    }
   } else if (BIAS == ATTN_BIAS_BINS) {
     br.row = reinterpret_cast<const typename BR::BT*>(a.bins + ((size_t)b * Mq + qc) * Nk);
   }

@@ -353,6 +353,10 @@ int check_attn(const dfl_attn_params* p, bool bwd) {
   if (p->window && p->Mq != p->Nk) return fail("windowed attention needs Mq == Nk");
   if (p->bias_mode == DFL_ATTN_BIAS_WINDOW && !p->window) return fail("a window bias needs window = 1");
   if (bwd && (!p->grad_o || !p->dq || !p->dk || !p->dv)) return fail("grad_o, dq, dk and dv are required");
+  // the window bias is shared by the batch, so its gradient is a sum over batch rows,
+  // which one launch does not form: call once per batch row and add the slabs
+  if (bwd && p->bias_mode == DFL_ATTN_BIAS_WINDOW && p->dbias && p->B > 1)
+    return fail("the window-bias gradient needs B = 1 per call (the bias is shared by the batch; sum per-row calls)");
   return 0;
 }
 

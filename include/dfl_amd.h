@@ -266,9 +266,10 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
  * Forward outputs: o (B,H,Mq,d) element type of q, contiguous; lse (B,H,Mq) fp32.
  * Backward inputs: grad_o (B,H,Mq,d) contiguous, plus the forward's o and lse;
  * outputs (element type of q, contiguous): dq, dk, dv; dg if g; dbias if a dense
- * or window bias is given (may be NULL; a window bias gradient must be
- * zero-filled by the caller: entries outside each window are not written);
- * dpos_weight (H,68) fp32 for BINS (may be NULL).
+ * or window bias is given (may be NULL; every entry is written, window entries
+ * outside the sequence as zero).  The window bias is shared by the batch, so a
+ * window-bias gradient is accepted only with B = 1: call once per batch row and
+ * sum the slabs.  dpos_weight (H,68) fp32 for BINS (may be NULL).
  */
 enum dfl_attn_bias { DFL_ATTN_BIAS_NONE = 0, DFL_ATTN_BIAS_BINS = 1, DFL_ATTN_BIAS_DENSE = 2, DFL_ATTN_BIAS_WINDOW = 3 };
 

@@ -139,6 +139,23 @@ def test_pending_error_is_clear_without_launches(lib_path):
     _lib.raise_pending("test")
 
 
+def test_attn_bwd_refuses_batched_window_bias_gradient(lib_path):
+    """The window bias is shared by the batch; its gradient is a batch sum that one
+    launch does not form, so the entry point refuses B > 1 before any GPU work (the
+    pointers are never dereferenced: argument checks come first)."""
+    from deepfold_amd import _lib
+
+    lib = _lib.load(lib_path)
+    fake = 4096
+    p = _lib.AttnParams(dtype=_lib.DFL_BF16, q=fake, k=fake, v=fake, q_stride_b=64 * 32, q_stride_h=64 * 32,
+                        q_stride_n=32, k_stride_b=64 * 32, k_stride_h=64 * 32, k_stride_n=32,
+                        bias_mode=_lib.DFL_ATTN_BIAS_WINDOW, bias=fake, window=1, B=2, H=1, Mq=64, Nk=64, d=32,
+                        scale=1.0, o=fake, lse=fake, grad_o=fake, dq=fake, dk=fake, dv=fake, dbias=fake)
+    rc = lib.dfl_attn_bwd(ctypes.byref(p), None, 0, None)
+    assert rc != 0
+    assert "B = 1" in lib.dfl_last_error().decode()
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
     from deepfold_amd import (atom_to_token_attn, balanced_sinkhorn_transport, balanced_sinkhorn_transport_dual,

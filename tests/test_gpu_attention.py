@@ -122,7 +122,7 @@ def test_diffusion_unbatched_and_no_mask():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("B,H,M,D,with_mask,with_bias", [
     (1, 4, 256, 32, False, False), (2, 4, 100, 32, True, False), (1, 2, 75, 64, True, True),
-    (1, 4, 512, 32, True, True)])
+    (1, 4, 512, 32, True, True), (3, 2, 150, 32, True, True)])
 def test_atom_window_attention(B, H, M, D, with_mask, with_bias, dtype):
     from deepfold_amd import flash_atom_attn
 
