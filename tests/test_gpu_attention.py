@@ -85,11 +85,11 @@ def test_diffusion_forward_backward(B, H, N, D, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("N,D", [(160, 24), (150, 20)])
+@pytest.mark.parametrize("N,D", [(160, 24), (150, 20), (96, 64)])
 def test_diffusion_pair_bias_and_gate(N, D, dtype):
     """cfg3-shaped extension (smaller N): dense pair bias + sigmoid gate.  N = 150 is not
     a multiple of 8, so the kernels take their element-load staging (and D = 20 is not a
-    whole number of 16-byte bf16 blocks)."""
+    whole number of 16-byte bf16 blocks); D = 64 runs the 64-wide head instantiations."""
     from deepfold_amd import flash_diffusion_attn
 
     B, H = 1, 4
