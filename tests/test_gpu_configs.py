@@ -158,6 +158,9 @@ def _ragged_case(B, H, N, d, lengths, seed, dtype, eps):
     (torch.bfloat16, 2e-2, 192, [192, 161, 177, 128], {2, 3}, "cg"),
     # 8 tiles per member (one wave per tile in the split passes)
     (torch.bfloat16, 2e-2, 512, [512, 497, 400, 330], {6, 7, 8}, "cg"),
+    # 9-10 tiles per member: the heavy passes give waves whole tiles, the forward's sweep
+    # runs resident chunks of 4 + 4 + 1-2 tiles
+    (torch.bfloat16, 2e-2, 640, [640, 600, 560, 530], {9, 10}, "cg"),
 ])
 def test_resident_multi_tile(dtype, tol, N, lengths, expect, solver):
     B, H, d, K = 4, 16, 32, 12
