@@ -186,6 +186,18 @@ def test_unrolled_content_only_bf16(B, H, N, d, K, lens):
     _check(*_content_only(B, H, N, d, K, lens, torch.bfloat16), 2e-2)
 
 
+# B*H = 64 -> 4 members per head: 5-6 resident tiles per member (strided wave mapping,
+# two tiles a wave on some SIMDs) and 8-10 (whole tiles per wave); fp32 reads Q and K from L2
+@pytest.mark.parametrize("N,lens,dtype,tol", [
+    (384, [384, 350, 300, 330], torch.bfloat16, 2e-2),
+    (640, [640, 600, 560, 530], torch.bfloat16, 2e-2),
+    (384, [384, 350, 300, 330], torch.float32, 1e-4),
+])
+def test_unrolled_many_tiles_per_member(N, lens, dtype, tol):
+    print(f"case many tiles B4 H16 N{N} {dtype}", flush=True)
+    _check(*_content_only(4, 16, N, 32, 3, lens, dtype), tol)
+
+
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
 def test_unrolled_exact_factor_path(dtype, tol):
     """Sweeps whose exponential ratio leaves the factored range take the exact path."""
