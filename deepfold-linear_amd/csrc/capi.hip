@@ -98,28 +98,51 @@ int hip_fail(hipError_t e, const char* what) {
 int cu_count();
 
 // Launch mode of the persistent kernels, whose group members wait on each other and
-// so must all be resident at once.  A grid of at most one workgroup per CU
-// (dfl::grid_blocks(n_groups, G) <= CU count, which group_size() arranges) is
-// launched as an ordinary launch: on an otherwise idle device every workgroup is
-// resident at once, and a member kept waiting by other work on the device shows up
-// as an expired wait (error 2), not a hang.  A cooperative launch also guarantees
+// so must all be resident at once.  DFL_LAUNCH_AUTO launches a grid of at most one
+// workgroup per CU (dfl::grid_blocks(n_groups, G) <= CU count, which group_size()
+// arranges) as an ordinary launch: on an otherwise idle device every workgroup is
+// resident at once.  If other kernels hold CUs when it starts, a member that cannot
+// become resident leaves the others polling: their waits give up after about 2-4 s,
+// the call's outputs are invalid, and the error (code 2) is raised by the next call
+// (dfl_pending_error) or dfl_workspace_error.  DFL_LAUNCH_COOPERATIVE guarantees
 // residency against concurrent kernels on other streams, at about 12-16 us more per
-// launch on MI355X (measured: cfg2 layer 0.602 vs 0.572 ms).  DFL_AMD_COOP=1 forces
-// cooperative launches (callers that run other kernels concurrently), DFL_AMD_COOP=0
-// forces ordinary ones; grids larger than the CU count are always cooperative (the
-// runtime then checks that they fit).  rocprofv3 ends with SIGSEGV in its exit-time
-// teardown after any cooperative launch, even of a trivial kernel, so the committed
-// profiles use DFL_AMD_COOP=0.
+// launch on MI355X (measured: cfg2 layer 0.602 vs 0.572 ms); grids larger than the
+// CU count are always cooperative (the runtime then checks that they fit).
+// rocprofv3 ends with SIGSEGV in its exit-time teardown after any cooperative
+// launch, even of a trivial kernel, so the committed profiles use ordinary launches.
+// Process-wide launch mode (dfl_set_launch_mode); its start value comes from
+// DFL_AMD_COOP ("1" cooperative, "0" ordinary), else DFL_LAUNCH_AUTO.
+std::atomic<int> g_launch_mode{[] {
+  const char* v = std::getenv("DFL_AMD_COOP");
+  if (v && v[0] == '1' && v[1] == 0) return (int)DFL_LAUNCH_COOPERATIVE;
+  if (v && v[0] == '0' && v[1] == 0) return (int)DFL_LAUNCH_ORDINARY;
+  return (int)DFL_LAUNCH_AUTO;
+}()};
 bool coop_launch(int G, int n_groups) {
-  static const int mode = [] {
-    const char* v = std::getenv("DFL_AMD_COOP");
-    if (v && v[0] == '1' && v[1] == 0) return 1;
-    if (v && v[0] == '0' && v[1] == 0) return 0;
-    return -1;
-  }();
-  if (G <= 1 || mode == 0) return false;
-  if (mode == 1) return true;
+  const int mode = g_launch_mode.load(std::memory_order_relaxed);
+  if (G <= 1 || mode == DFL_LAUNCH_ORDINARY) return false;
+  if (mode == DFL_LAUNCH_COOPERATIVE) return true;
   return dfl::grid_blocks(n_groups, G) > cu_count();
+}
+
+// Polls a cross-workgroup wait makes before it gives up (dfl_debug_set_spin_limit).
+std::atomic<uint32_t> g_spin_limit{dfl::SPIN_LIMIT};
+
+// The persistent kernels tag their exchange words with a salt chosen on the host
+// per call, so a graph that captured one call would replay that salt, and a replay
+// would accept the words an earlier replay left in the workspace.  Such captures are
+// refused; the allocation-free forward, which clears its scratch with a kernel on
+// every call, is the entry point for graph capture.
+int refuse_capture(void* stream, const char* what) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;  // not a capturing stream (a launch into an invalid capture fails on its own)
+  }
+  if (st != hipStreamCaptureStatusNone)
+    return fail("%s cannot be captured into a HIP graph (its exchange tags are chosen on the host per call); "
+                "dfl_sinkhorn_fwd_noalloc supports capture", what);
+  return 0;
 }
 
 std::atomic<uint64_t> g_salt_counter{1};
@@ -199,6 +222,7 @@ dfl::ErrRef err_ref(void* workspace, bool may_allocate = true) {
   dfl::ErrRef r;
   r.ws = static_cast<uint32_t*>(workspace);
   r.host = may_allocate ? mailbox() : g_mailbox_dev.load();
+  r.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   return r;
 }
 
@@ -447,6 +471,7 @@ struct FwdScratch {
   bool allow_stream;   // false: the buffer has no stream region
   WsState* fixed;      // salt-epoch record of a library-owned buffer (else the map)
   bool may_allocate;   // the host mailbox may be allocated by this call
+  bool clear_always;   // clear header and exchange words with a fill kernel on every call
 };
 
 // Storage-mode choice, workspace pointers and launches of the persistent forward
@@ -471,8 +496,19 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
   a.G = G;
   // the forward's exchange words: u and v of every (b,h), then 32 placement words per (b,h)
   const size_t xch_end = WS_HEADER + (size_t)a.B * a.H * (2 * np32(a.N) + 32) * 8;
-  if (int rc = acquire_salt(ws, xch_end, stream, &a.salt, w.fixed))
-    return hip_fail((hipError_t)rc, "workspace clear launch");
+  if (w.clear_always) {
+    // every call starts from zeroed words, so a replay of a captured call (same salt)
+    // never meets an earlier replay's words
+    hipError_t e = dfl::launch_fill_u64(reinterpret_cast<uint64_t*>(ws), xch_end / 8, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "scratch clear launch");
+    uint64_t c = g_salt_counter.fetch_add(1);
+    if ((c & 0xfffffu) == 0) c = g_salt_counter.fetch_add(1);
+    a.salt = (uint32_t)(c & 0xfffffu);
+  } else {
+    if (int rc = refuse_capture(stream, "dfl_sinkhorn_fwd")) return rc;
+    if (int rc = acquire_salt(ws, xch_end, stream, &a.salt, w.fixed))
+      return hip_fail((hipError_t)rc, "workspace clear launch");
+  }
   if (a.bins)
     if (int rc = prepare_bins8(a.bins, a.B, a.N, workspace, w.bins_off, &a.bins8, &a.bins8t, stream)) return rc;
   const bool coop = coop_launch(G, a.B * a.H);
@@ -599,6 +635,20 @@ int dfl_pending_error(void) {
   return code;
 }
 
+int dfl_set_launch_mode(int mode) {
+  if (mode != DFL_LAUNCH_AUTO && mode != DFL_LAUNCH_ORDINARY && mode != DFL_LAUNCH_COOPERATIVE)
+    return fail("unknown launch mode %d", mode);
+  g_launch_mode.store(mode);
+  return 0;
+}
+
+int dfl_get_launch_mode(void) { return g_launch_mode.load(); }
+
+int dfl_debug_set_spin_limit(unsigned limit) {
+  g_spin_limit.store(limit == 0 ? dfl::SPIN_LIMIT : (uint32_t)limit);
+  return 0;
+}
+
 int dfl_workspace_error(const void* workspace, void* stream) {
   if (!workspace) return fail("workspace is NULL");
   uint32_t words[2] = {0, 0};
@@ -618,7 +668,7 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
   const size_t need = dfl_sinkhorn_workspace_size(p->B, p->H, p->N);
   if (!workspace || workspace_bytes < need) return fail("workspace too small: need %zu bytes", need);
   const FwdScratch w{static_cast<unsigned char*>(workspace), sinkhorn_bins8_offset(p->B, p->H, p->N), true, nullptr,
-                     true};
+                     true, false};
   return run_fwd(a, p->dtype == DFL_BF16, head_dim_pad(p->d), p->storage, w, stream);
 }
 
@@ -653,8 +703,22 @@ int dfl_sinkhorn_fwd_noalloc(const dfl_sinkhorn_fwd_params* p, void* stream) {
       slot->state = WsState{~(uint64_t)0, 0};  // first use clears the exchange region
     }
   }
-  const FwdScratch w{slot->ptr, bins_off, false, &slot->state, false};
+  const FwdScratch w{slot->ptr, bins_off, false, &slot->state, false, true};
   return run_fwd(a, p->dtype == DFL_BF16, head_dim_pad(p->d), p->storage, w, stream);
+}
+
+int dfl_noalloc_error(void* stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= MAX_DEVICES) return fail("device %d outside [0, %d)", dev, MAX_DEVICES);
+  unsigned char* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    base = g_scratch[dev].ptr;
+  }
+  if (!base) return 0;  // no allocation-free call has run on this device
+  return dfl_workspace_error(base, stream);
 }
 
 int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
@@ -720,6 +784,7 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
   a.go_t = cur + 2 * opb;
   a.dcoef = reinterpret_cast<float*>(cur + 3 * opb);
   a.G = G;
+  if (int rc = refuse_capture(stream, "dfl_sinkhorn_bwd")) return rc;
   if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
     return hip_fail((hipError_t)rc, "workspace clear launch");
   a.ch = CH;
@@ -986,7 +1051,7 @@ int dfl_balanced_fwd(const dfl_balanced_fwd_params* p, void* workspace, size_t w
   a.x_centroid = p->x_centroid; a.o_avg = p->h_centroid;
   a.log_u = p->log_u; a.log_v = p->log_v; a.log_z = p->log_z;
   a.balanced = 1; a.alpha = p->alpha_h; a.r_h = p->r_h; a.hist = p->hist;
-  const FwdScratch w{static_cast<unsigned char*>(workspace), 0, true, nullptr, true};  // no bins
+  const FwdScratch w{static_cast<unsigned char*>(workspace), 0, true, nullptr, true, false};  // no bins
   return run_fwd(a, false, head_dim_pad(p->d), p->storage, w, stream);
 }
 
@@ -1036,6 +1101,7 @@ int dfl_balanced_bwd(const dfl_balanced_bwd_params* p, void* workspace, size_t w
   a.err = err_ref(ws);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
+  if (int rc = refuse_capture(stream, "dfl_balanced_bwd")) return rc;
   if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
     return hip_fail((hipError_t)rc, "workspace clear launch");
   e = dfl::launch_balanced_bwd(a, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H));
@@ -1109,6 +1175,7 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
   a.err = err_ref(ws);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
+  if (int rc = refuse_capture(stream, "dfl_sinkhorn_unrolled_bwd")) return rc;
   if (int rc = acquire_salt(ws, WS_HEADER + xch_words(p->B, p->H, p->N) * 8, stream, &a.salt))
     return hip_fail((hipError_t)rc, "workspace clear launch");
   e = dfl::launch_unrolled_bwd(a, p->dtype == DFL_BF16, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H),

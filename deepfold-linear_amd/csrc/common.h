@@ -255,8 +255,10 @@ constexpr uint32_t SPIN_LIMIT = 1u << 22;  // ~2-4 s of polling
 // device-mapped host memory that the host reads at its next call without a
 // synchronisation (only a kernel that gives up writes it).
 struct ErrRef {
-  uint32_t* ws;    // workspace error word (word 1 of the header holds the latest salt)
-  uint32_t* host;  // mapped host mailbox, or null
+  uint32_t* ws;         // workspace error word (word 1 of the header holds the latest salt)
+  uint32_t* host;       // mapped host mailbox, or null
+  uint32_t spin_limit;  // polls before a wait gives up: SPIN_LIMIT, lowered only by tests
+                        // of the failure path (dfl_debug_set_spin_limit)
 };
 __device__ __forceinline__ void raise_error(ErrRef err, uint32_t salt, uint32_t code) {
   const uint32_t w = (salt << 12) | (code & 0xfffu);

@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(PNT) peak_exchange(uint64_t* buf, uint32_t* er
   if (!group_of(groups, XG, grp, member)) return;
   if (threadIdx.x == 0) s_flag = 0;
   __syncthreads();
-  const ErrRef err{errw, nullptr};
+  const ErrRef err{errw, nullptr, SPIN_LIMIT};
   const bool local = xcc_placed();
   float acc = 0.f;
   const long long t0 = clock64();

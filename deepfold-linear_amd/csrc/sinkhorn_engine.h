@@ -234,7 +234,7 @@ __device__ __forceinline__ bool poll_batch(const uint64_t* buf, int base, int n,
     // would leave the compiler unable to count the loads in flight, and it would then
     // wait for all of them.  A member that gave up stops publishing, so the others'
     // waits expire too, within the spin limit (well under a second).
-    if (++spins > SPIN_LIMIT / 2) { raise_error(err, salt, 2u); return false; }
+    if (++spins > err.spin_limit / 2) { raise_error(err, salt, 2u); return false; }
   }
 }
 
@@ -609,7 +609,7 @@ __device__ __forceinline__ bool read_placement(const uint64_t* pw, int G, int n_
         break;
       }
       __builtin_amdgcn_s_sleep(1);
-      if (++spins > SPIN_LIMIT) { raise_error(err, salt, 2u); *s_flag = 1; break; }
+      if (++spins > err.spin_limit) { raise_error(err, salt, 2u); *s_flag = 1; break; }
       if ((spins & 255u) == 0u && error_raised(err, salt)) { *s_flag = 1; break; }
     }
   }

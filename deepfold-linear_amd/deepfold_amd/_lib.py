@@ -25,6 +25,9 @@ DFL_IFT_ANALYTIC = 1
 DFL_STORAGE_AUTO = 0
 DFL_STORAGE_RESIDENT = 1
 DFL_STORAGE_STREAM = 2
+DFL_LAUNCH_AUTO = 0
+DFL_LAUNCH_ORDINARY = 1
+DFL_LAUNCH_COOPERATIVE = 2
 
 _lock = threading.Lock()
 _lib = None
@@ -224,9 +227,13 @@ SIGNATURES = [
     ("dfl_version", ctypes.c_char_p, []),
     ("dfl_workspace_error", I32, [P, P]),
     ("dfl_pending_error", I32, []),
+    ("dfl_set_launch_mode", I32, [I32]),
+    ("dfl_get_launch_mode", I32, []),
+    ("dfl_debug_set_spin_limit", I32, [ctypes.c_uint]),
     ("dfl_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
     ("dfl_sinkhorn_fwd", I32, [ctypes.POINTER(SinkhornFwdParams), P, ctypes.c_size_t, P]),
     ("dfl_sinkhorn_fwd_noalloc", I32, [ctypes.POINTER(SinkhornFwdParams), P]),
+    ("dfl_noalloc_error", I32, [P]),
     ("dfl_sinkhorn_bwd", I32, [ctypes.POINTER(SinkhornBwdParams), P, ctypes.c_size_t, P]),
     ("dfl_sinkhorn_unrolled_workspace_size", ctypes.c_size_t, [I32, I32, I32, I32]),
     ("dfl_sinkhorn_unrolled_bwd", I32, [ctypes.POINTER(SinkhornUnrolledBwdParams), P, ctypes.c_size_t, P]),
@@ -350,6 +357,15 @@ def timed_launch(name: str, device: torch.device, fn):
     e.record(stream)
     launch_timings.append((name, s, e))
     return rc
+
+
+def set_launch_mode(mode: int) -> None:
+    """Process-wide launch mode of the persistent kernels (``DFL_LAUNCH_*``)."""
+    check(load().dfl_set_launch_mode(int(mode)), "dfl_set_launch_mode")
+
+
+def get_launch_mode() -> int:
+    return int(load().dfl_get_launch_mode())
 
 
 def debug_checks() -> bool:

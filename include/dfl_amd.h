@@ -23,9 +23,12 @@
  *    error in the workspace, which dfl_workspace_error() reports (it
  *    synchronises `stream`), and in a pinned host word, which
  *    dfl_pending_error() reads without synchronising.
- *  - Exchange words are tagged with a 20-bit call salt.  When the salt wraps
- *    (every 2^20 calls), the first call on each workspace clears that
- *    workspace's exchange region with a fill kernel on its stream.
+ *  - Exchange words are tagged with a 20-bit call salt chosen on the host per
+ *    call.  When the salt wraps (every 2^20 calls), the first call on each
+ *    workspace clears that workspace's exchange region with a fill kernel on its
+ *    stream.  Because the salt is fixed at call time, the workspace entry points
+ *    of the persistent kernels refuse a stream that is capturing a HIP graph
+ *    (argument error); dfl_sinkhorn_fwd_noalloc is the capturable forward.
  */
 #ifndef DFL_AMD_H
 #define DFL_AMD_H
@@ -54,6 +57,29 @@ int dfl_workspace_error(const void* workspace, void* stream);
  * The reference has no counterpart: its ops fall back to the CPU on any exception
  * (flash_sinkhorn_attn.py:144, 751); here a failure is reported, never hidden. */
 int dfl_pending_error(void);
+
+/* Launch mode of the persistent kernels (the Sinkhorn forward and backwards), whose
+ * workgroups wait on each other and so must all be resident at once.  No counterpart
+ * in the reference, whose Triton launches are independent (sinkhorn_kernel.py:1991-2011).
+ *  DFL_LAUNCH_AUTO (default): grids of at most one workgroup per CU are ordinary
+ *    launches.  On an otherwise idle device all workgroups are resident.  If other
+ *    kernels hold CUs (concurrent streams), a workgroup that cannot start leaves the
+ *    others polling: their waits give up after about 2-4 s, the call's outputs are
+ *    invalid, and error 2 is reported by dfl_pending_error() / dfl_workspace_error().
+ *  DFL_LAUNCH_ORDINARY: always ordinary launches.
+ *  DFL_LAUNCH_COOPERATIVE: cooperative launches, which the runtime makes resident as
+ *    a whole even beside concurrent kernels, at about 12-16 us more per launch.
+ * The process starts in COOPERATIVE if the environment sets DFL_AMD_COOP=1, ORDINARY
+ * if it sets DFL_AMD_COOP=0, else AUTO.  Process-wide; returns 0 or an argument error. */
+enum dfl_launch_mode { DFL_LAUNCH_AUTO = 0, DFL_LAUNCH_ORDINARY = 1, DFL_LAUNCH_COOPERATIVE = 2 };
+int dfl_set_launch_mode(int mode);
+int dfl_get_launch_mode(void);
+
+/* For tests of the failure path only: the number of polls after which a
+ * cross-workgroup wait gives up (0 restores the default of about 2-4 s).  A tiny
+ * limit makes the persistent kernels' waits expire, so they report error 2 and exit
+ * normally.  No counterpart in the reference.  Process-wide; returns 0. */
+int dfl_debug_set_spin_limit(unsigned limit);
 
 /* ---------------------------------------------------------------------------
  * Flash-Sinkhorn forward.
@@ -124,9 +150,17 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
  * held until the process ends: it needs 256 + 16*B*H*(Np + 16) bytes (+ 2*B*Np*Np
  * with pos_bins), Np = N rounded up to 32, and rejects larger problems.  Every call on
  * one GPU shares that array, so calls that overlap in time on one GPU race.  It
- * calls no hipMalloc / hipFree and no allocating library routine. */
+ * calls no hipMalloc / hipFree and no allocating library routine.  Every call first
+ * clears the array's header and exchange words with a fill kernel on `stream`, so a
+ * HIP graph that captured the call can be replayed with new input values. */
 #define DFL_NOALLOC_SCRATCH_BYTES (8u << 20)
 int dfl_sinkhorn_fwd_noalloc(const dfl_sinkhorn_fwd_params* p, void* stream);
+
+/* Error code (0 = none) recorded by the latest dfl_sinkhorn_fwd_noalloc call on the
+ * current device, read from the static array's header; synchronises `stream`.  The
+ * allocation-free forward reports an expired wait here, and also through
+ * dfl_pending_error() once any other call has created the pinned host word. */
+int dfl_noalloc_error(void* stream);
 
 /* ---------------------------------------------------------------------------
  * Flash-Sinkhorn IFT backward.

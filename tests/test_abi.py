@@ -211,3 +211,21 @@ def test_bench_refuses_multi_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_launch_mode_setter_round_trips(lib_path):
+    """dfl_set_launch_mode / dfl_get_launch_mode are host state only (no GPU call)."""
+    from deepfold_amd import _lib
+
+    lib = _lib.load(lib_path)
+    before = lib.dfl_get_launch_mode()
+    try:
+        for mode in (_lib.DFL_LAUNCH_COOPERATIVE, _lib.DFL_LAUNCH_ORDINARY, _lib.DFL_LAUNCH_AUTO):
+            assert lib.dfl_set_launch_mode(mode) == 0
+            assert lib.dfl_get_launch_mode() == mode
+        assert lib.dfl_set_launch_mode(3) != 0
+        assert b"launch mode" in lib.dfl_last_error()
+        assert lib.dfl_get_launch_mode() == _lib.DFL_LAUNCH_AUTO
+    finally:
+        lib.dfl_set_launch_mode(before)
+    assert lib.dfl_debug_set_spin_limit(0) == 0

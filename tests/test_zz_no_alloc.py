@@ -113,3 +113,89 @@ def test_noalloc_rejects_what_does_not_fit():
     p = _params(t2, 5, _outputs(1, 2, 64, 32), storage=_lib.DFL_STORAGE_STREAM)
     assert lib.dfl_sinkhorn_fwd_noalloc(ctypes.byref(p), stream) != 0
     assert b"resident" in lib.dfl_last_error()
+
+
+def test_noalloc_error_query_reports_expired_waits():
+    """dfl_noalloc_error reads the static array's error word: 0 after a good call, 2
+    after a call whose waits were made to expire from the host."""
+    from deepfold_amd import _lib
+
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    t = _inputs(2, 4, 256, 32, torch.float32, seed=12, lengths=[256, 200])
+    outs = _outputs(2, 4, 256, 32)
+    p = _params(t, 30, outs)
+    _lib.check(lib.dfl_sinkhorn_fwd_noalloc(ctypes.byref(p), stream), "dfl_sinkhorn_fwd_noalloc")
+    assert lib.dfl_noalloc_error(stream) == 0
+    try:
+        lib.dfl_debug_set_spin_limit(1)
+        _lib.check(lib.dfl_sinkhorn_fwd_noalloc(ctypes.byref(p), stream), "dfl_sinkhorn_fwd_noalloc")
+        torch.cuda.synchronize()
+        assert lib.dfl_noalloc_error(stream) == 2
+    finally:
+        lib.dfl_debug_set_spin_limit(0)
+        lib.dfl_pending_error()  # the pinned word (if created earlier) saw it too: clear it
+    _lib.check(lib.dfl_sinkhorn_fwd_noalloc(ctypes.byref(p), stream), "dfl_sinkhorn_fwd_noalloc")
+    assert lib.dfl_noalloc_error(stream) == 0
+
+
+def test_noalloc_graph_replays_with_new_inputs():
+    """A HIP graph that captured one allocation-free call, replayed with new input
+    values in the same buffers, gives the eager workspace entry point's outputs bit
+    for bit on every replay: each call clears the array's exchange words with a fill
+    kernel (captured with it), so a replay never accepts an earlier replay's words."""
+    from deepfold_amd import _lib
+
+    lib = _lib.load()
+    B, H, N, d = 2, 8, 768, 32
+    t = _inputs(B, H, N, d, torch.bfloat16, seed=20, lengths=[501, 759])
+    got = _outputs(B, H, N, d)
+    p = _params(t, 12, got)
+    side = torch.cuda.Stream(DEV)
+    side.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(side):  # eager warm-up on the capture stream
+        _lib.check(lib.dfl_sinkhorn_fwd_noalloc(ctypes.byref(p), ctypes.c_void_p(side.cuda_stream)), "warm-up")
+    torch.cuda.current_stream(DEV).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side, capture_error_mode="thread_local"):
+        rc = lib.dfl_sinkhorn_fwd_noalloc(ctypes.byref(p), ctypes.c_void_p(side.cuda_stream))
+    assert rc == 0, lib.dfl_last_error()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    ws = torch.zeros(lib.dfl_sinkhorn_workspace_size(B, H, N), dtype=torch.uint8, device=DEV)
+    for seed in (21, 22, 23):
+        new = _inputs(B, H, N, d, torch.bfloat16, seed=seed, lengths=[501, 759])
+        for k in t:
+            t[k].copy_(new[k])
+        for k in got:
+            got[k].fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _outputs(B, H, N, d)
+        q = _params(t, 12, want)
+        _lib.check(lib.dfl_sinkhorn_fwd(ctypes.byref(q), ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream),
+                   "dfl_sinkhorn_fwd")
+        torch.cuda.synchronize()
+        for k in OUTS:
+            assert torch.equal(want[k], got[k]), (seed, k)
+    assert lib.dfl_noalloc_error(stream) == 0
+    _lib.raise_pending("graph replay test")
+
+
+def test_workspace_entry_points_refuse_capture():
+    """The workspace forward chooses its exchange salt on the host per call, so a
+    captured call would replay a stale salt: it refuses a capturing stream."""
+    from deepfold_amd import _lib
+
+    lib = _lib.load()
+    B, H, N, d = 1, 2, 64, 32
+    t = _inputs(B, H, N, d, torch.float32, seed=24)
+    outs = _outputs(B, H, N, d)
+    p = _params(t, 5, outs)
+    ws = torch.zeros(lib.dfl_sinkhorn_workspace_size(B, H, N), dtype=torch.uint8, device=DEV)
+    side = torch.cuda.Stream(DEV)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side, capture_error_mode="thread_local"):
+        rc = lib.dfl_sinkhorn_fwd(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                  ctypes.c_void_p(side.cuda_stream))
+    assert rc != 0 and b"graph" in lib.dfl_last_error()
