@@ -104,6 +104,10 @@ def make_workload(cfg, device, dtype=None):
     return cpu, dev
 
 
+# where the forward keeps the cost (flash_sinkhorn_attn's storage=; --storage)
+STORAGE = "auto"
+
+
 def step(cfg, t, want=False):
     """One layer: forward + backward with upstream dO.  want=True also makes log mu /
     log nu leaves and returns every output and gradient (the same kernels run)."""
@@ -117,17 +121,17 @@ def step(cfg, t, want=False):
         pw, wd, x = (t[n].detach().requires_grad_(True) for n in ("pos_weight", "w_dist", "x_res"))
         o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, x, pw, t["pos_bins"], t["eps"], wd,
                                             lmu, lnu, K_iter=cfg["K_iter"], mask=t["mask"],
-                                            ift_solver="cg", ift_iters=cfg["n_cg"])
+                                            ift_solver="cg", ift_iters=cfg["n_cg"], storage=STORAGE)
     elif cfg.get("unrolled"):
         # neutral terms: no bins and no geometry weight (w_dist = None is the reference's
         # w_dist = 0 without reading x), so the kernels built without the bias terms run
         o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], None,
                                             lmu, lnu, K_iter=cfg["K_iter"], mask=t["mask"],
-                                            ift_mode="unrolled")
+                                            ift_mode="unrolled", storage=STORAGE)
     else:
         o, xc, lu, lv = flash_sinkhorn_attn(q, k, v, g, t["x_res"], t["pos_weight"], None, t["eps"], None,
                                             lmu, lnu, K_iter=cfg["K_iter"], mask=t["mask"],
-                                            ift_solver="cg", ift_iters=cfg["n_cg"])
+                                            ift_solver="cg", ift_iters=cfg["n_cg"], storage=STORAGE)
     o.backward(t["dO"])
     if not want:
         return q.grad
@@ -911,6 +915,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--storage", default="auto", choices=["auto", "register", "resident", "stream"],
+                    help="where the Sinkhorn forward keeps the cost (flash_sinkhorn_attn storage=)")
     ap.add_argument("--workload", default="cfg2",
                     choices=["cfg2", "cfg5", "cfg2-full", "cfg2-unrolled", "cfg3", "cfg4", "balanced", "tokenot-step",
                              "peaks"],
@@ -923,6 +929,8 @@ def main():
     ap.add_argument("--rocpd-summary", metavar="DB", help="print the kernel table of a rocprofv3 results "
                     "database (no GPU needed) and exit")
     args = ap.parse_args()
+    global STORAGE
+    STORAGE = args.storage
     if args.rocpd_summary:
         rocpd_summary(args.rocpd_summary)
         return

@@ -28,6 +28,11 @@ hipError_t launch_sinkhorn_fwd(const SinkFwdArgs& a, bool bf16_in, int DP, size_
 hipError_t launch_sinkhorn_fwd_stream(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                       bool coop);
 hipError_t launch_sinkhorn_pad(const PadArgs& p, bool bf16_in, int DP, hipStream_t stream);
+hipError_t launch_sinkhorn_fwd_blk(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, int L, hipStream_t stream,
+                                   bool coop);
+size_t sinkhorn_fwd_blk_lds_bytes(int N, int DP, int elem);
+bool sinkhorn_fwd_blk_fits(int B, int H, int N, int L);
+size_t sinkhorn_fwd_blk_xch_words(int B, int H, int N);
 size_t sinkhorn_bwd_lds_bytes(int N, int DP, int elem, int G, int CH, bool stream);
 hipError_t launch_sinkhorn_bwd(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                bool coop);
@@ -247,9 +252,10 @@ int cu_count() {
 
 size_t np32(int N) { return (size_t)((N + 31) / 32) * 32; }
 
-// Exchange words per (b,h): u and v for the forward, four vectors for the backward,
-// then 32 placement words per (b,h) (after all vector slots).
-size_t xch_words(int B, int H, int N) { return (size_t)B * H * (4 * np32(N) + 32); }
+// Exchange words: the register-storage forward's (its partial vectors, the largest
+// use: dfl::sinkhorn_fwd_blk_xch_words), which also covers the resident / stream
+// forward (u and v, 32 placement words per (b,h)) and the backward (four vectors).
+size_t xch_words(int B, int H, int N) { return dfl::sinkhorn_fwd_blk_xch_words(B, H, N); }
 
 int head_dim_pad(int d) { return d <= 32 ? 32 : (d <= 64 ? 64 : -1); }
 
@@ -279,6 +285,8 @@ size_t prep_operand_bytes(int B, int H, int N) { return (size_t)B * H * np32(N) 
 // coordinates (B*Np*3 floats), then the backward's per-workgroup vectors.
 constexpr int STREAM_VECS = 19;  // dfl::BWD_STREAM_VECS
 constexpr size_t LDS_LIMIT = 160 * 1024;
+// static LDS of the register-storage forward (its plan tables), beside the dynamic part
+constexpr size_t BLK_STATIC_LDS = 9 * 1024;
 size_t stream_region_bytes(int B, int H, int N, int G) {
   const size_t np = np32(N);
   size_t b = 3 * prep_operand_bytes(B, H, N);
@@ -434,7 +442,7 @@ int fwd_args(const dfl_sinkhorn_fwd_params* p, dfl::SinkFwdArgs& a) {
     return fail("output pointer is NULL");
   if (p->stride_n < p->d) return fail("stride_n must be >= d (unit inner stride)");
   if (p->pos_bins && !p->pos_weight) return fail("pos_bins given without pos_weight");
-  if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_STREAM) return fail("unknown storage %d", p->storage);
+  if (p->storage < DFL_STORAGE_AUTO || p->storage > DFL_STORAGE_REGISTER) return fail("unknown storage %d", p->storage);
   memset(&a, 0, sizeof(a));
   a.q = p->q; a.k = p->k; a.v = p->v; a.g = p->g;
   a.sb = p->stride_b; a.sh = p->stride_h; a.sn = p->stride_n;
@@ -480,9 +488,24 @@ struct FwdScratch {
 int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratch& w, void* stream) {
   const int G = group_size(a.B, a.H, a.N);
   const int elem = bf16 ? 2 : 4;
+  const int L = cu_count() / 8;
   const size_t lds_res = dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, false);
-  const bool stream_mode = storage == DFL_STORAGE_STREAM || (storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT);
-  const size_t lds = stream_mode ? dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, true) : lds_res;
+  const size_t lds_blk = dfl::sinkhorn_fwd_blk_lds_bytes(a.N, DP, elem);
+  // register storage: the UOT forward (not the balanced one) with at least one iteration,
+  // whose member grids fit the register tiles and whose output pass fits resident LDS
+  const bool blk_ok = !a.balanced && a.K_iter >= 1 && lds_blk + BLK_STATIC_LDS <= LDS_LIMIT &&
+                      dfl::sinkhorn_fwd_blk_fits(a.B, a.H, a.N, L);
+  if (storage == DFL_STORAGE_REGISTER && !blk_ok)
+    return fail("register storage does not fit B=%d, H=%d, N=%d, d=%d%s (needs %zu bytes of LDS, limit %zu)", a.B, a.H,
+                a.N, a.d, a.balanced ? " (balanced transport)" : (a.K_iter < 1 ? " with K_iter = 0" : ""), lds_blk,
+                LDS_LIMIT);
+  // AUTO takes register storage where it is the faster forward: with position bins or a
+  // geometry term, whose per-element cost it computes once instead of every sweep
+  const bool has_bias = (a.bins && a.pos_w) || (a.x && a.w_dist);
+  const bool blk_mode = blk_ok && (storage == DFL_STORAGE_REGISTER || (storage == DFL_STORAGE_AUTO && has_bias));
+  const bool stream_mode =
+      !blk_mode && (storage == DFL_STORAGE_STREAM || (storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT));
+  const size_t lds = blk_mode ? lds_blk : (stream_mode ? dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, true) : lds_res);
   if (stream_mode && !w.allow_stream)
     return fail("N=%d, d=%d needs stream storage (resident needs %zu bytes of LDS, limit %zu), which the "
                 "allocation-free forward does not provide", a.N, a.d, lds_res, LDS_LIMIT);
@@ -494,8 +517,10 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
   a.err = err_ref(ws, w.may_allocate);
   a.xch = reinterpret_cast<uint64_t*>(ws + WS_HEADER);
   a.G = G;
-  // the forward's exchange words: u and v of every (b,h), then 32 placement words per (b,h)
-  const size_t xch_end = WS_HEADER + (size_t)a.B * a.H * (2 * np32(a.N) + 32) * 8;
+  // the exchange words this launch uses: the register-storage layout, or u and v of
+  // every (b,h) then 32 placement words per (b,h)
+  const size_t xch_end = WS_HEADER + (blk_mode ? dfl::sinkhorn_fwd_blk_xch_words(a.B, a.H, a.N)
+                                               : (size_t)a.B * a.H * (2 * np32(a.N) + 32)) * 8;
   if (w.clear_always) {
     // every call starts from zeroed words, so a replay of a captured call (same salt)
     // never meets an earlier replay's words
@@ -511,9 +536,11 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
   }
   if (a.bins)
     if (int rc = prepare_bins8(a.bins, a.B, a.N, workspace, w.bins_off, &a.bins8, &a.bins8t, stream)) return rc;
-  const bool coop = coop_launch(G, a.B * a.H);
   hipError_t e;
-  if (stream_mode) {
+  if (blk_mode) {
+    e = dfl::launch_sinkhorn_fwd_blk(a, bf16, DP, lds, L, (hipStream_t)stream, coop_launch(L, 8));
+  } else if (stream_mode) {
+    const bool coop = coop_launch(G, a.B * a.H);
     const StreamPtrs sp = stream_ptrs(workspace, a.B, a.H, a.N, G);
     dfl::PadArgs pa;
     memset(&pa, 0, sizeof(pa));
@@ -527,7 +554,7 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
     a.qp = sp.qp; a.kp = sp.kp; a.vt = sp.vt; a.xs_p = sp.xs_p;
     e = dfl::launch_sinkhorn_fwd_stream(a, bf16, DP, lds, (hipStream_t)stream, coop);
   } else {
-    e = dfl::launch_sinkhorn_fwd(a, bf16, DP, lds, (hipStream_t)stream, coop);
+    e = dfl::launch_sinkhorn_fwd(a, bf16, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H));
   }
   if (e != hipSuccess) return hip_fail(e, "sinkhorn forward launch");
   return 0;
@@ -677,9 +704,9 @@ int dfl_sinkhorn_fwd_noalloc(const dfl_sinkhorn_fwd_params* p, void* stream) {
   if (int rc = fwd_args(p, a)) return rc;
   if (p->storage == DFL_STORAGE_STREAM)
     return fail("the allocation-free forward runs resident storage only (storage=DFL_STORAGE_STREAM given)");
-  // layout in the static array: header, u/v exchange words and placement words, then
-  // the uint8 bins copies
-  const size_t xch_end = WS_HEADER + (size_t)p->B * p->H * (2 * np32(p->N) + 32) * 8;
+  // layout in the static array: header, exchange words (as many as the register-storage
+  // forward uses, the most of any storage), then the uint8 bins copies
+  const size_t xch_end = WS_HEADER + dfl::sinkhorn_fwd_blk_xch_words(p->B, p->H, p->N) * 8;
   const size_t bins_off = (xch_end + 255) / 256 * 256;
   const size_t need = bins_off + (p->pos_bins ? bins8_bytes(p->B, p->N) : 0);
   if (need > NOALLOC_SCRATCH_BYTES)

@@ -147,6 +147,78 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
   }
 }
 
+// Resident-storage output pass for the row tiles [t0, t0 + nr): O_avg = T_norm V,
+// x_c = T_norm x and the per-row outputs (fwd_write_tile), from the final row LSE
+// lse2 and row maxima mx2 (local rows of the tile range) and the final potentials
+// vecU (these rows) and vecV (all columns), log2 units.  K is read from KS (all
+// rows); V^T is staged over QS; Q fragments come from global memory.  Called by
+// the whole block.
+template <typename T, int DP>
+__device__ __forceinline__ void fwd_resident_output(const SinkFwdArgs& a, int b, int h, int n, int n_tiles, int Np,
+                                                    int t0, int nr, const unsigned char* valid, T* QS, const T* KS,
+                                                    const float* vecU, const float* vecV, const float* xs,
+                                                    const float* lse2, const float* mx2, float sc, const Bias& bias,
+                                                    bool general, bool bal, bool has_v, const T* Qg, const T* Vg,
+                                                    const T* Gg) {
+  using M = Mfma<T, DP>;
+  const int N = a.N, d = a.d;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  const int g = lane >> 4;
+  constexpr int NC = DP / 16;
+  // V^T replaces Q in LDS; resident Q fragments are read from global memory.
+  T* VT = QS;  // [DP][Np]
+  __syncthreads();
+  if (has_v) stage_rows_t<T, DP>(VT, Vg, a.sn, n, d, Np);
+  __syncthreads();
+  const int n_pairs = (n_tiles + 1) / 2;
+  for (int rt = wave; rt < nr; rt += FWD_NW) {
+    const int tile = t0 + rt;
+    const int qloc = rt * 16;
+    const int irow = tile * 16 + (lane & 15);  // this lane's row in the P layout
+    typename M::Frag qf;
+    load_frag_global<T, DP>(qf, Qg, a.sn, irow, n, d, lane);
+    const float l2 = lse2[qloc + (lane & 15)];
+    f32x4 oacc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float xc0 = 0.f, xc1 = 0.f, xc2 = 0.f;
+    for (int sp = 0; sp < n_pairs; ++sp) {
+      f32x4 p[2];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int st = 2 * sp + half;
+        p[half] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (st < n_tiles) {
+          typename M::Frag af;
+          M::load(af, KS + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+          const f32x4 w = *reinterpret_cast<const f32x4*>(vecV + st * 16 + 4 * g);
+          const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+          const f32x4 acc = M::qk(af, qf, zero);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            const int j = st * 16 + 4 * g + kk;
+            float x = __builtin_fmaf(acc[kk], sc, w[kk]);
+            if (general && w[kk] > 0.5f * NEG_BIG) x += bias(irow, j);
+            const float pv = fast_exp2(x - l2);
+            p[half][kk] = pv;
+            xc0 = __builtin_fmaf(pv, xs[3 * j], xc0);
+            xc1 = __builtin_fmaf(pv, xs[3 * j + 1], xc1);
+            xc2 = __builtin_fmaf(pv, xs[3 * j + 2], xc2);
+          }
+        }
+      }
+      if (has_v) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          oacc[c] = M::pv_split(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
+      }
+    }
+    fwd_write_tile<T, DP>(a, b, h, tile, n, valid, lse2 + qloc, mx2 + qloc, vecU, vecV, oacc, xc0, xc1, xc2, Gg,
+                          lane, bal);
+  }
+}
+
 // MODE (compile time, so the plain UOT instantiation carries none of the other
 // modes' code): FWD_UOT, FWD_UOT_HIST (also records the potentials history for the
 // unrolled backward) or FWD_BALANCED (balanced transport, history recorded).  The
@@ -418,57 +490,8 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const int g = lane >> 4;
   constexpr int NC = DP / 16;
   if constexpr (!STREAM) {
-    // V^T replaces Q in LDS; resident Q fragments are read from global memory.
-    T* VT = QS;  // [DP][Np]
-    __syncthreads();
-    if (has_v) stage_rows_t<T, DP>(VT, Vg, a.sn, n, d, Np);
-    __syncthreads();
-    const int n_pairs = (n_tiles + 1) / 2;
-    for (int rt = wave; rt < nr; rt += FWD_NW) {
-      const int tile = t0 + rt;
-      const int qloc = rt * 16;
-      const int irow = tile * 16 + (lane & 15);  // this lane's row in the P layout
-      typename M::Frag qf;
-      load_frag_global<T, DP>(qf, Qg, a.sn, irow, n, d, lane);
-      const float l2 = lse2[qloc + (lane & 15)];
-      f32x4 oacc[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-      float xc0 = 0.f, xc1 = 0.f, xc2 = 0.f;
-      for (int sp = 0; sp < n_pairs; ++sp) {
-        f32x4 p[2];
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int st = 2 * sp + half;
-          p[half] = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (st < n_tiles) {
-            typename M::Frag af;
-            M::load(af, KS + (size_t)(st * 16 + (lane & 15)) * DP, lane);
-            const f32x4 w = *reinterpret_cast<const f32x4*>(vecV + st * 16 + 4 * g);
-            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 acc = M::qk(af, qf, zero);
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-              const int j = st * 16 + 4 * g + kk;
-              float x = __builtin_fmaf(acc[kk], sc, w[kk]);
-              if (general && w[kk] > 0.5f * NEG_BIG) x += bias(irow, j);
-              const float pv = fast_exp2(x - l2);
-              p[half][kk] = pv;
-              xc0 = __builtin_fmaf(pv, xs[3 * j], xc0);
-              xc1 = __builtin_fmaf(pv, xs[3 * j + 1], xc1);
-              xc2 = __builtin_fmaf(pv, xs[3 * j + 2], xc2);
-            }
-          }
-        }
-        if (has_v) {
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-            oacc[c] = M::pv_split(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
-        }
-      }
-      fwd_write_tile<T, DP>(a, b, h, tile, n, valid, lse2 + qloc, mx2 + qloc, vecU, vecV, oacc, xc0, xc1, xc2, Gg,
-                            lane, bal);
-    }
+    fwd_resident_output<T, DP>(a, b, h, n, n_tiles, Np, t0, nr, valid, QS, KS, vecU, vecV, xs, lse2, mx2, sc, bias,
+                               general, bal, has_v, Qg, Vg, Gg);
   } else {
     // Stream mode: K and V^T pass through LDS in chunks of FWD_OCH streamed rows
     // (the K stripe region is free now); resident Q fragments come from the Q stripe.

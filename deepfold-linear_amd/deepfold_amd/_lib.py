@@ -25,6 +25,7 @@ DFL_IFT_ANALYTIC = 1
 DFL_STORAGE_AUTO = 0
 DFL_STORAGE_RESIDENT = 1
 DFL_STORAGE_STREAM = 2
+DFL_STORAGE_REGISTER = 3
 DFL_LAUNCH_AUTO = 0
 DFL_LAUNCH_ORDINARY = 1
 DFL_LAUNCH_COOPERATIVE = 2

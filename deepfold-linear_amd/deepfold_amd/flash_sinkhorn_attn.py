@@ -20,10 +20,15 @@ Keyword-only extensions (defaults reproduce the reference):
   computes it; the forward then also records the potentials of every
   half-iteration (2*K*B*H*N floats) and ``ift_solver`` / ``ift_iters`` are unused.
 * ``cg_rtol``: CG stops early once ||r|| <= cg_rtol ||b|| (0: run all steps).
-* ``storage``: ``"auto"`` (default), ``"resident"`` or ``"stream"``: where the
-  kernels keep Q, K and the length-N vectors.  Resident keeps a whole (b,h) in
-  LDS; stream keeps one stripe per workgroup and streams the rest through L2
-  (long sequences such as N = 4096, d = 64).  Auto picks resident when it fits.
+* ``storage``: ``"auto"`` (default), ``"register"``, ``"resident"`` or ``"stream"``:
+  where the forward keeps the cost.  Register computes each workgroup's block of
+  logits once and keeps it in registers for all iterations (the UOT forward up to
+  N = 768 at B*H = 16); resident keeps Q, K and the length-N vectors of a whole
+  (b,h) in LDS and recomputes the cost every sweep; stream keeps one stripe per
+  workgroup and streams the rest through L2 (long sequences such as N = 4096,
+  d = 64).  Auto picks register when the cost has bins or a geometry term, else
+  resident, else stream.  The backward takes
+  resident or stream (``"register"`` means its automatic choice).
 
 Padding: tokens with mask == 0 are excluded from the transport plan in both
 passes; outputs at padded positions are zero (the reference's x_centroid rows
@@ -40,7 +45,10 @@ from . import _lib
 
 _SOLVERS = {"fixed_point": _lib.DFL_IFT_FIXED_POINT, "cg": _lib.DFL_IFT_CG}
 _MODES = {"reference": _lib.DFL_IFT_REFERENCE, "analytic": _lib.DFL_IFT_ANALYTIC}
-_STORAGE = {"auto": _lib.DFL_STORAGE_AUTO, "resident": _lib.DFL_STORAGE_RESIDENT, "stream": _lib.DFL_STORAGE_STREAM}
+_STORAGE = {"auto": _lib.DFL_STORAGE_AUTO, "resident": _lib.DFL_STORAGE_RESIDENT, "stream": _lib.DFL_STORAGE_STREAM,
+            "register": _lib.DFL_STORAGE_REGISTER}
+# the backward has no register storage: there "register" means its automatic choice
+_BWD_STORAGE = dict(_STORAGE, register=_lib.DFL_STORAGE_AUTO)
 
 
 def _qkvg(Q, K, V, G):
@@ -180,7 +188,7 @@ class FlashSinkhornAttn(torch.autograd.Function):
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
             dlmu.data_ptr(), dlnu.data_ptr(),
             _lib.ptr(dx) if need_dx else None, _lib.ptr(dpw) if need_dpw else None,
-            _lib.ptr(dw) if need_dw else None, _STORAGE[storage])
+            _lib.ptr(dw) if need_dw else None, _BWD_STORAGE[storage])
         rc = _lib.timed_launch("sinkhorn_bwd", dev, lambda: lib.dfl_sinkhorn_bwd(
             ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(_lib.stream_handle(dev))))
         _lib.check(rc, "dfl_sinkhorn_bwd")

@@ -95,16 +95,24 @@ int dfl_debug_set_spin_limit(unsigned limit);
  * Outputs o_flat (B,N,H*d), x_centroid (B,H,N,3), log_u, log_v (B,H,N); saved for the
  * backward: o_avg (B,H,N,d), log_z (B,H,N) = LSE_j(u_i + L_ij + v_j) and
  * col_lse (B,H,N) = LSE_i(L_ij + u_i) of the last column update.
- * storage selects where the kernels keep Q, K and the length-N vectors:
- * DFL_STORAGE_AUTO (0) picks RESIDENT when it fits in LDS, else STREAM;
- * RESIDENT keeps all of them in LDS (fails with an argument error if they do not
- * fit); STREAM keeps only each workgroup's stripe in LDS and streams the rest
- * through L2 (long sequences, e.g. N = 4096, d = 64).  Results agree to rounding.
+ * storage selects where the kernels keep the cost:
+ * DFL_STORAGE_REGISTER (3) computes each workgroup's block of logits once and keeps
+ * it in registers for all iterations (each (b,h) split into a grid of plan blocks);
+ * it serves the UOT forward with K_iter >= 1 while the blocks fit the register tiles
+ * (at B*H = 16 up to N = 768; the balanced transport, K_iter = 0 and larger problems
+ * are refused with an argument error);
+ * RESIDENT keeps Q, K and the length-N vectors in LDS and recomputes the cost tile
+ * on MFMA every sweep (fails with an argument error if they do not fit);
+ * STREAM keeps only each workgroup's stripe in LDS and streams the rest through L2
+ * (long sequences, e.g. N = 4096, d = 64);
+ * DFL_STORAGE_AUTO (0) picks REGISTER where it serves and the cost carries position
+ * bins or a geometry term, else RESIDENT where it fits, else STREAM.  Results agree
+ * to rounding.
  * hist (K_iter,2,B,H,N) may be NULL; if given, the forward also writes v after the
  * column update and u after the row update of every iteration (natural log), which
  * dfl_sinkhorn_unrolled_bwd needs.
  */
-enum dfl_storage { DFL_STORAGE_AUTO = 0, DFL_STORAGE_RESIDENT = 1, DFL_STORAGE_STREAM = 2 };
+enum dfl_storage { DFL_STORAGE_AUTO = 0, DFL_STORAGE_RESIDENT = 1, DFL_STORAGE_STREAM = 2, DFL_STORAGE_REGISTER = 3 };
 
 typedef struct dfl_sinkhorn_fwd_params {
   int dtype;
@@ -145,9 +153,9 @@ int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t w
  * reference: it is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * params, outputs and kernels as dfl_sinkhorn_fwd, resident storage only (AUTO or
- * RESIDENT; a problem that needs stream storage is rejected).  Instead of a
- * workspace it uses a static device array of DFL_NOALLOC_SCRATCH_BYTES per GPU,
- * held until the process ends: it needs 256 + 16*B*H*(Np + 16) bytes (+ 2*B*Np*Np
+ * RESIDENT or REGISTER; a problem that needs stream storage is rejected).  Instead
+ * of a workspace it uses a static device array of DFL_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends: it needs 256 + 8*B*H*(17*Np + 64) bytes (+ 2*B*Np*Np
  * with pos_bins), Np = N rounded up to 32, and rejects larger problems.  Every call on
  * one GPU shares that array, so calls that overlap in time on one GPU race.  It
  * calls no hipMalloc / hipFree and no allocating library routine.  Every call first

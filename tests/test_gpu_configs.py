@@ -270,3 +270,31 @@ def test_config3_atom_to_token():
     ref_inp = dict(Q=Q.double(), K=K.double(), V=V.double(), starts=starts, counts=counts, token_mask=None)
     o_ref, g_ref = aref.grads(aref.atom_to_token, ref_inp, go.double(), wrt)
     _attn_check("config3-a2t", out, g, o_ref, g_ref, wrt)
+
+
+# ---------------------------------------------------------------------------
+# register storage (logits held in registers, 2-D member blocks) at the headline
+# layout and in fp32, neutral cost (AUTO routes only biased costs there)
+@pytest.mark.parametrize("solver", ["cg", "fixed_point"])
+def test_headline_config1_register_storage(solver):
+    cfg, cpu, t = _headline()
+    iters = cfg["n_cg"] if solver == "cg" else cfg["K_iter"]
+    got, ggot = run_layer(t, cfg["K_iter"], ift_solver=solver, ift_iters=iters, storage="register")
+    fo, gr = ref.backward_masked(oracle_fwd_inputs(cpu, cfg["K_iter"]), cpu["dO"].numpy(), None,
+                                 solver=solver, n_cg=cfg["n_cg"], K_back=cfg["K_iter"])
+    check_layer(got, ggot, fo, gr, 2e-2, f"config1-register-{solver}", cpu["lengths"])
+
+
+@pytest.mark.parametrize("dtype,tol,N,lengths", [
+    (torch.float32, 1e-4, 192, [192, 161]),
+    (torch.bfloat16, 2e-2, 512, [497, 330]),
+    (torch.float32, 1e-4, 448, [448, 400]),
+])
+def test_register_storage_multi_head(dtype, tol, N, lengths):
+    B, H, d, K = 2, 8, 32, 12
+    eps = [0.5, 1.0, 0.25, 2.0] * 2
+    cpu = _ragged_case(B, H, N, d, lengths, seed=91 + N, dtype=dtype, eps=eps)
+    t = {k: v.to(DEV) for k, v in cpu.items()}
+    got, ggot = run_layer(t, K, ift_solver="cg", ift_iters=16, storage="register")
+    fo, gr = ref.backward_masked(oracle_fwd_inputs(cpu, K), cpu["dO"].numpy(), None, solver="cg", n_cg=16, K_back=K)
+    check_layer(got, ggot, fo, gr, tol, f"register-{dtype}-{N}", lengths)
