@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "deepfold_amd", "libdfl_amd.so")
 OBJ_DIR = os.path.join(HERE, "_build")
-SOURCES = ["capi.hip", "sinkhorn_fwd.hip", "sinkhorn_fwd_stream.hip", "sinkhorn_fwd_blk.hip", "sinkhorn_bwd.hip",
+SOURCES = ["capi.hip", "sinkhorn_fwd.hip", "sinkhorn_fwd_stream.hip", "sinkhorn_fwd_reg.hip", "sinkhorn_fwd_blk.hip", "sinkhorn_bwd.hip",
            "sinkhorn_bwd_stream.hip", "attention.hip", "dense.hip", "balanced_bwd.hip",
            "unrolled_bwd.hip", "trunk_steps.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

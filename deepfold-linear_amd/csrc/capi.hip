@@ -28,6 +28,10 @@ hipError_t launch_sinkhorn_fwd(const SinkFwdArgs& a, bool bf16_in, int DP, size_
 hipError_t launch_sinkhorn_fwd_stream(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                       bool coop);
 hipError_t launch_sinkhorn_pad(const PadArgs& p, bool bf16_in, int DP, hipStream_t stream);
+hipError_t launch_sinkhorn_fwd_reg(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
+                                   bool coop);
+bool sinkhorn_fwd_reg_fits(int N, int G);
+size_t sinkhorn_fwd_reg_lds_bytes(int N, int DP, int elem, int G);
 hipError_t launch_sinkhorn_fwd_blk(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, int L, hipStream_t stream,
                                    bool coop);
 size_t sinkhorn_fwd_blk_lds_bytes(int N, int DP, int elem);
@@ -502,10 +506,19 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
   // AUTO takes register storage where it is the faster forward: with position bins or a
   // geometry term, whose per-element cost it computes once instead of every sweep
   const bool has_bias = (a.bins && a.pos_w) || (a.x && a.w_dist);
-  const bool blk_mode = blk_ok && (storage == DFL_STORAGE_REGISTER || (storage == DFL_STORAGE_AUTO && has_bias));
+  const size_t lds_reg = dfl::sinkhorn_fwd_reg_lds_bytes(a.N, DP, elem, G);
+  const bool reg_ok = !a.balanced && !a.hist && a.K_iter >= 1 && dfl::sinkhorn_fwd_reg_fits(a.N, G) &&
+                      lds_reg <= LDS_LIMIT;
+  const bool blk_mode =
+      blk_ok && (storage == DFL_STORAGE_REGISTER || (storage == DFL_STORAGE_AUTO && has_bias && !reg_ok));
   const bool stream_mode =
       !blk_mode && (storage == DFL_STORAGE_STREAM || (storage == DFL_STORAGE_AUTO && lds_res > LDS_LIMIT));
-  const size_t lds = blk_mode ? lds_blk : (stream_mode ? dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, true) : lds_res);
+  // resident layout with the logits in registers: the UOT forward without history whose
+  // stripes and slots fit the register tiles
+  const bool reg_mode = !blk_mode && !stream_mode && storage == DFL_STORAGE_AUTO && reg_ok;
+  const size_t lds = blk_mode ? lds_blk
+                              : (stream_mode ? dfl::sinkhorn_fwd_lds_bytes(a.N, DP, elem, G, true)
+                                             : (reg_mode ? lds_reg : lds_res));
   if (stream_mode && !w.allow_stream)
     return fail("N=%d, d=%d needs stream storage (resident needs %zu bytes of LDS, limit %zu), which the "
                 "allocation-free forward does not provide", a.N, a.d, lds_res, LDS_LIMIT);
@@ -553,6 +566,8 @@ int run_fwd(dfl::SinkFwdArgs& a, bool bf16, int DP, int storage, const FwdScratc
     if (e != hipSuccess) return hip_fail(e, "sinkhorn pad launch");
     a.qp = sp.qp; a.kp = sp.kp; a.vt = sp.vt; a.xs_p = sp.xs_p;
     e = dfl::launch_sinkhorn_fwd_stream(a, bf16, DP, lds, (hipStream_t)stream, coop);
+  } else if (reg_mode) {
+    e = dfl::launch_sinkhorn_fwd_reg(a, bf16, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H));
   } else {
     e = dfl::launch_sinkhorn_fwd(a, bf16, DP, lds, (hipStream_t)stream, coop_launch(G, a.B * a.H));
   }

@@ -178,26 +178,24 @@ __device__ __forceinline__ int mask_setup(const float* mask, int N, unsigned cha
   return n;
 }
 
-// Polls this thread's words i = base + t + k * stride, k < W, of [0, n) until each
+// Polls this thread's words buf[idx[k]], k < W (idx[k] < 0: none) until each
 // carries `tag`, calling take(k, word) once per word.  Every word has two loads in
 // flight, issued one sleep unit apart and checked alternately, so a load that still
 // saw the old word costs that stagger rather than a whole round trip (an exchange
 // round of a 16-member group measured 1826 instead of 2285 clocks on MI355X).
-// The loads are unconditional (words past n read word 0 and are ignored), so
+// The loads are unconditional (absent words read word 0 and are ignored), so
 // the compiler can wait for one set with the other still in flight.  Returns
-// false if the error flag is raised or the wait expires (then it raises it).
+// false if the wait expires (then it raises the error).
 template <int W, typename Take>
-__device__ __forceinline__ bool poll_batch(const uint64_t* buf, int base, int n, int stride, uint32_t tag, ErrRef err,
+__device__ __forceinline__ bool poll_words(const uint64_t* buf, const int (&idx)[W], uint32_t tag, ErrRef err,
                                            Take take) {
   const uint32_t salt = tag >> 12;
-  const int t = threadIdx.x;
   const uint64_t* addr[W];
   bool done[W];
 #pragma unroll
   for (int k = 0; k < W; ++k) {
-    const int i = base + t + k * stride;
-    done[k] = i >= n;
-    addr[k] = buf + (done[k] ? 0 : i);
+    done[k] = idx[k] < 0;
+    addr[k] = buf + (done[k] ? 0 : idx[k]);
   }
   auto all = [&]() {
     bool r = true;
@@ -236,6 +234,18 @@ __device__ __forceinline__ bool poll_batch(const uint64_t* buf, int base, int n,
     // waits expire too, within the spin limit (well under a second).
     if (++spins > err.spin_limit / 2) { raise_error(err, salt, 2u); return false; }
   }
+}
+// poll_words for the words i = base + t + k * stride of [0, n).
+template <int W, typename Take>
+__device__ __forceinline__ bool poll_batch(const uint64_t* buf, int base, int n, int stride, uint32_t tag, ErrRef err,
+                                           Take take) {
+  int idx[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int i = base + (int)threadIdx.x + k * stride;
+    idx[k] = i < n ? i : -1;
+  }
+  return poll_words<W>(buf, idx, tag, err, take);
 }
 
 // All words [0, n) of a vector, NT threads, batches of W = 1, 2 or 4 words a
@@ -583,6 +593,324 @@ __device__ __forceinline__ void lean_sweep(const T* res, const T* str, const flo
   else
     lean_chunks<NT, T, DP, SMAX, GENERAL, TRANS>(res, str, w2, (ks + SMAX - 1) / SMAX, t0, nr, sc, bias, lse,
                                                  scratch, s_reset, publish);
+}
+
+// ---------------------------------------------------------------------------
+// Potentials added to logits held in registers (register storage): a rank-2 bf16
+// MFMA whose operands carry three-part splits of the potentials.
+// Three-part bf16 split of x in the first three slots (hi + mid + lo = x to fp32
+// rounding); slot 3 is zero.
+__device__ __forceinline__ bf16x4 split3(float x) {
+  const bf16 h = (bf16)x;
+  const float r1 = x - (float)h;
+  const bf16 m = (bf16)r1;
+  const bf16 l = (bf16)(r1 - (float)m);
+  return bf16x4{h, m, l, (bf16)0.f};
+}
+
+// D = S + A B^T on v_mfma_f32_16x16x16_bf16: lane l supplies A[m = l%16][k = 4(l/16)..+3]
+// and B[n = l%16][same k], and holds D[4(l/16) + e][l%16] (the layout of S).
+__device__ __forceinline__ f32x4 mfma_rank(bf16x4 a, bf16x4 b, f32x4 s) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), s,
+                                                   0, 0, 0);
+}
+
+// Operands of the rank-2 update.  The column side (A, m = plan column j) carries the
+// column term's parts in lane group 0 and ones in group 1; the row side (B, n = plan
+// row i) carries ones in group 0 and the row term's parts in group 1; groups 2-3 are
+// zero.  So sum_k A[j][k] B[i][k] = colterm_j + rowterm_i.
+__device__ __forceinline__ bf16x4 blk_col_operand(const bf16x4* parts, int tile, int lane) {
+  const int g = lane >> 4;
+  const bf16x4 one = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)0.f};
+  const bf16x4 zero = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+  const bf16x4 p = parts[tile * 16 + (lane & 15)];
+  return g == 0 ? p : (g == 1 ? one : zero);
+}
+__device__ __forceinline__ bf16x4 blk_row_operand(const bf16x4* parts, int tile, int lane) {
+  const int g = lane >> 4;
+  const bf16x4 one = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)0.f};
+  const bf16x4 zero = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+  const bf16x4 p = parts[tile * 16 + (lane & 15)];
+  return g == 1 ? p : (g == 0 ? one : zero);
+}
+
+// ---------------------------------------------------------------------------
+// Dataflow half-iterations of resident storage.  A wave of a lean sweep reads the
+// potentials of its own streamed tiles st = wave + NW k only, so it needs no other
+// wave's gather: it polls those words itself (wave_gather) and starts its sweep as
+// soon as they carry the previous half-iteration's tag.  The fixed / online choice
+// is the wave's own (the largest change over its tiles), and each wave leaves an
+// absolute log2 partial per resident row; the partials of the NW waves are combined
+// after the chunk's barrier (flow_chunk), the only barrier of a half-iteration
+// with at most 4 resident tiles (2 with a bias).
+
+// Polls the words of this wave's streamed tiles (entries i < n) until they carry
+// `tag`, writes dst[i] = word * log2 e (NEG_BIG for a masked entry), and its split
+// parts[i] = split3(dst[i]) if parts is given, and sets dmax, in every lane, to the
+// largest |change| over the wave's valid entries (+inf for a NaN).  Returns false,
+// uniformly over the wave, if a wait expired (then the error has been raised).
+template <int NW>
+__device__ __forceinline__ bool wave_gather(const uint64_t* buf, int n, int n_tiles, uint32_t tag, float* dst,
+                                            const unsigned char* valid, ErrRef err, float& dmax,
+                                            bf16x4* parts = nullptr) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int nwords = wave < n_tiles ? ((n_tiles - 1 - wave) / NW + 1) * 16 : 0;
+  float dm = 0.f;
+  bool ok = true;
+  for (int base = 0; base < nwords && ok; base += 2 * WAVE) {
+    int idx[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = base + k * WAVE + lane;
+      const int i = (wave + NW * (e >> 4)) * 16 + (e & 15);
+      idx[k] = (e < nwords && i < n) ? i : -1;
+    }
+    ok = poll_words<2>(buf, idx, tag, err, [&](int k, uint64_t w) {
+      const int i = idx[k];
+      float nv = NEG_BIG;
+      if (valid[i]) {
+        nv = __uint_as_float((uint32_t)(w >> 32)) * LOG2E;
+        dm = fmaxf(dm, fabsf(nv - dst[i]));
+      }
+      dst[i] = nv;
+      if (parts) parts[i] = split3(nv);
+    });
+    ok = wave_max_u32(ok ? 0u : 1u) == 0u;
+  }
+  dmax = __uint_as_float(wave_max_u32(dm == dm ? __float_as_uint(dm) : 0x7f800000u));
+  return ok;
+}
+
+// Combine of the NW wave partials part[q * NW + w] of the nr * 16 rows q (threads
+// q < 16 nr): lse[q] = m + log2 sum_w exp2(p_w - m), m = max_w p_w, in wave order,
+// then publish(q, lse[q]).  A row's partials are adjacent: 16-byte reads.
+template <int NW, typename Pub>
+__device__ __forceinline__ void flow_combine(const float* part, int nr, float* lse, Pub publish) {
+  static_assert(NW % 4 == 0, "partials are read 4 at a time");
+  if ((int)threadIdx.x < nr * 16) {
+    const int q = threadIdx.x;
+    float p[NW];
+#pragma unroll
+    for (int w4 = 0; w4 < NW; w4 += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(part + q * NW + w4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) p[w4 + k] = v[k];
+    }
+    float m = p[0];
+#pragma unroll
+    for (int w_ = 1; w_ < NW; ++w_) m = fmaxf(m, p[w_]);
+    float ss = 0.f;
+#pragma unroll
+    for (int w_ = 0; w_ < NW; ++w_) ss += fast_exp2(p[w_] - m);
+    const float v = m + fast_log2(ss);
+    lse[q] = v;
+    publish(q, v);
+  }
+}
+
+// One chunk of NR resident tiles (absolute rt0.., local rows q0..) in dataflow form.
+// Each wave takes the shift of its partial from lse[q] (fixed: every term of its
+// tiles is then <= 2^delta, delta the wave's largest potential change) or, online,
+// from a first pass over its tiles (the row maximum of its streamed entries), and
+// writes p_w = shift + log2 sum_(its j) exp2(x_qj - shift) (NEG_BIG for an empty
+// sum) to part (flow_combine's layout).  After the barrier the threads of the chunk's rows combine the NW
+// partials in wave order, lse = m + log2 sum_w exp2(p_w - m) with m = max_w p_w,
+// store it and publish it.  part must not be written again before every wave has
+// passed one more barrier (flow_sweep alternates two slots).
+template <int NT, typename T, int DP, int NR, int SCH, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void flow_chunk(bool online, const T* __restrict__ res, const T* __restrict__ str,
+                                           const float* __restrict__ w2, int groups, int rt0, int q0, float sc,
+                                           const Bias& bias, float* lse, float* part, Pub publish) {
+  using M = Mfma<T, DP>;
+  using Frag = typename M::Frag;
+  constexpr int NW = NT / WAVE;
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int g = lane >> 4;
+  const float isc = 1.f / sc;
+  Frag bf[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) M::load(bf[r], res + (size_t)((rt0 + r) * 16 + (lane & 15)) * DP, lane);
+  const T* sb = str + (size_t)(wave * 16 + (lane & 15)) * DP;
+  const float* wb = w2 + wave * 16 + 4 * g;
+  // x_qj - shift_q for the wave's streamed entries (MFMA C operand -shift / sc), in
+  // groups of SCH tiles, handed to f(r, e[4 SCH]) per resident tile r
+  auto pass = [&](const f32x4(&ci)[NR], auto&& f) __attribute__((always_inline)) {
+    for (int kg = 0; kg < groups; ++kg) {
+      Frag af[SCH];
+      f32x4 w[SCH];
+#pragma unroll
+      for (int k = 0; k < SCH; ++k) {
+        M::load(af[k], sb + (size_t)(kg * SCH + k) * NW * 16 * DP, lane);
+        w[k] = *reinterpret_cast<const f32x4*>(wb + (kg * SCH + k) * NW * 16);
+      }
+      f32x4 x[NR][SCH];
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int k = 0; k < SCH; ++k) x[r][k] = M::qk(af[k], bf[r], ci[r]);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        f32x4 bv[SCH];
+        if (GENERAL) {
+          int s0[SCH];
+#pragma unroll
+          for (int k = 0; k < SCH; ++k) s0[k] = min((wave + NW * (kg * SCH + k)) * 16 + 4 * g, bias.Np - 4);
+          bias.template quads<TRANS>((rt0 + r) * 16 + (lane & 15), s0, bv);
+        }
+        float e[4 * SCH];
+#pragma unroll
+        for (int k = 0; k < SCH; ++k)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float xv = __builtin_fmaf(x[r][k][q], sc, w[k][q]);
+            e[4 * k + q] = GENERAL ? xv + bv[k][q] : xv;
+          }
+        f(r, e);
+      }
+    }
+  };
+  float sh[NR];
+  if (online) {
+    f32x4 zero[NR];
+    float m[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      zero[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m[r] = NEG_BIG;
+    }
+    pass(zero, [&](int r, float(&e)[4 * SCH]) {
+#pragma unroll
+      for (int w_ = 1; w_ < 4 * SCH; w_ *= 2)
+#pragma unroll
+        for (int i = 0; i + w_ < 4 * SCH; i += 2 * w_) e[i] = fmaxf(e[i], e[i + w_]);
+      m[r] = fmaxf(m[r], e[0]);
+    });
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const float mr = max_groups(m[r]);
+      sh[r] = mr > 0.5f * NEG_BIG ? mr : 0.f;  // no live entry: the sum is 0 whatever the shift
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) sh[r] = lse[q0 + r * 16 + (lane & 15)];
+  }
+  f32x4 ci[NR];
+  float s[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float c = -sh[r] * isc;
+    ci[r] = f32x4{c, c, c, c};
+    s[r] = 0.f;
+  }
+  pass(ci, [&](int r, float(&e)[4 * SCH]) {
+#pragma unroll
+    for (int i = 0; i < 4 * SCH; ++i) e[i] = fast_exp2(e[i]);
+    s[r] += tree_sum(e);
+  });
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float ss = sum_groups(s[r]);
+    if (lane < 16) part[(r * 16 + lane) * NW + wave] = ss > 0.f ? sh[r] + fast_log2(ss) : NEG_BIG;
+  }
+  lds_barrier();
+  flow_combine<NW>(part, NR, lse + q0, [&](int q, float v) { publish(q0 + q, v); });
+}
+
+// Dataflow sweep of resident tiles [t0, t0 + nr) against n_str_tiles streamed tiles
+// (the lean sweep's layout and padding): chunks of at most SK_RT resident tiles (2
+// with a bias), partial slots alternating with the caller's chunk counter, which
+// every wave advances alike.  lse holds the fixed shifts on entry (unused online)
+// and the combined LSEs on exit (written by the combining threads only: visible to
+// the other waves after their next barrier).
+template <int NT, typename T, int DP, bool GENERAL, bool TRANS, typename Pub>
+__device__ __forceinline__ void flow_sweep(bool online, const T* res, const T* str, const float* w2, int n_str_tiles,
+                                           int t0, int nr, float sc, const Bias& bias, float* lse, float* scratch,
+                                           int& chunk, Pub publish) {
+  constexpr int NW = NT / WAVE;
+  constexpr int SMAX = lean_sch<T, DP>();
+  constexpr int CMAX = GENERAL ? 2 : SK_RT;
+  const int ks = (n_str_tiles + NW - 1) / NW;
+  const bool small = SMAX == 6 && ks <= 4;
+  const int groups = small ? 1 : (ks + SMAX - 1) / SMAX;
+  for (int c0 = 0; c0 < nr; c0 += CMAX, ++chunk) {
+    float* part = scratch + (chunk & 1) * (NW * SK_RT * 16);
+    const int nc = min(CMAX, nr - c0);
+    const int rt0 = t0 + c0, q0 = c0 * 16;
+#define DFL_FLOW(NRV, SCHV)                                                                                      \
+  flow_chunk<NT, T, DP, NRV, SCHV, GENERAL, TRANS>(online, res, str, w2, groups, rt0, q0, sc, bias, lse, part, \
+                                                   publish)
+    if (small) {
+      if (CMAX == 4 && nc == 4) DFL_FLOW(CMAX, 4);
+      else if (CMAX == 4 && nc == 3) DFL_FLOW(CMAX - 1, 4);
+      else if (nc == 2) DFL_FLOW(2, 4);
+      else DFL_FLOW(1, 4);
+    } else {
+      if (CMAX == 4 && nc == 4) DFL_FLOW(CMAX, SMAX);
+      else if (CMAX == 4 && nc == 3) DFL_FLOW(CMAX - 1, SMAX);
+      else if (nc == 2) DFL_FLOW(2, SMAX);
+      else DFL_FLOW(1, SMAX);
+    }
+#undef DFL_FLOW
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Register storage of the resident layout.  A wave keeps the logits of its (resident
+// tile r, streamed slot k) pairs in VGPRs, S[r KS + k] for r < nr, k < KS (streamed
+// tile st = wave + NW k; slots of tiles the wave does not have hold NEG_BIG), computed
+// once per launch.  A sweep adds the potentials with one rank-2 MFMA per pair
+// (streamed term in the A operand, -shift of the resident row in B) and sums exp2;
+// each row's partial p_w goes to part as in flow_chunk.  Online (the first sweep, or
+// a wave whose streamed potentials moved by more than the fixed-shift bound) takes
+// the row maxima of its pairs first and uses them as its shifts.
+//   colp : split parts of the streamed potentials (by absolute streamed index)
+//   rowp : split parts of -shift of the resident rows (local), for the fixed mode
+//   shift: the fixed shifts (local rows)
+template <int KS, int NRM, int NW>
+__device__ __forceinline__ void reg_sweep(bool online, const f32x4 (&S)[NRM * KS], int nr, const bf16x4* colp,
+                                          const bf16x4* rowp, const float* shift, float* part) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int g = lane >> 4;
+  const bf16x4 one = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)0.f};
+  const bf16x4 zero = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+  bf16x4 A[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) A[k] = blk_col_operand(colp, wave + NW * k, lane);
+#pragma unroll
+  for (int r = 0; r < NRM; ++r) {
+    if (r < nr) {
+      float sh;
+      bf16x4 Bv;
+      if (online) {
+        const bf16x4 b0 = g == 0 ? one : zero;  // row term 0
+        float m = NEG_BIG;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+          const f32x4 x = mfma_rank(A[k], b0, S[r * KS + k]);
+          m = fmaxf(m, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+        }
+        m = max_groups(m);
+        sh = m > 0.5f * NEG_BIG ? m : 0.f;  // no live entry: the sum is 0 whatever the shift
+        Bv = g == 1 ? split3(-sh) : b0;
+      } else {
+        sh = shift[r * 16 + (lane & 15)];
+        Bv = blk_row_operand(rowp, r, lane);
+      }
+      float e[4 * KS];
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const f32x4 x = mfma_rank(A[k], Bv, S[r * KS + k]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) e[4 * k + q] = fast_exp2(x[q]);
+      }
+      const float ss = sum_groups(tree_sum(e));
+      if (lane < 16) part[(r * 16 + lane) * NW + wave] = ss > 0.f ? sh + fast_log2(ss) : NEG_BIG;
+    }
+  }
 }
 
 // Exchange-placement agreement of a group.  At the start of a launch every member

@@ -55,43 +55,6 @@ inline size_t blk_lds_bytes(int N, int DP, int elem) {
   return blk_persist_lds(Np) + (qk > it ? qk : it);
 }
 
-// Three-part bf16 split of x in the first three slots (hi + mid + lo = x to fp32
-// rounding); slot 3 is zero.
-__device__ __forceinline__ bf16x4 split3(float x) {
-  const bf16 h = (bf16)x;
-  const float r1 = x - (float)h;
-  const bf16 m = (bf16)r1;
-  const bf16 l = (bf16)(r1 - (float)m);
-  return bf16x4{h, m, l, (bf16)0.f};
-}
-
-// D = S + A B^T on v_mfma_f32_16x16x16_bf16: lane l supplies A[m = l%16][k = 4(l/16)..+3]
-// and B[n = l%16][same k], and holds D[4(l/16) + e][l%16] (the layout of S).
-__device__ __forceinline__ f32x4 mfma_rank(bf16x4 a, bf16x4 b, f32x4 s) {
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), s,
-                                                   0, 0, 0);
-}
-
-// Operands of the rank-2 update.  The column side (A, m = plan column j) carries the
-// column term's parts in lane group 0 and ones in group 1; the row side (B, n = plan
-// row i) carries ones in group 0 and the row term's parts in group 1; groups 2-3 are
-// zero.  So sum_k A[j][k] B[i][k] = colterm_j + rowterm_i.
-__device__ __forceinline__ bf16x4 blk_col_operand(const bf16x4* parts, int tile, int lane) {
-  const int g = lane >> 4;
-  const bf16x4 one = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)0.f};
-  const bf16x4 zero = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
-  const bf16x4 p = parts[tile * 16 + (lane & 15)];
-  return g == 0 ? p : (g == 1 ? one : zero);
-}
-__device__ __forceinline__ bf16x4 blk_row_operand(const bf16x4* parts, int tile, int lane) {
-  const int g = lane >> 4;
-  const bf16x4 one = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)0.f};
-  const bf16x4 zero = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
-  const bf16x4 p = parts[tile * 16 + (lane & 15)];
-  return g == 1 ? p : (g == 0 ? one : zero);
-}
-
 // One sweep of a wave's sub-block: row tiles wr0 .. wr0 + wr (wr <= BLK_WR, wave-uniform)
 // against BLK_WC column tiles, of which the first wc are the wave's (wc0 .. wc0 + wc);
 // the logits of the others are NEG_BIG, so they add exp2(-huge) = 0 and the inner loop

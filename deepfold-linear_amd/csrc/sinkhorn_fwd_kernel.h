@@ -33,6 +33,8 @@
 // All logits are handled in log2 units (x * log2 e) so that exp2 maps onto
 // v_exp_f32 directly.
 #pragma once
+#include <type_traits>
+
 #include "sinkhorn_args.h"
 #include "sinkhorn_engine.h"
 
@@ -227,15 +229,37 @@ __device__ __forceinline__ void fwd_resident_output(const SinkFwdArgs& a, int b,
 // GEN: the cost may carry position bins or geometry (the host sets it when either
 // is passed); GEN = false compiles no bias code, which keeps the content-only
 // sweeps at their register budget.
-enum FwdMode : int { FWD_UOT = 0, FWD_UOT_HIST = 1, FWD_BALANCED = 2 };
+enum FwdMode : int { FWD_UOT = 0, FWD_UOT_HIST = 1, FWD_BALANCED = 2, FWD_UOT_REG = 3 };
+
+// Register storage of the resident layout (FWD_UOT_REG): a wave holds the logits of
+// its pairs (resident tile r < nr of the member's stripe, streamed tile wave + 8 k,
+// k < KS) in VGPRs, KS = ceil(n_tiles / 8) rounded up to 2, 4 or 6 and nr at most
+// reg_nrm(KS) (at most 18 pairs per direction, 144 VGPRs for both).
+__host__ __device__ constexpr int reg_ks(int n_tiles) {
+  return (n_tiles + 7) / 8 <= 2 ? 2 : ((n_tiles + 7) / 8 <= 4 ? 4 : ((n_tiles + 7) / 8 <= 6 ? 6 : 0));
+}
+__host__ __device__ constexpr int reg_nrm(int ks) { return ks == 6 ? 3 : 4; }
+// Whether every member of every group fits when G members share up to N tokens (a
+// group with fewer valid tokens has no more stripe tiles and no more slots).
+__host__ __device__ inline bool reg_fits(int N, int G) {
+  const int T = (N + 15) / 16, ks = reg_ks(T);
+  return ks > 0 && G >= 1 && (T + G - 1) / G <= reg_nrm(ks);
+}
+// Entries of the split-potential arrays: every slot's streamed tile reads inside them.
+__host__ __device__ inline int reg_cp_rows(int N, int rcap) {
+  const int r = 8 * 16 * reg_ks((N + 15) / 16);
+  return rcap > r ? rcap : r;
+}
 template <typename T, int DP, bool STREAM, int MODE, bool GEN>
 __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   constexpr bool BAL = MODE == FWD_BALANCED;
-  constexpr bool HIST = MODE != FWD_UOT;
+  constexpr bool HIST = MODE == FWD_UOT_HIST || MODE == FWD_BALANCED;
+  constexpr bool REG = !STREAM && MODE == FWD_UOT_REG;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_flag, s_tmp, s_local;
   __shared__ unsigned s_du, s_dv;
   __shared__ int s_cnt;
+  __shared__ int s_flagp[2];  // resident dataflow: expired waits of the half-iterations, by parity
   __shared__ float s_posw[BIN_NONE + 1];
   int grp, member;
   if (!group_of(a.B * a.H, a.G, grp, member)) return;  // surplus workgroup of the XCD-aligned grid
@@ -244,7 +268,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const int Np = ((N + 31) / 32) * 32;
   constexpr bool bal = BAL;
   const bool has_v = !BAL || (a.v != nullptr && a.o_avg != nullptr);  // UOT mode always has V
-  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; s_cnt = 0; s_local = 1; }
+  if (threadIdx.x == 0) { s_flag = 0; s_du = 0u; s_dv = 0u; s_cnt = 0; s_local = 1; s_flagp[0] = s_flagp[1] = 0; }
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(a.err.ws + 1, a.salt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
@@ -267,6 +291,12 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   float* lmu_l = mx2 + loc;     // log mu of my rows
   float* lnu_l = lmu_l + loc;   // log nu of my columns
   float* scratch = lnu_l + loc;
+  // register storage: split parts of u and v (by index) and of -shift of my rows / columns
+  const int cpn = REG ? reg_cp_rows(N, rcap) : 0;
+  bf16x4* cpU = reinterpret_cast<bf16x4*>(scratch + sweep_scratch<FWD_NT>());
+  bf16x4* cpV = cpU + cpn;
+  bf16x4* rpR = cpV + cpn;
+  bf16x4* rpC = rpR + loc;
 
   const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &s_tmp);
   const int n_tiles = (n + 15) / 16;
@@ -333,6 +363,13 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
     const bool ok = i < n && valid[i];
     vecU[i] = ok ? (a.u_init ? a.u_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
     vecV[i] = ok ? (a.v_init ? a.v_init[bh * N + i] * LOG2E : 0.f) : NEG_BIG;
+  }
+  if constexpr (REG) {
+    for (int i = threadIdx.x; i < cpn; i += FWD_NT) {  // the same thread wrote vecU[i], vecV[i]
+      cpU[i] = split3(i < rcap ? vecU[i] : NEG_BIG);
+      cpV[i] = split3(i < rcap ? vecV[i] : NEG_BIG);
+    }
+    for (int q = threadIdx.x; q < loc; q += FWD_NT) rpR[q] = rpC[q] = split3(0.f);
   }
   const float w_h = bal ? w_bal : (a.w_dist ? a.w_dist[h] : 0.f);
   const bool use_geo = GEN && (a.x != nullptr) && (w_h != 0.f);
@@ -422,10 +459,38 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       }
     }
   };
+  // Resident storage runs dataflow half-iterations (flow_sweep): each wave polls the
+  // previous half-iteration's words of its own streamed tiles, chooses its shift from
+  // their change, and the wave partials are combined after the chunk's barrier; no
+  // block-wide gather.  The first sweep of each direction is online.  A wait that
+  // expires sets the flag of its half-iteration's parity, read after that
+  // half-iteration's last barrier (a wave can be at most one half-iteration ahead).
+  int chunk = 0;
+  auto flow_poll = [&](uint64_t* words, float* w2, int it) __attribute__((always_inline)) -> bool {
+    if (phase == 1) return true;  // the first sweep reads the initial potentials
+    float dm;
+    if (!wave_gather<FWD_NW>(words, n, n_tiles, (salt | phase) - 1, w2, valid, a.err, dm)) s_flagp[phase & 1] = 1;
+    return it == 0 || !(dm <= FIXED_SHIFT_MAX_DELTA);
+  };
   // ---- row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j)) for my rows
   auto row_update = [&](int it) __attribute__((always_inline)) -> bool {
     ++phase;
-    {
+    if constexpr (!STREAM) {
+      const uint32_t tag = salt | phase;
+      const bool online = flow_poll(xv, vecV, it) || it == 0;
+      auto pub = [&](int q, float l2) {
+        const int i = r_lo + q;
+        if (i < n) {
+          const float u = kappa * (lmu_l[q] - l2 * LN2);
+          xch_put(xu + i, u, tag, local);
+          if constexpr (HIST) a.hist[((size_t)(2 * it + 1) * a.B * a.H + bh) * N + i] = valid[i] ? u : 0.f;
+        }
+      };
+      if (general) flow_sweep<FWD_NT, T, DP, true, false>(online, QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse_r, scratch, chunk, pub);
+      else flow_sweep<FWD_NT, T, DP, false, false>(online, QS, KS, vecV, n_tiles, t0, nr, sc, bias, lse_r, scratch, chunk, pub);
+      if (s_flagp[phase & 1]) return false;
+      return agree_placement();
+    } else {
       const uint32_t tag = salt | phase;
       const bool online = it == 0 || __uint_as_float(s_dv) > FIXED_SHIFT_MAX_DELTA;
       auto pub = [&](int q, float l2) {
@@ -442,7 +507,24 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   // ---- column update: v_j = kappa (log nu_j - LSE_i(L_ij + u_i)) for my columns
   auto col_update = [&](int it) __attribute__((always_inline)) -> bool {
     ++phase;
-    {
+    if constexpr (!STREAM) {
+      const uint32_t tag = salt | phase;
+      const bool online = flow_poll(xu, vecU, it) || it == 0;
+      const bool last = it == a.K_iter - 1;
+      auto pub = [&](int q, float l2) {
+        const int j = r_lo + q;
+        if (j < n) {
+          const float v = kappa * (lnu_l[q] - l2 * LN2);
+          xch_put(xv + j, v, tag, local);
+          if (!BAL && last && valid[j]) a.col_lse[bh * N + j] = l2 * LN2;
+          if constexpr (HIST) a.hist[((size_t)(2 * it) * a.B * a.H + bh) * N + j] = valid[j] ? v : 0.f;
+        }
+      };
+      if (general) flow_sweep<FWD_NT, T, DP, true, true>(online, KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse_c, scratch, chunk, pub);
+      else flow_sweep<FWD_NT, T, DP, false, true>(online, KS, QS, vecU, n_tiles, t0, nr, sc, bias, lse_c, scratch, chunk, pub);
+      if (s_flagp[phase & 1]) return false;
+      return agree_placement();
+    } else {
       const uint32_t tag = salt | phase;
       const bool online = it == 0 || __uint_as_float(s_du) > FIXED_SHIFT_MAX_DELTA;
       const bool last = it == a.K_iter - 1;
@@ -463,12 +545,126 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   // The UOT order is row then column, the balanced order column then row.  One call
   // site per update in each instantiation: with two, the compiler outlines them
   // into calls with a stack frame.
-  for (int it = 0; it < a.K_iter; ++it) {
-    if constexpr (BAL) {
-      if (!col_update(it) || !row_update(it)) return;
-    } else {
-      if (!row_update(it) || !col_update(it)) return;
+  if constexpr (REG) {
+    // ---- register storage: the logits of every wave's pairs stay in VGPRs
+    auto reg_loop = [&](auto ksc) __attribute__((always_inline)) -> bool {
+      constexpr int KSL = decltype(ksc)::value;
+      constexpr int NRM = reg_nrm(KSL);
+      using M = Mfma<T, DP>;
+      const int lane = threadIdx.x & (WAVE - 1);
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+      const int g = lane >> 4;
+      if (nr > NRM) {  // the host's reg_fits rules this out
+        if (threadIdx.x == 0) raise_error(a.err, a.salt, 3u);
+        return false;
+      }
+      // S[r KSL + k]: row block (i resident, j streamed) and column block (j resident,
+      // i streamed), sc q.k + bias, NEG_BIG where the wave has no tile
+      f32x4 SR[NRM * KSL], SC[NRM * KSL];
+#pragma unroll
+      for (int r = 0; r < NRM; ++r) {
+#pragma unroll
+        for (int k = 0; k < KSL; ++k) {
+          const int sl = r * KSL + k, st = wave + FWD_NW * k;
+          SR[sl] = SC[sl] = f32x4{NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG};
+          if (r < nr && st < n_tiles) {
+            const int ri = (t0 + r) * 16 + (lane & 15), si = st * 16 + (lane & 15);
+            typename M::Frag qr, kr, qs, ks;
+            M::load(qr, QS + (size_t)ri * DP, lane);
+            M::load(kr, KS + (size_t)ri * DP, lane);
+            M::load(qs, QS + (size_t)si * DP, lane);
+            M::load(ks, KS + (size_t)si * DP, lane);
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 xr = M::qk(ks, qr, z);  // [m = j streamed][n = i resident]
+            const f32x4 xc = M::qk(qs, kr, z);  // [m = i streamed][n = j resident]
+            f32x4 br[1] = {z}, bc[1] = {z};
+            if (general) {
+              const int s0[1] = {st * 16 + 4 * g};
+              bias.template quads<false, 1>(ri, s0, br);
+              bias.template quads<true, 1>(ri, s0, bc);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              SR[sl][q] = __builtin_fmaf(xr[q], sc, br[0][q]);
+              SC[sl][q] = __builtin_fmaf(xc[q], sc, bc[0][q]);
+            }
+          }
+        }
+      }
+      // what the combining thread of local row / column q = threadIdx.x publishes with,
+      // loaded once
+      const int qc = threadIdx.x, ic = r_lo + qc;
+      const bool in_c = qc < nr * 16 && ic < n, ok_c = in_c && valid[ic];
+      const float lmu_c = in_c ? lmu_l[qc] : 0.f, lnu_c = in_c ? lnu_l[qc] : 0.f;
+      for (int it = 0; it < a.K_iter; ++it) {
+        // row update: u_i = kappa (log mu_i - LSE_j(L_ij + v_j))
+        {
+          ++phase;
+          const uint32_t tag = salt | phase;
+          bool online = it == 0;
+          if (phase > 1) {
+            float dm;
+            if (!wave_gather<FWD_NW>(xv, n, n_tiles, tag - 1, vecV, valid, a.err, dm, cpV)) s_flagp[phase & 1] = 1;
+            online = online || !(dm <= FIXED_SHIFT_MAX_DELTA);
+          }
+          float* part = scratch + (chunk & 1) * (FWD_NW * SK_RT * 16);
+          ++chunk;
+          reg_sweep<KSL, NRM, FWD_NW>(online, SR, nr, cpV, rpR, lse_r, part);
+          lds_barrier();
+          flow_combine<FWD_NW>(part, nr, lse_r, [&](int q, float l2) {
+            if (in_c) xch_put(xu + ic, kappa * (lmu_c - l2 * LN2), tag, local);
+            rpR[q] = split3(ok_c ? -l2 : 0.f);
+          });
+          if (s_flagp[phase & 1]) return false;
+          if (!agree_placement()) return false;
+        }
+        // column update: v_j = kappa (log nu_j - LSE_i(L_ij + u_i))
+        {
+          ++phase;
+          const uint32_t tag = salt | phase;
+          const bool last = it == a.K_iter - 1;
+          float dm;
+          if (!wave_gather<FWD_NW>(xu, n, n_tiles, tag - 1, vecU, valid, a.err, dm, cpU)) s_flagp[phase & 1] = 1;
+          const bool online = it == 0 || !(dm <= FIXED_SHIFT_MAX_DELTA);
+          float* part = scratch + (chunk & 1) * (FWD_NW * SK_RT * 16);
+          ++chunk;
+          reg_sweep<KSL, NRM, FWD_NW>(online, SC, nr, cpU, rpC, lse_c, part);
+          lds_barrier();
+          flow_combine<FWD_NW>(part, nr, lse_c, [&](int q, float l2) {
+            if (in_c) xch_put(xv + ic, kappa * (lnu_c - l2 * LN2), tag, local);
+            rpC[q] = split3(ok_c ? -l2 : 0.f);
+            if (last && ok_c) a.col_lse[bh * N + ic] = l2 * LN2;
+          });
+          if (s_flagp[phase & 1]) return false;
+        }
+      }
+      return true;
+    };
+    const int ksg = reg_ks(n_tiles);
+    bool ok;
+    if (ksg == 2) ok = reg_loop(std::integral_constant<int, 2>{});
+    else if (ksg == 4) ok = reg_loop(std::integral_constant<int, 4>{});
+    else if (ksg == 6) ok = reg_loop(std::integral_constant<int, 6>{});
+    else {
+      if (threadIdx.x == 0) raise_error(a.err, a.salt, 3u);
+      ok = false;
     }
+    if (!ok) return;
+  } else {
+    for (int it = 0; it < a.K_iter; ++it) {
+      if constexpr (BAL) {
+        if (!col_update(it) || !row_update(it)) return;
+      } else {
+        if (!row_update(it) || !col_update(it)) return;
+      }
+    }
+  }
+  if (!STREAM && a.K_iter > 0) {
+    // The output pass reads whole vectors.  The last half-iteration's is gathered by
+    // the block; the other one is whole already (the last sweep's waves polled every
+    // tile of it).
+    if (!gather_potential<FWD_NT>(BAL ? xu : xv, n, salt | phase, BAL ? vecU : vecV, valid, a.err, &s_flag, &s_dv))
+      return;
   }
   if (a.K_iter == 0 && !BAL) {
     auto pub = [&](int q, float l2) {
@@ -584,7 +780,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stream) {
+inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stream, bool reg = false) {
   const size_t Np = ((N + 31) / 32) * 32;
   const size_t loc = fwd_local_rows(N, G);
   size_t bytes = ((Np + 15) / 16) * 16;  // valid
@@ -600,6 +796,7 @@ inline size_t sinkhorn_fwd_lds_bytes_t(int N, int DP, int elem, int G, bool stre
     bytes += (2 * rcap + 3 * Np) * 4;     // vecU, vecV, xs
     bytes += 5 * loc * 4;                 // lse_r, lse_c, mx2, lmu_l, lnu_l
     bytes += (size_t)sweep_scratch<FWD_NT>() * 4;
+    if (reg) bytes += (2 * (size_t)reg_cp_rows(N, (int)rcap) + 2 * loc) * 8;  // cpU, cpV, rpR, rpC
   }
   return bytes;
 }
@@ -630,6 +827,18 @@ hipError_t launch_fwd_dt(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds,
   } else {
     if (DP == 32) return launch_fwd_t<float, 32, STREAM, MODE, GEN>(a, lds, stream, coop);
     if (DP == 64) return launch_fwd_t<float, 64, STREAM, MODE, GEN>(a, lds, stream, coop);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <bool GEN>
+hipError_t launch_fwd_reg_dt(const SinkFwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream, bool coop) {
+  if (bf16_in) {
+    if (DP == 32) return launch_fwd_t<bf16, 32, false, FWD_UOT_REG, GEN>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<bf16, 64, false, FWD_UOT_REG, GEN>(a, lds, stream, coop);
+  } else {
+    if (DP == 32) return launch_fwd_t<float, 32, false, FWD_UOT_REG, GEN>(a, lds, stream, coop);
+    if (DP == 64) return launch_fwd_t<float, 64, false, FWD_UOT_REG, GEN>(a, lds, stream, coop);
   }
   return hipErrorInvalidValue;
 }

@@ -105,9 +105,12 @@ int dfl_debug_set_spin_limit(unsigned limit);
  * on MFMA every sweep (fails with an argument error if they do not fit);
  * STREAM keeps only each workgroup's stripe in LDS and streams the rest through L2
  * (long sequences, e.g. N = 4096, d = 64);
- * DFL_STORAGE_AUTO (0) picks REGISTER where it serves and the cost carries position
- * bins or a geometry term, else RESIDENT where it fits, else STREAM.  Results agree
- * to rounding.
+ * DFL_STORAGE_AUTO (0) picks the resident layout with its logits held in registers
+ * (each workgroup's stripe of plan rows and of plan columns, computed once) for the
+ * UOT forward without hist where every stripe fits the register tiles (N <= 768 with
+ * at most 3 tiles of 16 rows per stripe at N > 512, 4 below), else REGISTER where it
+ * serves and the cost carries position bins or a geometry term, else RESIDENT where
+ * it fits, else STREAM.  Results agree to rounding.
  * hist (K_iter,2,B,H,N) may be NULL; if given, the forward also writes v after the
  * column update and u after the row update of every iteration (natural log), which
  * dfl_sinkhorn_unrolled_bwd needs.
