@@ -100,18 +100,15 @@ __global__ void __launch_bounds__(256) balanced_finalize_kernel(BalBwdArgs a, fl
   const int nx = a.B * a.N * 3;
   if (e < nx) {
     const int b = e / (a.N * 3), r = e % (a.N * 3);
-    float s = 0.f;
-    for (int h = 0; h < a.H; ++h) s += a.dx_part[((size_t)b * a.H + h) * a.N * 3 + r];
-    dx[e] = s;
+    dx[e] = ordered_sum(a.dx_part + (size_t)b * a.H * a.N * 3 + r, (size_t)a.N * 3, a.H, 0.f);
   } else if (e < nx + a.H) {
     const int h = e - nx;
     float sa = 0.f, sr = 0.f;
-    for (int b = 0; b < a.B; ++b)
-      for (int m = 0; m < a.G; ++m) {
-        const size_t o = ((size_t)(b * a.H + h) * a.G + m) * 2;
-        sa += a.ar_part[o];
-        sr += a.ar_part[o + 1];
-      }
+    for (int b = 0; b < a.B; ++b) {
+      const float* p = a.ar_part + ((size_t)(b * a.H + h) * a.G) * 2;
+      sa = ordered_sum(p, 2, a.G, sa);
+      sr = ordered_sum(p + 1, 2, a.G, sr);
+    }
     if (dalpha) dalpha[h] = sa;
     if (dr) dr[h] = sr;
   }

@@ -43,6 +43,7 @@ hipError_t launch_sinkhorn_bwd(const SinkBwdArgs& a, bool bf16_in, int DP, size_
 hipError_t launch_sinkhorn_bwd_stream(const SinkBwdArgs& a, bool bf16_in, int DP, size_t lds, hipStream_t stream,
                                       bool coop);
 hipError_t launch_sinkhorn_bwd_prep(const SinkBwdArgs& a, bool bf16_in, int DP, hipStream_t stream);
+hipError_t launch_bias_mat(const SinkBwdArgs& a, float* mat, float* matT, hipStream_t stream);
 hipError_t launch_sinkhorn_bwd_finalize(const SinkBwdArgs& a, float* dx, float* dpw, float* dw,
                                         hipStream_t stream);
 hipError_t launch_attn_fwd(const AttnArgs& a, bool bf16_in, int DP, hipStream_t s);
@@ -667,6 +668,15 @@ size_t dfl_sinkhorn_workspace_size(int B, int H, int N) {
   return stream_region_offset(B, H, N, G) + stream_region_bytes(B, H, N, G) + bins8_bytes(B, N);
 }
 
+// The backward's precomputed bias: [B*H][Np][Np] floats and the transposed copy, after
+// the regular workspace (rounded up to 256 bytes).
+static size_t bias_mat_offset(int B, int H, int N) { return (dfl_sinkhorn_workspace_size(B, H, N) + 255) / 256 * 256; }
+size_t dfl_sinkhorn_bias_workspace_size(int B, int H, int N) {
+  if (B <= 0 || H <= 0 || N <= 0) return 0;
+  const size_t np = np32(N);
+  return 2 * (size_t)B * H * np * np * 4 + (bias_mat_offset(B, H, N) - dfl_sinkhorn_workspace_size(B, H, N));
+}
+
 int dfl_pending_error(void) {
   if (!g_mailbox_host) return 0;
   const uint32_t w = __atomic_exchange_n(g_mailbox_host, 0u, __ATOMIC_ACQ_REL);
@@ -834,6 +844,17 @@ int dfl_sinkhorn_bwd(const dfl_sinkhorn_bwd_params* p, void* workspace, size_t w
     if (int rc = prepare_bins8(p->pos_bins, p->B, p->N, workspace, sinkhorn_bins8_offset(p->B, p->H, p->N),
                                &a.bins8, &a.bins8t, stream))
       return rc;
+  // a workspace with room for the bias matrices: the per-element bins lookups and
+  // distances are evaluated once here instead of in every sweep
+  const bool has_bias = (p->pos_bins && p->pos_weight) || (p->x_res && p->w_dist);
+  if (has_bias && workspace_bytes >= need + dfl_sinkhorn_bias_workspace_size(p->B, p->H, p->N)) {
+    float* mat = reinterpret_cast<float*>(ws + bias_mat_offset(p->B, p->H, p->N));
+    float* matT = mat + (size_t)p->B * p->H * np32(p->N) * np32(p->N);
+    hipError_t e = dfl::launch_bias_mat(a, mat, matT, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "bias matrix launch");
+    a.bias_mat = mat;
+    a.bias_matT = matT;
+  }
   const bool coop = coop_launch(G, a.B * a.H);
   hipError_t e = dfl::launch_sinkhorn_bwd_prep(a, p->dtype == DFL_BF16, DP, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "sinkhorn backward prep launch");

@@ -245,6 +245,20 @@ __device__ __forceinline__ void block_atomic_max_u32(unsigned* s, unsigned x) {
   if ((threadIdx.x & (WAVE - 1)) == 0) atomicMax(s, w);
 }
 
+// s + sum_{k < n} p[k * stride] in the order k = 0, 1, ...: loads in batches of 8 in
+// flight, then the adds (the order of a plain loop, without one memory latency per term).
+__device__ __forceinline__ float ordered_sum(const float* p, size_t stride, int n, float s) {
+  for (int k0 = 0; k0 < n; k0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = k0 + k < n ? p[(size_t)(k0 + k) * stride] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k0 + k < n) s += v[k];
+  }
+  return s;
+}
+
 // ---------------------------------------------------------------------------
 // Error flag and tagged exchange.
 constexpr uint32_t SPIN_LIMIT = 1u << 22;  // ~2-4 s of polling

@@ -116,6 +116,9 @@ struct SinkBwdArgs {
   float* vec_ws;   // per-workgroup vectors, BWD_STREAM_VECS * Np floats each
   const uint8_t* bins8;   // padded uint8 bins [B][Np][Np] and transposed (null without bins)
   const uint8_t* bins8t;
+  // per-head bias computed once (bias_mat_kernel), [B*H][Np][Np] and transposed, or null
+  const float* bias_mat;
+  const float* bias_matT;
 };
 
 // Unrolled backward of the balanced transport (flash_sinkhorn_transport.py:322-373,

@@ -60,21 +60,19 @@ __global__ void sinkhorn_bwd_finalize_kernel(SinkBwdArgs a, float* dx, float* dp
     const int i = rem / 3;
     const bool ok = a.mask ? a.mask[(size_t)b * a.N + i] > 0.5f : true;
     float s = 0.f;
-    if (ok)
-      for (int h = 0; h < a.H; ++h) s += a.dx_part[(((size_t)b * a.H + h) * a.N) * 3 + rem];
+    if (ok) s = ordered_sum(a.dx_part + ((size_t)b * a.H * a.N) * 3 + rem, (size_t)a.N * 3, a.H, 0.f);
     dx[tid] = s;
   }
   if (tid < a.H * 68) {
     const int h = tid / 68, k = tid % 68;
     float s = 0.f;
     for (int b = 0; b < a.B; ++b)
-      for (int m = 0; m < a.G; ++m) s += a.dpw_part[(((size_t)b * a.H + h) * a.G + m) * 68 + k];
+      s = ordered_sum(a.dpw_part + (((size_t)b * a.H + h) * a.G) * 68 + k, 68, a.G, s);
     if (dpw) dpw[tid] = s;  // zeros without position bins (their partials are zero)
   }
   if (tid < a.H) {
     float s = 0.f;
-    for (int b = 0; b < a.B; ++b)
-      for (int m = 0; m < a.G; ++m) s += a.dw_part[((size_t)b * a.H + tid) * a.G + m];
+    for (int b = 0; b < a.B; ++b) s = ordered_sum(a.dw_part + ((size_t)b * a.H + tid) * a.G, 1, a.G, s);
     if (dw) dw[tid] = s;
   }
 }
@@ -107,6 +105,66 @@ hipError_t launch_sinkhorn_bwd_prep(const SinkBwdArgs& a, bool bf16_in, int DP, 
     if (DP == 64) return launch_prep_t<float, 64>(a, stream);
   }
   return hipErrorInvalidValue;
+}
+
+// The cost bias of every (b,h), once per backward call, in the backward's sweep
+// orientations: mat[bh][i][j] = bias(i, j) and matT[bh][i][j] = bias(j, i), i, j < Np,
+// from Bias::quads with the coordinates and tables a backward workgroup stages (x of
+// rows below the batch row's last valid token, else 0), so the sweeps read exactly the
+// values they would compute.  Block: 16 rows i of one (b,h); thread: 4 columns at a time.
+constexpr int BIAS_ROWS = 16;
+__global__ void __launch_bounds__(256) bias_mat_kernel(SinkBwdArgs a, float* mat, float* matT) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float posw[BIN_NONE + 1];
+  __shared__ int s_tmp;
+  const int N = a.N, Np = ((N + 31) / 32) * 32;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  float* xs = reinterpret_cast<float*>(smem);                       // [Np][3]
+  unsigned char* valid = smem + (size_t)Np * 3 * sizeof(float);     // [Np]
+  const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &s_tmp);
+  const float eps = a.eps[h];
+  const float w_h = a.w_dist ? a.w_dist[h] : 0.f;
+  const bool use_geo = a.x != nullptr && w_h != 0.f;
+  const bool use_pos = a.bins8 != nullptr && a.pos_w != nullptr;
+  for (int k = threadIdx.x; k <= (int)BIN_NONE; k += blockDim.x)
+    posw[k] = (use_pos && k < (int)BIN_NONE) ? -LOG2E * a.pos_w[h * 68 + k] / eps : 0.f;
+  for (int e = threadIdx.x; e < 3 * Np; e += blockDim.x) {
+    const int i = e / 3, c = e - 3 * i;
+    xs[e] = (a.x && i < n) ? a.x[((size_t)b * N + i) * 3 + c] : 0.f;
+  }
+  __syncthreads();
+  Bias bias;
+  bias.b8 = use_pos ? a.bins8 + (size_t)b * Np * Np : nullptr;
+  bias.b8t = use_pos ? a.bins8t + (size_t)b * Np * Np : nullptr;
+  bias.posw = posw;
+  bias.xs = use_geo ? xs : nullptr;
+  bias.geo_scale = -LOG2E * w_h / eps;
+  bias.r0 = a.r0;
+  bias.Np = Np;
+  // Bias::quads itself in both orientations (a distance evaluated separately and added
+  // afterwards would round differently from the fused form the sweeps use)
+  const int q4 = Np / 4;
+  for (int e = threadIdx.x; e < BIAS_ROWS * q4; e += blockDim.x) {
+    const int i = blockIdx.x * BIAS_ROWS + e / q4, j0 = 4 * (e % q4);
+    if (i >= Np) break;
+    const int s0[1] = {j0};
+    f32x4 o[1], ot[1];
+    bias.template quads<false, 1>(i, s0, o);
+    bias.template quads<true, 1>(i, s0, ot);
+    const size_t off = ((size_t)bh * Np + i) * Np + j0;
+    *reinterpret_cast<f32x4*>(mat + off) = o[0];
+    *reinterpret_cast<f32x4*>(matT + off) = ot[0];
+  }
+}
+
+hipError_t launch_bias_mat(const SinkBwdArgs& a, float* mat, float* matT, hipStream_t stream) {
+  const int Np = ((a.N + 31) / 32) * 32;
+  const size_t lds = (size_t)Np * 3 * sizeof(float) + Np;
+  hipError_t e = set_lds_limit((const void*)bias_mat_kernel, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(bias_mat_kernel, dim3((unsigned)((Np + BIAS_ROWS - 1) / BIAS_ROWS), (unsigned)(a.B * a.H)),
+                     dim3(256), lds, stream, a, mat, matT);
+  return hipGetLastError();
 }
 
 hipError_t launch_sinkhorn_bwd_finalize(const SinkBwdArgs& a, float* dx, float* dpw, float* dw, hipStream_t stream) {

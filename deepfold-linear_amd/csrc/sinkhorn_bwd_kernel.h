@@ -677,6 +677,10 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   bias.r0 = a.r0;
   bias.Np = Np;
   const bool general = use_pos || use_geo;
+  if (general && a.bias_mat) {
+    bias.mat = a.bias_mat + bh * Np * Np;
+    bias.matT = a.bias_matT + bh * Np * Np;
+  }
   const bool geo_grad = GEN && a.geo_grad != 0 && a.x != nullptr;
 
   // ---- D_i (prep kernel) for all rows

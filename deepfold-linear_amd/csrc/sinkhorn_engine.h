@@ -39,6 +39,11 @@ struct Bias {
   float geo_scale;     // -log2e * w / eps
   float r0;
   int Np;
+  // The same values computed once for this (b,h) (bias_mat_kernel): mat[i][j] =
+  // bias(i, j) and matT[j][i] = bias(i, j), row stride Np; when set, the lookups
+  // below read them instead of evaluating bins and distances.
+  const float* mat = nullptr;
+  const float* matT = nullptr;
   __device__ __forceinline__ float geo(float dx, float dy, float dz) const {
     const float dist = fmaxf(__builtin_amdgcn_sqrtf(dx * dx + dy * dy + dz * dz), 1e-8f);
     return geo_scale * dist * __builtin_amdgcn_rcpf(r0 + dist);
@@ -48,6 +53,7 @@ struct Bias {
     // are discarded, and clamping keeps every read inside the padded arrays.
     i = min(i, Np - 1);
     j = min(j, Np - 1);
+    if (mat) return mat[(size_t)i * Np + j];
     float b = 0.f;
     if (b8) b += posw[b8[(size_t)i * Np + j]];
     if (xs) b += geo(xs[3 * i] - xs[3 * j], xs[3 * i + 1] - xs[3 * j + 1], xs[3 * i + 2] - xs[3 * j + 2]);
@@ -60,6 +66,12 @@ struct Bias {
   // back, so their latencies overlap (a test per word leaves one wait per load).
   template <bool COL, int S>
   __device__ __forceinline__ void quads(int r, const int (&s0)[S], f32x4 (&out)[S]) const {
+    if (mat) {
+      const float* row = (COL ? matT : mat) + (size_t)r * Np;
+#pragma unroll
+      for (int k = 0; k < S; ++k) out[k] = *reinterpret_cast<const f32x4*>(row + s0[k]);
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < S; ++k) out[k] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (b8) {

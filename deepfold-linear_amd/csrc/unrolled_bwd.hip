@@ -94,21 +94,17 @@ __global__ void __launch_bounds__(256) unrolled_finalize_kernel(UnrBwdArgs a, fl
   const int nx = a.B * a.N * 3;
   if (dx && e < nx) {
     const int b = e / (a.N * 3), r = e % (a.N * 3);
-    float s = 0.f;
-    for (int h = 0; h < a.H; ++h) s += a.dx_part[((size_t)b * a.H + h) * a.N * 3 + r];
-    dx[e] = s;
+    dx[e] = ordered_sum(a.dx_part + (size_t)b * a.H * a.N * 3 + r, (size_t)a.N * 3, a.H, 0.f);
   }
   if (dpw && e < a.H * 68) {
     const int h = e / 68, k = e % 68;
     float s = 0.f;
-    for (int b = 0; b < a.B; ++b)
-      for (int m = 0; m < a.G; ++m) s += a.dpw_part[(((size_t)b * a.H + h) * a.G + m) * 68 + k];
+    for (int b = 0; b < a.B; ++b) s = ordered_sum(a.dpw_part + (((size_t)b * a.H + h) * a.G) * 68 + k, 68, a.G, s);
     dpw[e] = s;
   }
   if (dw && e < a.H) {
     float s = 0.f;
-    for (int b = 0; b < a.B; ++b)
-      for (int m = 0; m < a.G; ++m) s += a.dw_part[((size_t)b * a.H + e) * a.G + m];
+    for (int b = 0; b < a.B; ++b) s = ordered_sum(a.dw_part + ((size_t)b * a.H + e) * a.G, 1, a.G, s);
     dw[e] = s;
   }
 }

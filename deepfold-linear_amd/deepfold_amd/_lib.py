@@ -232,6 +232,7 @@ SIGNATURES = [
     ("dfl_get_launch_mode", I32, []),
     ("dfl_debug_set_spin_limit", I32, [ctypes.c_uint]),
     ("dfl_sinkhorn_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
+    ("dfl_sinkhorn_bias_workspace_size", ctypes.c_size_t, [I32, I32, I32]),
     ("dfl_sinkhorn_fwd", I32, [ctypes.POINTER(SinkhornFwdParams), P, ctypes.c_size_t, P]),
     ("dfl_sinkhorn_fwd_noalloc", I32, [ctypes.POINTER(SinkhornFwdParams), P]),
     ("dfl_noalloc_error", I32, [P]),

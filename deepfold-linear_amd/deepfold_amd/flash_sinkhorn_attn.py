@@ -49,6 +49,9 @@ _STORAGE = {"auto": _lib.DFL_STORAGE_AUTO, "resident": _lib.DFL_STORAGE_RESIDENT
             "register": _lib.DFL_STORAGE_REGISTER}
 # the backward has no register storage: there "register" means its automatic choice
 _BWD_STORAGE = dict(_STORAGE, register=_lib.DFL_STORAGE_AUTO)
+# largest bias extension of the backward workspace requested (dfl_sinkhorn_bias_workspace_size:
+# 2 B H Np^2 floats, 75 MB at B 2, H 8, N 768); above it the sweeps evaluate the bias
+_BIAS_WS_MAX = 4 << 30
 
 
 def _qkvg(Q, K, V, G):
@@ -173,7 +176,12 @@ class FlashSinkhornAttn(torch.autograd.Function):
         if ctx.unrolled:
             return FlashSinkhornAttn._backward_unrolled(ctx, go, gxc, dq, dk, dv, dg, dlmu, dlnu, dx, dpw, dw)
         lib = _lib.load()
-        ws = _lib.workspace(dev, lib.dfl_sinkhorn_workspace_size(B, H, N))
+        nbytes = lib.dfl_sinkhorn_workspace_size(B, H, N)
+        if (pw is not None and bins is not None) or (x is not None and wd is not None):
+            extra = lib.dfl_sinkhorn_bias_workspace_size(B, H, N)
+            if extra <= _BIAS_WS_MAX:  # the bias once per call instead of in every sweep
+                nbytes += extra
+        ws = _lib.workspace(dev, nbytes)
         sb, sh, sn, _ = q.stride()
         p = _lib.SinkhornBwdParams(
             _lib.DFL_BF16 if dt == torch.bfloat16 else _lib.DFL_F32,

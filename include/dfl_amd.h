@@ -152,6 +152,16 @@ typedef struct dfl_sinkhorn_fwd_params {
 size_t dfl_sinkhorn_workspace_size(int B, int H, int N);
 int dfl_sinkhorn_fwd(const dfl_sinkhorn_fwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Optional extension of the workspace for dfl_sinkhorn_bwd: a workspace of
+ * dfl_sinkhorn_workspace_size(B, H, N) + dfl_sinkhorn_bias_workspace_size(B, H, N)
+ * bytes lets a backward whose cost has position bins or a geometry term evaluate
+ * that bias once per call (2 B H Np^2 floats, Np = N rounded up to 32) and read it
+ * in every sweep instead of looking up bins and evaluating distances per element.
+ * The results are the same; the forward ignores the extension.  No counterpart in
+ * the reference, whose Triton backward recomputes the cost tile
+ * (sinkhorn_kernel.py:1578-1760). */
+size_t dfl_sinkhorn_bias_workspace_size(int B, int H, int N);
+
 /* Allocation-free variant of dfl_sinkhorn_fwd.  It has no counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same

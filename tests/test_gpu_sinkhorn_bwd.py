@@ -203,3 +203,47 @@ def test_backward_bins_outside_table():
     want = ref.backward_reference(dict(oi, K_iter=5), fo, go.numpy(), gxc.numpy())
     compare(got, want, 1e-4, "bins-outside", skip=("pos_weight",))
     assert_close_rel(got["pos_weight"], np.asarray(want["pos_weight"])[:, :68], 1e-4, "bins-outside:pos_weight")
+
+
+@pytest.mark.parametrize("dtype,solver", [(torch.float32, "cg"), (torch.bfloat16, "fixed_point")])
+def test_backward_precomputed_bias_matches_per_element(dtype, solver):
+    """With the workspace extension (dfl_sinkhorn_bias_workspace_size) the backward
+    evaluates the position / geometry bias once and reads it in its sweeps; without it
+    every sweep evaluates bins and distances.  Both read the same values, so the
+    gradients of Q, K, V, G and the marginals are bit-identical (ragged lengths, masked
+    tokens, bins outside the table); d pos_weight, d w_dist and d x_res reduce through
+    LDS atomics whose order varies from run to run, so they agree to fp32 rounding."""
+    import importlib
+
+    from deepfold_amd import _lib
+
+    fsa = importlib.import_module("deepfold_amd.flash_sinkhorn_attn")  # the module, not the function
+
+    B, H, N, d = 2, 3, 200, 32
+    inp = make_inputs(B, H, N, d, seed=91, eps=[0.5, 1.0, 2.0], pos_geo=True)
+    g = torch.Generator().manual_seed(92)
+    bins = inp["pos_bins"].clone()
+    bins[torch.rand(bins.shape, generator=g) < 0.1] = 77
+    inp["pos_bins"] = bins
+    mask = torch.ones(B, N)
+    mask[0, 150:] = 0
+    mask[1, 17] = 0
+    go, gxc = grad_inputs(B, H, N, d, seed=93, with_xc=True)
+    go = go * mask[:, :, None]
+    kw = dict(ift_solver=solver, ift_iters=12 if solver == "cg" else None)
+    got = {}
+    saved = fsa._BIAS_WS_MAX
+    try:
+        for label, cap in (("matrix", saved), ("per_element", -1)):
+            fsa._BIAS_WS_MAX = cap
+            _lib._ws_cache.clear()  # the next workspace is exactly the requested size
+            got[label] = run_gpu_bwd(inp, 6, dtype, go, gxc, mask=mask, **kw)
+    finally:
+        fsa._BIAS_WS_MAX = saved
+        _lib._ws_cache.clear()
+    for k in got["matrix"]:
+        if k in ("pos_weight", "w_dist", "x_res"):
+            assert max_rel_err(got["matrix"][k], got["per_element"][k]) <= 1e-6, k
+        else:
+            assert np.array_equal(got["matrix"][k], got["per_element"][k]), k
+    assert all(np.isfinite(v).all() for v in got["matrix"].values())
