@@ -36,6 +36,7 @@
 #include "sinkhorn_engine.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace dfl {
 
@@ -255,6 +256,101 @@ __device__ __forceinline__ void lean_wsum(const T* res_lds, const T* str_lds, co
       lean_wsum_chunk<T, DP, 1, GENERAL, TRANS>(res_lds, str_lds, w2, zv, n_str_tiles, rt0 + c0, c0 * 16, sc, cres,
                                                 bias, out, scratch);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Register storage of the CG matrix.  During the CG solve W_ij = exp2(sc q_i.k_j +
+// alpha_i + beta_j (+ bias_ij)) does not change, so each wave computes its tiles once,
+// in lean_wsum's work split (resident tile r < nr of the stripe against streamed tile
+// wave + BWD_NW k, k < KS; tiles it lacks hold 0), for both orientations, and every
+// matvec is one fma per element.  KS = bwd_reg_ks(n_tiles) (2, 4 or 6) and nr <=
+// bwd_reg_nrm(KS), the limits of the forward's register mode.
+__host__ __device__ constexpr int bwd_reg_ks(int n_tiles) {
+  return (n_tiles + 7) / 8 <= 2 ? 2 : ((n_tiles + 7) / 8 <= 4 ? 4 : ((n_tiles + 7) / 8 <= 6 ? 6 : 0));
+}
+__host__ __device__ constexpr int bwd_reg_nrm(int ks) { return ks == 6 ? 3 : 4; }
+constexpr int BWD_REG_SLOTS = 18;  // max over KS of bwd_reg_nrm(KS) * KS
+
+// W tiles of one orientation: resident rows of res_lds (cres: their constant), streamed
+// rows of str_lds (w2: their constant), the expression of lean_wsum_chunk / bias_wsum.
+template <typename T, int DP, int KS, bool GENERAL, bool TRANS>
+__device__ __forceinline__ void reg_wtiles(f32x4 (&W)[BWD_REG_SLOTS], const T* __restrict__ res_lds,
+                                           const T* __restrict__ str_lds, const float* __restrict__ w2,
+                                           int n_str_tiles, int rt0, int nr, float sc,
+                                           const float* __restrict__ cres, const Bias& bias) {
+  using M = Mfma<T, DP>;
+  constexpr int NRM = bwd_reg_nrm(KS);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int g = lane >> 4;
+  const float isc = 1.f / sc;
+#pragma unroll
+  for (int r = 0; r < NRM; ++r) {
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int sl = r * KS + k, st = wave + BWD_NW * k;
+      W[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (r < nr && st < n_str_tiles) {
+        typename M::Frag af, bf;
+        M::load(bf, res_lds + (size_t)((rt0 + r) * 16 + (lane & 15)) * DP, lane);
+        M::load(af, str_lds + (size_t)(st * 16 + (lane & 15)) * DP, lane);
+        const float c = cres[r * 16 + (lane & 15)] * isc;
+        const f32x4 x = M::qk(af, bf, f32x4{c, c, c, c});
+        const f32x4 w = *reinterpret_cast<const f32x4*>(w2 + st * 16 + 4 * g);
+        f32x4 bv[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+        if (GENERAL) {
+          const int s0[1] = {st * 16 + 4 * g};
+          bias.template quads<TRANS, 1>((rt0 + r) * 16 + (lane & 15), s0, bv);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float xv = __builtin_fmaf(x[e], sc, w[e]);
+          if (GENERAL) xv += bv[0][e];
+          W[sl][e] = fast_exp2(xv);
+        }
+      }
+    }
+  }
+}
+
+// out[q] = sum_j W[q][j] z_j for the nr resident tiles: lean_wsum_chunk's order (four
+// accumulators per resident tile over the slots in order, (s0 + s1) + (s2 + s3), the
+// lane groups, then the waves in order).  Called by the whole block.
+template <int KS>
+__device__ __forceinline__ void reg_wsum(const f32x4 (&W)[BWD_REG_SLOTS], int n_str_tiles, int nr,
+                                         const float* __restrict__ zv, float* out, float* scratch) {
+  constexpr int NRM = bwd_reg_nrm(KS);
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int g = lane >> 4;
+  f32x4 z[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    const int st = wave + BWD_NW * k;
+    z[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (st < n_str_tiles) z[k] = *reinterpret_cast<const f32x4*>(zv + st * 16 + 4 * g);
+  }
+#pragma unroll
+  for (int r = 0; r < NRM; ++r) {
+    if (r < nr) {
+      float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] = __builtin_fmaf(W[r * KS + k][e], z[k][e], s[e]);
+      const float ss = sum_groups((s[0] + s[1]) + (s[2] + s[3]));
+      if (lane < 16) scratch[(wave * nr + r) * 16 + lane] = ss;
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < nr * 16) {
+    const int q = threadIdx.x, r = q >> 4, l = q & 15;
+    float ss = 0.f;
+#pragma unroll
+    for (int w_ = 0; w_ < BWD_NW; ++w_) ss += scratch[(w_ * nr + r) * 16 + l];
+    out[q] = ss;
+  }
+  __syncthreads();
 }
 
 // Deterministic block-wide sum of f(i) over i in [0, n) (same order in every block).
@@ -955,15 +1051,17 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     const bool early_exit = a.cg_rtol > 0.f;
     const float stop2 = a.cg_rtol * a.cg_rtol * rr;
     const float k2 = kappa * kappa;
+    // mv(true): lout = W p (my rows); mv(false): lout = W^T t (my columns)
+    auto cg_run = [&](auto&& mv) __attribute__((always_inline)) -> bool {
     for (int it = 0; it < a.iters; ++it) {
       if (early_exit && (rr <= stop2 || rr == 0.f)) break;
       // t_i = sum_j W_ij p_j (my rows)
-      wsum(true, be, cp, al + r_lo);
+      mv(true);
       ++phase;
       for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, lout[i - r_lo], salt | phase, local);
-      if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) return;
+      if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) return false;
       // s_j = sum_i W_ij t_i (my cols)
-      wsum(false, al, ct, be + r_lo);
+      mv(false);
       ++phase;
       for (int j = r_lo + (int)threadIdx.x; j < r_hi; j += BWD_NT) xch_put(xB + j, lout[j - r_lo], salt | phase, local);
       // CG update, identical in every member (utils/cg.py:70-92 with x0 = 0); p^T A p
@@ -971,7 +1069,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       float pAp;
       if (!gather_vector_dot(xB, n, Np, salt | phase, cs, valid, a.err, &sh.flag,
                              [&](int i) { return cp[i] * (cp[i] - k2 * cs[i]); }, sh.red, flip, &pAp))
-        return;
+        return false;
       if (early_exit && pAp == 0.f) break;
       const float alpha = (pAp != 0.f && rr != 0.f) ? rr / pAp : 0.f;
       // the update and ||r_new||^2 in one pass: each thread squares the entries it wrote
@@ -998,6 +1096,40 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
         }
       }
     }
+    return true;
+    };
+    bool cg_ok = false, reg_done = false;
+    if constexpr (!STREAM) {
+      const int ksg = bwd_reg_ks(n_tiles);
+      if (ksg > 0 && nr <= bwd_reg_nrm(ksg)) {
+        // register storage of W for the whole solve
+        auto reg_cg = [&](auto ksc) __attribute__((always_inline)) -> bool {
+          constexpr int KSL = decltype(ksc)::value;
+          f32x4 WR[BWD_REG_SLOTS], WC[BWD_REG_SLOTS];
+          if (general) {
+            reg_wtiles<T, DP, KSL, true, false>(WR, QS, KS, be, n_tiles, t0, nr, sc, al + r_lo, bias);
+            reg_wtiles<T, DP, KSL, true, true>(WC, KS, QS, al, n_tiles, t0, nr, sc, be + r_lo, bias);
+          } else {
+            reg_wtiles<T, DP, KSL, false, false>(WR, QS, KS, be, n_tiles, t0, nr, sc, al + r_lo, bias);
+            reg_wtiles<T, DP, KSL, false, true>(WC, KS, QS, al, n_tiles, t0, nr, sc, be + r_lo, bias);
+          }
+          return cg_run([&](bool row) __attribute__((always_inline)) {
+            if (row) reg_wsum<KSL>(WR, n_tiles, nr, cp, lout, scratch);
+            else reg_wsum<KSL>(WC, n_tiles, nr, ct, lout, scratch);
+          });
+        };
+        if (ksg == 2) cg_ok = reg_cg(std::integral_constant<int, 2>{});
+        else if (ksg == 4) cg_ok = reg_cg(std::integral_constant<int, 4>{});
+        else cg_ok = reg_cg(std::integral_constant<int, 6>{});
+        reg_done = true;
+      }
+    }
+    if (!reg_done)
+      cg_ok = cg_run([&](bool row) __attribute__((always_inline)) {
+        if (row) wsum(true, be, cp, al + r_lo);
+        else wsum(false, al, ct, be + r_lo);
+      });
+    if (!cg_ok) return;
     // z_v = D_c^{1/2} y, z_u = kappa D_r^{1/2} (W y)
     for (int i = threadIdx.x; i < Np; i += BWD_NT) {
       const bool ok = i < n && valid[i];
