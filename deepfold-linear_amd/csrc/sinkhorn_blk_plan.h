@@ -20,8 +20,9 @@ constexpr int BLK_WC = 8;     // column tiles of a wave's sub-block (a wave alwa
 constexpr int BLK_MAXRC = 8;  // rows / columns of a member grid, at most
 constexpr int BLK_MAXS = 32;  // groups per XCD, at most
 constexpr int BLK_MAXL = 64;  // workgroups per XCD, at most
-// Exchange vectors of Np words per (b,h): C row partials, R column partials, final v.
-constexpr int BLK_XCH_VECS = 2 * BLK_MAXRC + 1;
+// Exchange vectors of Np words per (b,h): C row partials and R column partials, each in
+// two slots used by alternate iterations, then the final v.
+constexpr int BLK_XCH_VECS = 4 * BLK_MAXRC + 1;
 
 __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 

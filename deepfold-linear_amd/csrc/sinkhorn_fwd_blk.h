@@ -416,9 +416,13 @@ __global__ void __launch_bounds__(BLK_NT) sinkhorn_fwd_blk_kernel(SinkFwdArgs a)
 
   // ---- exchange words of this (b,h)
   uint64_t* xbase = a.xch + bh * (size_t)BLK_XCH_VECS * Np;
-  uint64_t* xrow = xbase;                         // [C][Np] row partials
-  uint64_t* xcol = xbase + (size_t)BLK_MAXRC * Np;  // [R][Np] column partials
-  uint64_t* xfin = xbase + (size_t)2 * BLK_MAXRC * Np;  // final v
+  // Row partials [2][C][Np] and column partials [2][R][Np], slot it & 1: a member can
+  // write iteration it + 2's partials only after every member of its row (column) band
+  // has published iteration it + 1's, which each does after reading iteration it's, so
+  // no word is overwritten before all its readers have it.
+  uint64_t* xrow = xbase;
+  uint64_t* xcol = xbase + (size_t)2 * BLK_MAXRC * Np;
+  uint64_t* xfin = xbase + (size_t)4 * BLK_MAXRC * Np;  // final v
   uint64_t* xpl = a.xch + (size_t)BH * BLK_XCH_VECS * Np + bh * BLK_MAXL;
   const uint32_t salt = a.salt << 12;
   uint32_t phase = 0;
@@ -470,9 +474,10 @@ __global__ void __launch_bounds__(BLK_NT) sinkhorn_fwd_blk_kernel(SinkFwdArgs a)
       float lse = 0.f;
       if (ok) {
         const float part = sig[q] + fast_log2(blk_row_reduce<false>(part_r, q, TR, sc));
-        xch_put(xrow + (size_t)c * Np + i, part, tag, local);
+        uint64_t* xr = xrow + (size_t)(it & 1) * BLK_MAXRC * Np;
+        xch_put(xr + (size_t)c * Np + i, part, tag, local);
         float val[BLK_MAXRC];
-        if (!blk_poll<BLK_MAXRC>(xrow + i, Np, C, tag, a.err, val)) s_flag = 1;
+        if (!blk_poll<BLK_MAXRC>(xr + i, Np, C, tag, a.err, val)) s_flag = 1;
         lse = blk_combine<BLK_MAXRC>(val, C);
         const float u = kappa * (lmu[q] - lse * LN2);
         const float un = u * LOG2E;
@@ -534,9 +539,10 @@ __global__ void __launch_bounds__(BLK_NT) sinkhorn_fwd_blk_kernel(SinkFwdArgs a)
         const bool ok = j < n && valid[j];
         float lse = 0.f;
         if (ok) {
-          xch_put(xcol + (size_t)r * Np + j, tau[q] + fast_log2(s), tag, local);
+          uint64_t* xc = xcol + (size_t)(it & 1) * BLK_MAXRC * Np;
+          xch_put(xc + (size_t)r * Np + j, tau[q] + fast_log2(s), tag, local);
           float val[BLK_MAXRC];
-          if (!blk_poll<BLK_MAXRC>(xcol + j, Np, R, tag, a.err, val)) s_flag = 1;
+          if (!blk_poll<BLK_MAXRC>(xc + j, Np, R, tag, a.err, val)) s_flag = 1;
           lse = blk_combine<BLK_MAXRC>(val, R);
           const float v = kappa * (lnu[q] - lse * LN2);
           const float vn = v * LOG2E;

@@ -168,7 +168,7 @@ size_t dfl_sinkhorn_bias_workspace_size(int B, int H, int N);
  * params, outputs and kernels as dfl_sinkhorn_fwd, resident storage only (AUTO or
  * RESIDENT or REGISTER; a problem that needs stream storage is rejected).  Instead
  * of a workspace it uses a static device array of DFL_NOALLOC_SCRATCH_BYTES per GPU,
- * held until the process ends: it needs 256 + 8*B*H*(17*Np + 64) bytes (+ 2*B*Np*Np
+ * held until the process ends: it needs 256 + 8*B*H*(33*Np + 64) bytes (+ 2*B*Np*Np
  * with pos_bins), Np = N rounded up to 32, and rejects larger problems.  Every call on
  * one GPU shares that array, so calls that overlap in time on one GPU race.  It
  * calls no hipMalloc / hipFree and no allocating library routine.  Every call first
