@@ -315,10 +315,20 @@ __device__ __forceinline__ void reg_wtiles(f32x4 (&W)[BWD_REG_SLOTS], const T* _
 
 // out[q] = sum_j W[q][j] z_j for the nr resident tiles: lean_wsum_chunk's order (four
 // accumulators per resident tile over the slots in order, (s0 + s1) + (s2 + s3), the
-// lane groups, then the waves in order).  Called by the whole block.
+// lane groups, then the waves in order).  Called by the whole block.  The vectors are
+// given as float offsets into the kernel's dynamic LDS (so every access is a ds_
+// instruction with a 32-bit address) and the counts are made wave-uniform: in the
+// register-bound backward kernel, pointers and counts kept in VGPRs were spilled to
+// scratch and reloaded before every matvec.
 template <int KS>
-__device__ __forceinline__ void reg_wsum(const f32x4 (&W)[BWD_REG_SLOTS], int n_str_tiles, int nr,
-                                         const float* __restrict__ zv, float* out, float* scratch) {
+__device__ __forceinline__ void reg_wsum(const f32x4 (&W)[BWD_REG_SLOTS], int n_str_tiles_in, int nr_in, int zv_off,
+                                         int out_off, int scratch_off) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const float* zv = reinterpret_cast<const float*>(smem) + __builtin_amdgcn_readfirstlane(zv_off);
+  float* out = reinterpret_cast<float*>(smem) + __builtin_amdgcn_readfirstlane(out_off);
+  float* scratch = reinterpret_cast<float*>(smem) + __builtin_amdgcn_readfirstlane(scratch_off);
+  const int n_str_tiles = __builtin_amdgcn_readfirstlane(n_str_tiles_in);
+  const int nr = __builtin_amdgcn_readfirstlane(nr_in);
   constexpr int NRM = bwd_reg_nrm(KS);
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -700,10 +710,14 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
   float* dxs = lout + loc;       // dx accumulator for my stripe [loc][3]
   float* dpw = dxs + 3 * loc;    // d pos_weight histogram [68]
   float* scratch = dpw + 68;     // BWD_SCRATCH (resident) or BWD_STREAM_SCRATCH (stream) floats
-  const int n = mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &sh.tmp);
+  // block-uniform counts, made scalar: held in VGPRs they were among the values this
+  // register-bound kernel spills to scratch and reloads in its loops
+  const int n = __builtin_amdgcn_readfirstlane(mask_setup(a.mask ? a.mask + (size_t)b * N : nullptr, N, valid, &sh.tmp));
   const int n_tiles = (n + 15) / 16;
   int t0, t1;
   stripe(n_tiles, member, a.G, t0, t1);
+  t0 = __builtin_amdgcn_readfirstlane(t0);
+  t1 = __builtin_amdgcn_readfirstlane(t1);
   const int nr = t1 - t0;
   // Every output position is written: rows past the last valid tile (owned by no
   // stripe) are zeroed here, row i by member i % G; invalid stripe rows get zeros
@@ -1113,9 +1127,13 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
             reg_wtiles<T, DP, KSL, false, false>(WR, QS, KS, be, n_tiles, t0, nr, sc, al + r_lo, bias);
             reg_wtiles<T, DP, KSL, false, true>(WC, KS, QS, al, n_tiles, t0, nr, sc, be + r_lo, bias);
           }
+          // float offsets of the vectors in the dynamic LDS (reg_wsum)
+          const float* lds0 = reinterpret_cast<const float*>(smem);
+          const int o_cp = (int)(cp - lds0), o_ct = (int)(ct - lds0), o_out = (int)(lout - lds0),
+                    o_scr = (int)(scratch - lds0);
           return cg_run([&](bool row) __attribute__((always_inline)) {
-            if (row) reg_wsum<KSL>(WR, n_tiles, nr, cp, lout, scratch);
-            else reg_wsum<KSL>(WC, n_tiles, nr, ct, lout, scratch);
+            if (row) reg_wsum<KSL>(WR, n_tiles, nr, o_cp, o_out, o_scr);
+            else reg_wsum<KSL>(WC, n_tiles, nr, o_ct, o_out, o_scr);
           });
         };
         if (ksg == 2) cg_ok = reg_cg(std::integral_constant<int, 2>{});
