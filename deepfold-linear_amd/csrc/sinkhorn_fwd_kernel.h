@@ -155,26 +155,35 @@ __device__ __forceinline__ void fwd_write_tile(const SinkFwdArgs& a, int b, int 
 // vecU (these rows) and vecV (all columns), log2 units.  K is read from KS (all
 // rows); V^T is staged over QS; Q fragments come from global memory.  Called by
 // the whole block.
+// part / part_floats: free LDS for partial sums.  Where it holds them, the P =
+// min(8 / nr, ...) waves of a tile take every P-th pair of streamed tiles each
+// (nr < 8 leaves waves idle otherwise); the tile's first wave adds the others'
+// partials in wave order and writes the tile.
 template <typename T, int DP>
 __device__ __forceinline__ void fwd_resident_output(const SinkFwdArgs& a, int b, int h, int n, int n_tiles, int Np,
                                                     int t0, int nr, const unsigned char* valid, T* QS, const T* KS,
                                                     const float* vecU, const float* vecV, const float* xs,
                                                     const float* lse2, const float* mx2, float sc, const Bias& bias,
                                                     bool general, bool bal, bool has_v, const T* Qg, const T* Vg,
-                                                    const T* Gg) {
+                                                    const T* Gg, float* part = nullptr, int part_floats = 0) {
   using M = Mfma<T, DP>;
   const int N = a.N, d = a.d;
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int g = lane >> 4;
   constexpr int NC = DP / 16;
+  constexpr int PF = 4 * NC + 3;  // floats of one lane's partial: O accumulators, x_c sums
   // V^T replaces Q in LDS; resident Q fragments are read from global memory.
   T* VT = QS;  // [DP][Np]
   __syncthreads();
   if (has_v) stage_rows_t<T, DP>(VT, Vg, a.sn, n, d, Np);
   __syncthreads();
   const int n_pairs = (n_tiles + 1) / 2;
-  for (int rt = wave; rt < nr; rt += FWD_NW) {
+  int P = nr < FWD_NW ? FWD_NW / nr : 1;
+  if (P > 1) P = min(P, 1 + part_floats / (nr * WAVE * PF));
+  const int slots = P > 1 ? nr * P : nr;
+  for (int wi = wave; wi < slots; wi += FWD_NW) {
+    const int rt = wi % nr, pi = wi / nr;
     const int tile = t0 + rt;
     const int qloc = rt * 16;
     const int irow = tile * 16 + (lane & 15);  // this lane's row in the P layout
@@ -185,7 +194,7 @@ __device__ __forceinline__ void fwd_resident_output(const SinkFwdArgs& a, int b,
 #pragma unroll
     for (int c = 0; c < NC; ++c) oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
     float xc0 = 0.f, xc1 = 0.f, xc2 = 0.f;
-    for (int sp = 0; sp < n_pairs; ++sp) {
+    for (int sp = pi; sp < n_pairs; sp += P) {
       f32x4 p[2];
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -216,9 +225,39 @@ __device__ __forceinline__ void fwd_resident_output(const SinkFwdArgs& a, int b,
           oacc[c] = M::pv_split(p[0], p[1], VT + (size_t)(c * 16 + (lane & 15)) * Np + sp * 32, lane, oacc[c]);
       }
     }
-    fwd_write_tile<T, DP>(a, b, h, tile, n, valid, lse2 + qloc, mx2 + qloc, vecU, vecV, oacc, xc0, xc1, xc2, Gg,
-                          lane, bal);
+    if (P == 1) {
+      fwd_write_tile<T, DP>(a, b, h, tile, n, valid, lse2 + qloc, mx2 + qloc, vecU, vecV, oacc, xc0, xc1, xc2, Gg,
+                            lane, bal);
+      continue;
+    }
+    // slots <= FWD_NW: every wave holds at most one (tile, part)
+    float* my = part + ((size_t)(pi > 0 ? pi - 1 : 0) * nr + rt) * WAVE * PF + lane;
+    if (pi > 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) my[(4 * c + r) * WAVE] = oacc[c][r];
+      my[(4 * NC) * WAVE] = xc0;
+      my[(4 * NC + 1) * WAVE] = xc1;
+      my[(4 * NC + 2) * WAVE] = xc2;
+    }
+    __syncthreads();
+    if (pi == 0) {
+      for (int q = 1; q < P; ++q) {
+        const float* src = part + ((size_t)(q - 1) * nr + rt) * WAVE * PF + lane;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) oacc[c][r] += src[(4 * c + r) * WAVE];
+        xc0 += src[(4 * NC) * WAVE];
+        xc1 += src[(4 * NC + 1) * WAVE];
+        xc2 += src[(4 * NC + 2) * WAVE];
+      }
+      fwd_write_tile<T, DP>(a, b, h, tile, n, valid, lse2 + qloc, mx2 + qloc, vecU, vecV, oacc, xc0, xc1, xc2, Gg,
+                            lane, bal);
+    }
   }
+  if (P > 1 && wave >= slots) __syncthreads();  // the idle waves' share of the merge barrier
 }
 
 // MODE (compile time, so the plain UOT instantiation carries none of the other
@@ -686,8 +725,10 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   const int g = lane >> 4;
   constexpr int NC = DP / 16;
   if constexpr (!STREAM) {
+    // register storage: the sweep scratch and the split-potential arrays are free now
+    const int free_floats = REG ? sweep_scratch<FWD_NT>() + (2 * cpn + 2 * loc) * 2 : 0;
     fwd_resident_output<T, DP>(a, b, h, n, n_tiles, Np, t0, nr, valid, QS, KS, vecU, vecV, xs, lse2, mx2, sc, bias,
-                               general, bal, has_v, Qg, Vg, Gg);
+                               general, bal, has_v, Qg, Vg, Gg, scratch, free_floats);
   } else {
     // Stream mode: K and V^T pass through LDS in chunks of FWD_OCH streamed rows
     // (the K stripe region is free now); resident Q fragments come from the Q stripe.
