@@ -647,6 +647,30 @@ __device__ __forceinline__ bf16x4 blk_row_operand(const bf16x4* parts, int tile,
   return g == 1 ? p : (g == 0 ? one : zero);
 }
 
+// acc += P V for one 16x16 pair held in the accumulator layout of S (lane: plan row
+// l % 16, plan columns 4(l/16) + e of the streamed tile), giving the output layout
+// (lane: rows 4(l/16) + e, V column l % 16).  vt: V^T row (c0 + l%16) at column
+// st*16 + 4(l/16).  bf16: P as a hi + lo pair of bf16 A operands (two
+// 16x16x16 MFMAs on the same V operand); fp32: four 16x16x4 steps.
+template <typename T> __device__ __forceinline__ f32x4 reg_pv(const float (&p)[4], const T* vt, f32x4 acc);
+template <> __device__ __forceinline__ f32x4 reg_pv<bf16>(const float (&p)[4], const bf16* vt, f32x4 acc) {
+  bf16x4 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = (bf16)p[e];
+    lo[e] = (bf16)(p[e] - (float)hi[e]);
+  }
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(vt);
+  acc = mfma_rank(hi, v, acc);
+  return mfma_rank(lo, v, acc);
+}
+template <> __device__ __forceinline__ f32x4 reg_pv<float>(const float (&p)[4], const float* vt, f32x4 acc) {
+  const f32x4 v = *reinterpret_cast<const f32x4*>(vt);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p[e], v[e], acc, 0, 0, 0);
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // Dataflow half-iterations of resident storage.  A wave of a lean sweep reads the
 // potentials of its own streamed tiles st = wave + NW k only, so it needs no other
@@ -881,9 +905,12 @@ __device__ __forceinline__ void flow_sweep(bool online, const T* res, const T* s
 //   colp : split parts of the streamed potentials (by absolute streamed index)
 //   rowp : split parts of -shift of the resident rows (local), for the fixed mode
 //   shift: the fixed shifts (local rows)
+// pmax (online only): the wave's row maxima, pmax[(r 16 + l) NW + wave], NEG_BIG
+// where the wave has no live entry.
 template <int KS, int NRM, int NW>
 __device__ __forceinline__ void reg_sweep(bool online, const f32x4 (&S)[NRM * KS], int nr, const bf16x4* colp,
-                                          const bf16x4* rowp, const float* shift, float* part) {
+                                          const bf16x4* rowp, const float* shift, float* part,
+                                          float* pmax = nullptr) {
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int g = lane >> 4;
@@ -906,6 +933,7 @@ __device__ __forceinline__ void reg_sweep(bool online, const f32x4 (&S)[NRM * KS
           m = fmaxf(m, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
         }
         m = max_groups(m);
+        if (pmax && lane < 16) pmax[(r * 16 + lane) * NW + wave] = m;
         sh = m > 0.5f * NEG_BIG ? m : 0.f;  // no live entry: the sum is 0 whatever the shift
         Bv = g == 1 ? split3(-sh) : b0;
       } else {

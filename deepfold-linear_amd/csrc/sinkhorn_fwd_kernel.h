@@ -586,6 +586,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
   // into calls with a stack frame.
   if constexpr (REG) {
     // ---- register storage: the logits of every wave's pairs stay in VGPRs
+    bool reg_tail = false;  // the register tail wrote the outputs
     auto reg_loop = [&](auto ksc) __attribute__((always_inline)) -> bool {
       constexpr int KSL = decltype(ksc)::value;
       constexpr int NRM = reg_nrm(KSL);
@@ -677,6 +678,112 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
           if (s_flagp[phase & 1]) return false;
         }
       }
+      // ---- Tail from the register logits (where the merge of the output partials
+      // fits the Q and K region, dead after the prologue): the final row sweep (exact
+      // log Z and row maxima) and the output pass, with no QK^T or bias recompute.
+      // (head dim 32: at 64 the output accumulators no longer fit beside the logits)
+      if constexpr (DP == 32) {
+      constexpr int NC = DP / 16;
+      constexpr int PF = 4 * NC + 3;  // floats of one lane's output partial
+      if ((size_t)FWD_NW * nr * PF * WAVE * sizeof(float) > (size_t)2 * rcap * DP * sizeof(T)) return true;
+      T* VT = QS;  // [DP][Np]; its loads overlap the final sweep
+      stage_rows_t<T, DP>(VT, Vg, a.sn, n, d, Np);
+      {
+        const int fp = (phase + 1) & 1;  // the flag parity of this extra half-iteration
+        float dm;
+        if (!wave_gather<FWD_NW>(xv, n, n_tiles, salt | phase, vecV, valid, a.err, dm, cpV)) s_flagp[fp] = 1;
+        float* part = scratch + (chunk & 1) * (FWD_NW * SK_RT * 16);
+        ++chunk;
+        float* pmax = reinterpret_cast<float*>(cpU);  // u's parts are dead after the last column sweep
+        reg_sweep<KSL, NRM, FWD_NW>(true, SR, nr, cpV, rpR, lse_r, part, pmax);
+        lds_barrier();
+        if (s_flagp[fp]) return false;
+        if (qc < nr * 16) {
+          float mm = NEG_BIG;
+#pragma unroll
+          for (int w_ = 0; w_ < FWD_NW; ++w_) mm = fmaxf(mm, pmax[qc * FWD_NW + w_]);
+          mx2[qc] = mm;
+        }
+        flow_combine<FWD_NW>(part, nr, lse_r, [&](int q, float l2) { rpR[q] = split3(ok_c ? -l2 : 0.f); });
+        __syncthreads();
+      }
+      // P_ij = exp2(S_ij + v_j - lse_i); each wave sums its streamed tiles, the
+      // partials meet in LDS and the wave r writes resident tile r
+      {
+        bf16x4 A[KSL];
+#pragma unroll
+        for (int k = 0; k < KSL; ++k) A[k] = blk_col_operand(cpV, wave + FWD_NW * k, lane);
+        f32x4 oacc[NRM][NC];
+        float xc[NRM][3];
+#pragma unroll
+        for (int r = 0; r < NRM; ++r) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) oacc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+          xc[r][0] = xc[r][1] = xc[r][2] = 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < NRM; ++r) {
+          if (r < nr) {
+            const bf16x4 Bv = blk_row_operand(rpR, r, lane);
+#pragma unroll
+            for (int k = 0; k < KSL; ++k) {
+              const int st = wave + FWD_NW * k;
+              if (st < n_tiles) {
+                const f32x4 x = mfma_rank(A[k], Bv, SR[r * KSL + k]);
+                float pe[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pe[e] = fast_exp2(x[e]);
+                const f32x4* xj = reinterpret_cast<const f32x4*>(xs + 3 * (st * 16 + 4 * g));
+                const f32x4 x0 = xj[0], x1 = xj[1], x2 = xj[2];
+                const float xv[12] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3],
+                                      x2[0], x2[1], x2[2], x2[3]};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                  for (int c = 0; c < 3; ++c) xc[r][c] = __builtin_fmaf(pe[e], xv[3 * e + c], xc[r][c]);
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                  oacc[r][c] = reg_pv<T>(pe, VT + (size_t)(c * 16 + (lane & 15)) * Np + st * 16 + 4 * g, oacc[r][c]);
+              }
+            }
+          }
+        }
+        __syncthreads();  // V^T and the split parts are read
+        float* mg = reinterpret_cast<float*>(QS);
+#pragma unroll
+        for (int r = 0; r < NRM; ++r) {
+          if (r < nr) {
+            float* dst = mg + (size_t)(wave * nr + r) * PF * WAVE + lane;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) dst[(4 * c + e) * WAVE] = oacc[r][c][e];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) dst[(4 * NC + c) * WAVE] = xc[r][c];
+          }
+        }
+        __syncthreads();
+        if (wave < nr) {
+          const int r = wave;
+          f32x4 o[NC];
+          float x3[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int w_ = 0; w_ < FWD_NW; ++w_) {
+            const float* src = mg + (size_t)(w_ * nr + r) * PF * WAVE + lane;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[c][e] += src[(4 * c + e) * WAVE];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) x3[c] += src[(4 * NC + c) * WAVE];
+          }
+          fwd_write_tile<T, DP>(a, b, h, t0 + r, n, valid, lse_r + r * 16, mx2 + r * 16, vecU, vecV, o, x3[0], x3[1],
+                                x3[2], Gg, lane, false);
+        }
+      }
+      reg_tail = true;
+      }
       return true;
     };
     const int ksg = reg_ks(n_tiles);
@@ -688,7 +795,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
       if (threadIdx.x == 0) raise_error(a.err, a.salt, 3u);
       ok = false;
     }
-    if (!ok) return;
+    if (!ok || reg_tail) return;
   } else {
     for (int it = 0; it < a.K_iter; ++it) {
       if constexpr (BAL) {
