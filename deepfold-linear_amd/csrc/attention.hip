@@ -20,10 +20,18 @@
 
 namespace dfl {
 
-// dK / dV from query-split partials; d pos_weight from per-workgroup partials (fixed order).
+// dK / dV from query-split partials; d pos_weight from per-workgroup partials; the
+// window-bias gradient from per-batch-row slabs (all sums in a fixed order).
 template <typename T, int DP>
 __global__ void __launch_bounds__(256) attn_bwd_finalize_kernel(AttnArgs a, int n_qblocks) {
   const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t nslab = (size_t)((a.Mq + ATTN_WQ - 1) / ATTN_WQ) * a.H * ATTN_WQ * ATTN_WK;
+  if (a.dbias_rows && e < nslab) {
+    const T* rows = reinterpret_cast<const T*>(a.dbias_rows);
+    float s = 0.f;
+    for (int b = 0; b < a.B; ++b) s += to_f32(rows[(size_t)b * nslab + e]);
+    reinterpret_cast<T*>(a.dbias)[e] = from_f32<T>(s);
+  }
   const size_t nkv = (size_t)a.B * a.H * a.Nk * a.d;
   if (a.qsplit > 1 && e < nkv) {
     const size_t row = e / a.d;
@@ -254,8 +262,9 @@ static hipError_t attn_bwd_f(const AttnArgs& a, hipStream_t s) {
   const int nkb = (a.Nk + K::RK - 1) / K::RK;
   hipLaunchKernelGGL(kkv, dim3((unsigned)(nkb * a.qsplit * BH)), dim3(K::NT), lkv, s, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  if (a.qsplit > 1 || (BIAS == ATTN_BIAS_BINS && a.dpos_w)) {
-    const size_t n = std::max((size_t)BH * a.Nk * a.d, (size_t)a.H * 68);
+  if (a.qsplit > 1 || (BIAS == ATTN_BIAS_BINS && a.dpos_w) || a.dbias_rows) {
+    const size_t nslab = a.dbias_rows ? (size_t)((a.Mq + ATTN_WQ - 1) / ATTN_WQ) * a.H * ATTN_WQ * ATTN_WK : 0;
+    const size_t n = std::max(std::max((size_t)BH * a.Nk * a.d, (size_t)a.H * 68), nslab);
     hipLaunchKernelGGL((attn_bwd_finalize_kernel<T, DP>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a,
                        nqb);
     e = hipGetLastError();

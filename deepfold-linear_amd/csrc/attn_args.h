@@ -47,6 +47,7 @@ struct AttnArgs {
   float* dcoef;      // [B*H][Mq]  D_i = sum_c dO_ic O_ic
   float* kv_part;    // [qsplit][B*H][Nk][2][DP] fp32 partial dK / dV (qsplit > 1)
   float* dpw_part;   // [B*H][ceil(Mq/64)][68] fp32 bins-gradient partials of the dQ pass
+  void* dbias_rows;  // window bias, B > 1: [B][ceil(Mq/32)*H*32*128] per-batch-row gradients (type of q)
   int qsplit;        // query-range splits of the dK/dV pass
 };
 

@@ -569,14 +569,18 @@ __global__ void __launch_bounds__((Eng<T, DP, WIN>::NT)) attn_bwd_q2_kernel(Attn
     const int kofs = ATTN_WQ * w - ATTN_WOFF;
     br.row = reinterpret_cast<const typename BR::BT*>(reinterpret_cast<const T*>(a.bias) + off - kofs);
     if (a.dbias) {
-      drow = reinterpret_cast<T*>(a.dbias) + off - kofs;
+      // The window bias has no batch dimension, so with B > 1 every batch row writes
+      // its gradient to a slab set of its own and the finalize sums them in row order.
+      T* dbase = a.dbias_rows
+                     ? reinterpret_cast<T*>(a.dbias_rows) + (size_t)b * ((Mq + ATTN_WQ - 1) / ATTN_WQ) * a.H * ATTN_WQ * ATTN_WK
+                     : reinterpret_cast<T*>(a.dbias);
+      drow = dbase + off - kofs;
       // The main loop writes the window's keys [k_lo, k_hi) of its rows < Mq; the rest of
       // the (32, 128) slab (keys clipped at the sequence ends, rows past Mq) is zeroed
-      // here, so the caller need not clear the gradient.  The window bias has no batch
-      // dimension: the C ABI admits its gradient only for B = 1.
+      // here, so the caller need not clear the gradient.
       // (only windows at the sequence ends have such entries: a uniform test)
       if (k_lo > kofs || k_hi < kofs + ATTN_WK || q0 + ATTN_WQ > Mq) {
-        T* slab = reinterpret_cast<T*>(a.dbias) + ((size_t)w * a.H + h) * ATTN_WQ * ATTN_WK;
+        T* slab = dbase + ((size_t)w * a.H + h) * ATTN_WQ * ATTN_WK;
         for (int e = t; e < ATTN_WQ * ATTN_WK; e += NT) {
           const int key = kofs + (e % ATTN_WK);
           if (q0 + e / ATTN_WK >= Mq || key < k_lo || key >= k_hi) slab[e] = from_f32<T>(0.f);

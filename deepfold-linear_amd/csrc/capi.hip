@@ -360,9 +360,11 @@ int attn_qsplit(int B, int H, int Mq, int Nk) {
   return s;
 }
 
-// Attention backward workspace: do_w, D, dK/dV partials, d pos_weight partials.
+// Attention backward workspace: do_w, D, dK/dV partials, d pos_weight partials and,
+// for square shapes with B > 1 (a window bias is possible), per-batch-row window-bias
+// gradient slabs sized for 4-byte elements.
 struct AttnWs {
-  size_t do_w, dcoef, kv_part, dpw_part, total;
+  size_t do_w, dcoef, kv_part, dpw_part, dbias_rows, total;
 };
 AttnWs attn_ws_layout(int B, int H, int Mq, int Nk) {
   auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -373,7 +375,9 @@ AttnWs attn_ws_layout(int B, int H, int Mq, int Nk) {
   w.dcoef = w.do_w + r256(rows * 64 * 4);
   w.kv_part = w.dcoef + r256(rows * 4);
   w.dpw_part = w.kv_part + (qs > 1 ? r256((size_t)qs * B * H * Nk * 2 * 64 * 4) : 0);
-  w.total = w.dpw_part + r256((size_t)B * H * ((Mq + 31) / 32) * 68 * 4);  // per 32- or 64-query block
+  w.dbias_rows = w.dpw_part + r256((size_t)B * H * ((Mq + 31) / 32) * 68 * 4);  // per 32- or 64-query block
+  const size_t slab = (size_t)((Mq + 31) / 32) * H * 32 * 128;
+  w.total = w.dbias_rows + (B > 1 && Mq == Nk ? r256((size_t)B * slab * 4) : 0);
   return w;
 }
 
@@ -390,10 +394,6 @@ int check_attn(const dfl_attn_params* p, bool bwd) {
   if (p->window && p->Mq != p->Nk) return fail("windowed attention needs Mq == Nk");
   if (p->bias_mode == DFL_ATTN_BIAS_WINDOW && !p->window) return fail("a window bias needs window = 1");
   if (bwd && (!p->grad_o || !p->dq || !p->dk || !p->dv)) return fail("grad_o, dq, dk and dv are required");
-  // the window bias is shared by the batch, so its gradient is a sum over batch rows,
-  // which one launch does not form: call once per batch row and add the slabs
-  if (bwd && p->bias_mode == DFL_ATTN_BIAS_WINDOW && p->dbias && p->B > 1)
-    return fail("the window-bias gradient needs B = 1 per call (the bias is shared by the batch; sum per-row calls)");
   return 0;
 }
 
@@ -906,6 +906,8 @@ int dfl_attn_bwd(const dfl_attn_params* p, void* workspace, size_t workspace_byt
   a.dcoef = reinterpret_cast<float*>(ws + w.dcoef);
   a.kv_part = reinterpret_cast<float*>(ws + w.kv_part);
   a.dpw_part = reinterpret_cast<float*>(ws + w.dpw_part);
+  // the window bias is shared by the batch: with B > 1 its gradient sums per-row slabs
+  a.dbias_rows = (p->bias_mode == DFL_ATTN_BIAS_WINDOW && p->dbias && p->B > 1) ? ws + w.dbias_rows : nullptr;
   a.qsplit = attn_qsplit(p->B, p->H, p->Mq, p->Nk);
   if (a.bias_mode != dfl::ATTN_BIAS_DENSE && a.bias_mode != dfl::ATTN_BIAS_WINDOW) a.dbias = nullptr;
   if (!a.g) a.dg = nullptr;

@@ -102,35 +102,22 @@ class AttnFn(torch.autograd.Function):
         dpw = torch.empty(H, 68, dtype=torch.float32, device=dev) if (bins is not None and need[4]) else None
         ws = _lib.workspace(dev, lib.dfl_attn_workspace_size(B, H, Mq, Nk, d), kind="attn")
 
-        def launch(b0, b1, db):
-            """One dfl_attn_bwd call over batch rows [b0, b1), bias gradient into db."""
-            at = lambda t: None if t is None else t[b0:b1]
-            p = _lib.AttnParams(
-                dtype=_lib.DFL_BF16 if dt == torch.bfloat16 else _lib.DFL_F32,
-                q=qc[b0].data_ptr(), k=kc[b0].data_ptr(), v=vc[b0].data_ptr(), g=_lib.ptr(at(gc)),
-                q_stride_b=qc.stride(0), q_stride_h=qc.stride(1), q_stride_n=qc.stride(2),
-                k_stride_b=kc.stride(0), k_stride_h=kc.stride(1), k_stride_n=kc.stride(2),
-                q_mask=_lib.ptr(at(qm)), k_mask=_lib.ptr(at(km)), bias_mode=bias_mode,
-                pos_weight=_lib.ptr(pw), pos_bins=_lib.ptr(at(bins)), bias=_lib.ptr(bs if window else at(bs)),
-                window=window, B=b1 - b0, H=H, Mq=Mq, Nk=Nk, d=d, scale=1.0 / math.sqrt(d),
-                o=o[b0].data_ptr(), lse=lse[b0].data_ptr(), grad_o=go[b0].data_ptr(), dq=dq[b0].data_ptr(),
-                dk=dk[b0].data_ptr(), dv=dv[b0].data_ptr(), dg=_lib.ptr(at(dg)), dbias=_lib.ptr(db),
-                dpos_weight=_lib.ptr(dpw))
-            rc = _lib.timed_launch("attn_bwd", dev, lambda: lib.dfl_attn_bwd(
-                ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
-                ctypes.c_void_p(_lib.stream_handle(dev))))
-            _lib.check(rc, "dfl_attn_bwd")
-
-        if window and dbias is not None and B > 1:
-            # the window bias is shared by the batch: its gradient is the sum of the
-            # per-row gradients, which the library forms one batch row per call
-            acc = torch.zeros(bs.shape, dtype=torch.float32, device=dev)
-            for b in range(B):
-                launch(b, b + 1, dbias)
-                acc += dbias.float()
-            dbias = acc.to(bs.dtype)
-        else:
-            launch(0, B, dbias)
+        # (a window bias is shared by the batch; the library sums its per-row gradients)
+        p = _lib.AttnParams(
+            dtype=_lib.DFL_BF16 if dt == torch.bfloat16 else _lib.DFL_F32,
+            q=qc.data_ptr(), k=kc.data_ptr(), v=vc.data_ptr(), g=_lib.ptr(gc),
+            q_stride_b=qc.stride(0), q_stride_h=qc.stride(1), q_stride_n=qc.stride(2),
+            k_stride_b=kc.stride(0), k_stride_h=kc.stride(1), k_stride_n=kc.stride(2),
+            q_mask=_lib.ptr(qm), k_mask=_lib.ptr(km), bias_mode=bias_mode,
+            pos_weight=_lib.ptr(pw), pos_bins=_lib.ptr(bins), bias=_lib.ptr(bs),
+            window=window, B=B, H=H, Mq=Mq, Nk=Nk, d=d, scale=1.0 / math.sqrt(d),
+            o=o.data_ptr(), lse=lse.data_ptr(), grad_o=go.data_ptr(), dq=dq.data_ptr(),
+            dk=dk.data_ptr(), dv=dv.data_ptr(), dg=_lib.ptr(dg), dbias=_lib.ptr(dbias),
+            dpos_weight=_lib.ptr(dpw))
+        rc = _lib.timed_launch("attn_bwd", dev, lambda: lib.dfl_attn_bwd(
+            ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+            ctypes.c_void_p(_lib.stream_handle(dev))))
+        _lib.check(rc, "dfl_attn_bwd")
         cast = lambda t, dtp: None if t is None else (t if t.dtype == dtp else t.to(dtp))
         return (cast(dq, qdt) if need[0] else None, cast(dk, kdt) if need[1] else None,
                 cast(dv, vdt) if need[2] else None, cast(dg, gdt) if need[3] else None,

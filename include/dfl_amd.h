@@ -322,9 +322,10 @@ int dfl_sinkhorn_unrolled_bwd(const dfl_sinkhorn_unrolled_bwd_params* p, void* w
  * Backward inputs: grad_o (B,H,Mq,d) contiguous, plus the forward's o and lse;
  * outputs (element type of q, contiguous): dq, dk, dv; dg if g; dbias if a dense
  * or window bias is given (may be NULL; every entry is written, window entries
- * outside the sequence as zero).  The window bias is shared by the batch, so a
- * window-bias gradient is accepted only with B = 1: call once per batch row and
- * sum the slabs.  dpos_weight (H,68) fp32 for BINS (may be NULL).
+ * outside the sequence as zero).  The window bias is shared by the batch, so its
+ * gradient is the sum over batch rows: with B > 1 each row's gradient goes to a
+ * slab set of the workspace and the call sums them in row order (in fp32, rounded
+ * once to the element type).  dpos_weight (H,68) fp32 for BINS (may be NULL).
  */
 enum dfl_attn_bias { DFL_ATTN_BIAS_NONE = 0, DFL_ATTN_BIAS_BINS = 1, DFL_ATTN_BIAS_DENSE = 2, DFL_ATTN_BIAS_WINDOW = 3 };
 
@@ -356,7 +357,9 @@ typedef struct dfl_attn_params {
   float* dpos_weight;
 } dfl_attn_params;
 
-/* Bytes of backward workspace (no zeroing needed); the forward uses none. */
+/* Bytes of backward workspace (no zeroing needed); the forward uses none.  For
+ * Mq == Nk and B > 1 it includes B * ceil(Mq/32) * H * 32 * 128 * 4 bytes for the
+ * per-row window-bias gradients. */
 size_t dfl_attn_workspace_size(int B, int H, int Mq, int Nk, int d);
 int dfl_attn_fwd(const dfl_attn_params* p, void* stream);
 int dfl_attn_bwd(const dfl_attn_params* p, void* workspace, size_t workspace_bytes, void* stream);

@@ -139,21 +139,30 @@ def test_pending_error_is_clear_without_launches(lib_path):
     _lib.raise_pending("test")
 
 
-def test_attn_bwd_refuses_batched_window_bias_gradient(lib_path):
-    """The window bias is shared by the batch; its gradient is a batch sum that one
-    launch does not form, so the entry point refuses B > 1 before any GPU work (the
-    pointers are never dereferenced: argument checks come first)."""
+def test_attn_workspace_holds_batched_window_bias_gradient(lib_path):
+    """The window bias is shared by the batch, so with B > 1 its gradient is a sum of
+    per-row gradients, formed in the workspace: the size grows by B row slab sets of
+    ceil(M/32) * H * 32 * 128 four-byte entries for square shapes with B > 1 (where a
+    window is possible) and by nothing otherwise; a window-bias gradient call with a
+    workspace one byte short is refused before any GPU work (argument checks come
+    first, the pointers are never dereferenced)."""
     from deepfold_amd import _lib
 
     lib = _lib.load(lib_path)
+    H, M, d = 2, 150, 32
+    slab = -(-M // 32) * H * 32 * 128 * 4
+    ws1 = lib.dfl_attn_workspace_size(1, H, M, M, d)
+    ws3 = lib.dfl_attn_workspace_size(3, H, M, M, d)
+    assert ws3 - 3 * ws1 >= 3 * slab - 256 * 4 and ws3 - 3 * ws1 <= 3 * slab + 256 * 4
+    assert lib.dfl_attn_workspace_size(3, H, M, M + 8, d) < lib.dfl_attn_workspace_size(3, H, M, M, d)
     fake = 4096
-    p = _lib.AttnParams(dtype=_lib.DFL_BF16, q=fake, k=fake, v=fake, q_stride_b=64 * 32, q_stride_h=64 * 32,
-                        q_stride_n=32, k_stride_b=64 * 32, k_stride_h=64 * 32, k_stride_n=32,
-                        bias_mode=_lib.DFL_ATTN_BIAS_WINDOW, bias=fake, window=1, B=2, H=1, Mq=64, Nk=64, d=32,
+    p = _lib.AttnParams(dtype=_lib.DFL_BF16, q=fake, k=fake, v=fake, q_stride_b=H * M * d, q_stride_h=M * d,
+                        q_stride_n=d, k_stride_b=H * M * d, k_stride_h=M * d, k_stride_n=d,
+                        bias_mode=_lib.DFL_ATTN_BIAS_WINDOW, bias=fake, window=1, B=3, H=H, Mq=M, Nk=M, d=d,
                         scale=1.0, o=fake, lse=fake, grad_o=fake, dq=fake, dk=fake, dv=fake, dbias=fake)
-    rc = lib.dfl_attn_bwd(ctypes.byref(p), None, 0, None)
+    rc = lib.dfl_attn_bwd(ctypes.byref(p), ctypes.c_void_p(fake), ws3 - 1, None)
     assert rc != 0
-    assert "B = 1" in lib.dfl_last_error().decode()
+    assert "workspace too small" in lib.dfl_last_error().decode()
 
 
 def test_ops_refuse_cpu_tensors():
