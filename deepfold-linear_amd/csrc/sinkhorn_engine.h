@@ -1086,10 +1086,15 @@ __device__ __forceinline__ void stream_sweep(const T* __restrict__ res, const T*
       m[r] = NEG_BIG;
       s[r] = 0.f;
     }
-    Frag af[SCH], an[SCH];
-    f32x4 w[SCH], wn[SCH], z[SCH], zn[SCH];
-    if (ks > 0) load_group(0, af, w, z);
-    for (int k0 = 0; k0 < ks; k0 += SCH) {
+    // Two register sets alternate (the loop is unrolled by two): group k0's fragments
+    // sit in one set while group k0 + SCH's loads fill the other, with no copies
+    // between them (with a copy at the end of every iteration the compiler waited on
+    // the loads just issued before the group's MFMAs).
+    Frag fa[SCH], fb[SCH];
+    f32x4 wa[SCH], wb[SCH], za[SCH], zb[SCH];
+    if (ks > 0) load_group(0, fa, wa, za);
+    auto group = [&](int k0, Frag (&af)[SCH], f32x4 (&w)[SCH], f32x4 (&z)[SCH], Frag (&an)[SCH], f32x4 (&wn)[SCH],
+                     f32x4 (&zn)[SCH]) __attribute__((always_inline)) {
       const bool more = k0 + SCH < ks;
       if (more) load_group(k0 + SCH, an, wn, zn);
       // The resident fragments are loop-invariant; an opaque row offset keeps
@@ -1152,12 +1157,24 @@ __device__ __forceinline__ void stream_sweep(const T* __restrict__ res, const T*
           }
         }
       }
-      if (more) {
+    };
+    if constexpr (KIND != SW_WSUM) {
+      for (int k0 = 0; k0 < ks; k0 += 2 * SCH) {
+        group(k0, fa, wa, za, fb, wb, zb);
+        if (k0 + SCH < ks) group(k0 + SCH, fb, wb, zb, fa, wa, za);
+      }
+    } else {
+      // the weighted sum (inside the backward kernel, at its register limit) keeps one
+      // body: the unrolled pair of sets there pushed arrays to scratch
+      for (int k0 = 0; k0 < ks; k0 += SCH) {
+        group(k0, fa, wa, za, fb, wb, zb);
+        if (k0 + SCH < ks) {
 #pragma unroll
-        for (int k = 0; k < SCH; ++k) {
-          af[k] = an[k];
-          w[k] = wn[k];
-          z[k] = zn[k];
+          for (int k = 0; k < SCH; ++k) {
+            fa[k] = fb[k];
+            wa[k] = wb[k];
+            za[k] = zb[k];
+          }
         }
       }
     }
