@@ -330,6 +330,9 @@ def workspace(device: torch.device, nbytes: int, kind: str = "sinkhorn") -> torc
 # Optional per-launch timing: when a list is installed here, every C-ABI launch
 # appends (name, start_event, end_event) recorded on the launch stream.
 launch_timings: list | None = None
+# With launch_timings on: the launch names to bracket with events (None: every launch).
+# An event pair costs a few microseconds of stream time per launch.
+launch_timed: set | None = None
 
 
 def raise_pending(what: str = "deepfold_amd") -> None:
@@ -349,7 +352,7 @@ def timed_launch(name: str, device: torch.device, fn):
     """Run ``fn()`` (one C-ABI call), bracketing it with events if timing is on.
     Raises first if an earlier launch reported an expired wait."""
     raise_pending(name)
-    if launch_timings is None:
+    if launch_timings is None or (launch_timed is not None and name not in launch_timed):
         return fn()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
