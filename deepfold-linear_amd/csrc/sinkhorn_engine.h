@@ -941,11 +941,18 @@ __device__ __forceinline__ void reg_sweep(bool online, const f32x4 (&S)[NRM * KS
         Bv = blk_row_operand(rowp, r, lane);
       }
       float e[4 * KS];
+      // software pipelined: the MFMA of pair k + 1 issues before the exponentials of
+      // pair k (two accumulators live), so the exponentials rarely wait on an MFMA
+      f32x4 xc = mfma_rank(A[0], Bv, S[r * KS]);
 #pragma unroll
       for (int k = 0; k < KS; ++k) {
-        const f32x4 x = mfma_rank(A[k], Bv, S[r * KS + k]);
+        f32x4 xn;
+        if (k + 1 < KS) xn = mfma_rank(A[k + 1], Bv, S[r * KS + k + 1]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) e[4 * k + q] = fast_exp2(x[q]);
+        for (int q = 0; q < 4; ++q) e[4 * k + q] = fast_exp2(xc[q]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + 1 < KS) xc = xn;
       }
       const float ss = sum_groups(tree_sum(e));
       if (lane < 16) part[(r * 16 + lane) * NW + wave] = ss > 0.f ? sh + fast_log2(ss) : NEG_BIG;
