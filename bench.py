@@ -590,33 +590,36 @@ def bench_attention(args, which):
         step()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    # timed region: the same step captured once in a HIP graph (the attention entry
-    # points allocate nothing inside a call and record no memset), replayed `steps` times
-    cur = torch.cuda.current_stream(dev)
-    side = torch.cuda.Stream(dev)
-    side.wait_stream(cur)
-    with torch.cuda.stream(side):
-        step()
-    cur.wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
+    if args.eager:  # profiling runs: the eager calls are the timed region
+        ms = eager_ms
+    else:
+        # timed region: the same step captured once in a HIP graph (the attention entry
+        # points allocate nothing inside a call and record no memset), replayed `steps` times
+        cur = torch.cuda.current_stream(dev)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            step()
+        cur.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
         graph.replay()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
     _lib.raise_pending("attention bench")
-    ms = wall * 1e3 / args.steps
-    dev_ms = ms  # the roofline over the replayed step: its kernels and the gaps between them
+    dev_ms = ms  # the roofline over the timed step: its kernels and the gaps between them
     out = {
         "metric": f"{which} attention fwd+bwd ms/step", "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seed 1000 + config#)",
-        "config": info, "timed": "HIP graph replays of the captured fwd+bwd step",
+        "config": info,
+        "timed": "eager Python calls" if args.eager else "HIP graph replays of the captured fwd+bwd step",
         "eager_ms_per_step": round(eager_ms, 4),
         "kernel_ms_per_step": {k: round(v, 4) for k, v in kernel_ms.items()},
         "roofline": {"bound": "hbm", "achieved": round(bytes_alg / (dev_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM / 1e9,
@@ -952,6 +955,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="cfg3 / cfg4: time the eager Python calls instead of HIP graph replays")
     ap.add_argument("--storage", default="auto", choices=["auto", "register", "resident", "stream"],
                     help="where the Sinkhorn forward keeps the cost (flash_sinkhorn_attn storage=)")
     ap.add_argument("--workload", default="cfg2",
