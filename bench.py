@@ -603,7 +603,9 @@ def bench_attention(args, which):
         cur.wait_stream(side)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        # captured on the warm-up stream, whose cached workspace then exists: no
+        # allocation or zero fill is recorded into the graph
+        with torch.cuda.graph(graph, stream=side):
             step()
         graph.replay()
         torch.cuda.synchronize()
