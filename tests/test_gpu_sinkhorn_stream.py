@@ -185,7 +185,7 @@ def test_baseline_config5_full_size():
                             ("dQ", leaves[0].grad, gd["Q"]), ("dK", leaves[1].grad, gd["K"]),
                             ("dV", leaves[2].grad, gd["V"]), ("dG", leaves[3].grad, gd["G"]),
                             ("dlog_mu", lm.grad, gd["log_mu"]), ("dlog_nu", ln.grad, gd["log_nu"])):
-        errs[name] = float((got.float() - want).abs().max() / want.abs().max())
+        errs[name] = float((got.detach().float() - want).abs().max() / want.abs().max())
     print("[cfg5] max rel err vs dense fp32 checker: " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()),
           flush=True)
     for k, v in errs.items():
