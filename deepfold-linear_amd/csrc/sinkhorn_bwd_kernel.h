@@ -398,6 +398,35 @@ __device__ __forceinline__ bool gather_vector(const uint64_t* buf, int n, int Np
   return *s_flag == 0;
 }
 
+// Per-wave gather of the register-storage CG: the wave polls the words of its own
+// streamed tiles (wave + BWD_NW k, the tiles its slots of reg_wsum read) and writes
+// dst[i] (0 for a masked entry and for the last tile's entries i >= n), with no
+// barrier: each tile has one owner wave.  Returns false, uniformly over the wave, if
+// a wait expired (then the error has been raised).
+__device__ __forceinline__ bool gather_own_tiles(const uint64_t* buf, int n, int n_tiles, uint32_t tag, float* dst,
+                                                 const unsigned char* valid, ErrRef err) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int nwords = wave < n_tiles ? ((n_tiles - 1 - wave) / BWD_NW + 1) * 16 : 0;
+  bool ok = true;
+  for (int base = 0; base < nwords && ok; base += 2 * WAVE) {
+    int idx[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = base + k * WAVE + lane;
+      const int i = (wave + BWD_NW * (e >> 4)) * 16 + (e & 15);
+      idx[k] = (e < nwords && i < n) ? i : -1;
+      if (e < nwords && i >= n) dst[i] = 0.f;
+    }
+    ok = poll_words<2>(buf, idx, tag, err, [&](int k, uint64_t w) {
+      const int i = idx[k];
+      dst[i] = valid[i] ? __uint_as_float((uint32_t)(w >> 32)) : 0.f;
+    });
+    ok = wave_max_u32(ok ? 0u : 1u) == 0u;
+  }
+  return ok;
+}
+
 // gather_vector followed by block_sum(Np, f) in one barrier: every thread gathers the
 // entries i = t + k BWD_NT (the poll's assignment; the tail [n, Np) too), so after
 // its polls it already holds what f reads of dst and can sum f over its entries; the
@@ -1055,6 +1084,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       cr[i] = bj;
       cp[i] = bj;
       ctw[i] = 0.f;
+      ct[i] = 0.f;  // entries past the last tile are never gathered
     }
     __syncthreads();
     int flip = 0;
@@ -1065,15 +1095,22 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
     const bool early_exit = a.cg_rtol > 0.f;
     const float stop2 = a.cg_rtol * a.cg_rtol * rr;
     const float k2 = kappa * kappa;
-    // mv(true): lout = W p (my rows); mv(false): lout = W^T t (my columns)
-    auto cg_run = [&](auto&& mv) __attribute__((always_inline)) -> bool {
+    // mv(true): lout = W p (my rows); mv(false): lout = W^T t (my columns).  own_t: mv(false)
+    // reads t only on the wave's own streamed tiles (register storage), so each wave
+    // gathers just those; a failed wait sets the flag that the next gather's barrier
+    // turns into a uniform exit.
+    auto cg_run = [&](auto&& mv, bool own_t) __attribute__((always_inline)) -> bool {
     for (int it = 0; it < a.iters; ++it) {
       if (early_exit && (rr <= stop2 || rr == 0.f)) break;
       // t_i = sum_j W_ij p_j (my rows)
       mv(true);
       ++phase;
       for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += BWD_NT) xch_put(xA + i, lout[i - r_lo], salt | phase, local);
-      if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) return false;
+      if (own_t) {
+        if (!gather_own_tiles(xA, n, n_tiles, salt | phase, ct, valid, a.err)) sh.flag = 1;
+      } else if (!gather_vector(xA, n, Np, salt | phase, ct, valid, a.err, &sh.flag)) {
+        return false;
+      }
       // s_j = sum_i W_ij t_i (my cols)
       mv(false);
       ++phase;
@@ -1134,7 +1171,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
           return cg_run([&](bool row) __attribute__((always_inline)) {
             if (row) reg_wsum<KSL>(WR, n_tiles, nr, o_cp, o_out, o_scr);
             else reg_wsum<KSL>(WC, n_tiles, nr, o_ct, o_out, o_scr);
-          });
+          }, true);
         };
         if (ksg == 2) cg_ok = reg_cg(std::integral_constant<int, 2>{});
         else if (ksg == 4) cg_ok = reg_cg(std::integral_constant<int, 4>{});
@@ -1146,7 +1183,7 @@ __global__ void __launch_bounds__(BWD_NT) sinkhorn_bwd_kernel(SinkBwdArgs a) {
       cg_ok = cg_run([&](bool row) __attribute__((always_inline)) {
         if (row) wsum(true, be, cp, al + r_lo);
         else wsum(false, al, ct, be + r_lo);
-      });
+      }, false);
     if (!cg_ok) return;
     // z_v = D_c^{1/2} y, z_u = kappa D_r^{1/2} (W y)
     for (int i = threadIdx.x; i < Np; i += BWD_NT) {
