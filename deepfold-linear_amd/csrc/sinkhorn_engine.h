@@ -202,6 +202,9 @@ template <int W, typename Take>
 __device__ __forceinline__ bool poll_words(const uint64_t* buf, const int (&idx)[W], uint32_t tag, ErrRef err,
                                            Take take) {
   const uint32_t salt = tag >> 12;
+  // a limit of 1 (failure-path tests): the wait gives up at once, whatever has arrived,
+  // so the expiry does not depend on how early the words were published
+  if (err.spin_limit == 1u) { raise_error(err, salt, 2u); return false; }
   const uint64_t* addr[W];
   bool done[W];
 #pragma unroll

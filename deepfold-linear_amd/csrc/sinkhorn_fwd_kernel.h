@@ -655,6 +655,9 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
             if (in_c) xch_put(xu + ic, kappa * (lmu_c - l2 * LN2), tag, local);
             rpR[q] = split3(ok_c ? -l2 : 0.f);
           });
+          // the other waves start polling once the combining threads have published:
+          // earlier polls only load the L2 the publishing stores go through
+          lds_barrier();
           if (s_flagp[phase & 1]) return false;
           if (!agree_placement()) return false;
         }
@@ -675,6 +678,7 @@ __global__ void __launch_bounds__(FWD_NT) sinkhorn_fwd_kernel(SinkFwdArgs a) {
             rpC[q] = split3(ok_c ? -l2 : 0.f);
             if (last && ok_c) a.col_lse[bh * N + ic] = l2 * LN2;
           });
+          lds_barrier();  // as after the row combine
           if (s_flagp[phase & 1]) return false;
         }
       }

@@ -78,7 +78,8 @@ int dfl_get_launch_mode(void);
 /* For tests of the failure path only: the number of polls after which a
  * cross-workgroup wait gives up (0 restores the default of about 2-4 s).  A tiny
  * limit makes the persistent kernels' waits expire, so they report error 2 and exit
- * normally.  No counterpart in the reference.  Process-wide; returns 0. */
+ * normally; with 1 the exchange waits give up at their first poll, whatever has
+ * arrived.  No counterpart in the reference.  Process-wide; returns 0. */
 int dfl_debug_set_spin_limit(unsigned limit);
 
 /* ---------------------------------------------------------------------------

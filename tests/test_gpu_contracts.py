@@ -118,7 +118,7 @@ def test_expired_wait_is_reported_and_kernels_exit():
     good, _ = _layer(t, 30, grads=False)
     assert lib.dfl_pending_error() == 0
     try:
-        lib.dfl_debug_set_spin_limit(1)  # every wait gives up after its first check
+        lib.dfl_debug_set_spin_limit(1)  # every exchange wait gives up at once
         with pytest.raises(RuntimeError, match="error code 2|wait expired"):
             _layer(t, 30, grads=False)
         torch.cuda.synchronize()  # the kernels ended: the stream drains
